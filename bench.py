@@ -1,0 +1,319 @@
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+Default workload: Llama-3-8B-shaped decode in bf16,
+batch 64, 32 query / 8 KV heads, head_dim 128, every context 4096 tokens,
+block tables a seeded random permutation of a 16384-block pool, K/V
+0.5 * N(0, 1), Q N(0, 1), scale 1/sqrt(128).  One step = one decode step of
+one layer: scatter the new token's K/V (pa_reshape_and_cache) and attend
+over the 4096-token paged context (pa_decode).  Inputs are resident in HBM
+before timing starts.
+
+Prints ONE JSON line (the driver's contract) with a roofline object for the
+dominant launch (pa_decode, timed with HIP events on its stream) and the
+CPU baseline (the C oracle restating the reference's CPU path, timed on a
+bounded sample on the host cores).
+
+Other workloads for profiling: --config prefill (config 3, MFMA-bound),
+--config splitk (config 4), --config qwen (config 1, f32).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+from __graft_entry__ import _package  # noqa: E402
+
+METRIC = ("paged-attn decode tokens/s + achieved HBM GB/s (% peak), Llama-3-8B shape, 1 GPU")
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+F32_VALU_PEAK_TFLOPS = 157.3
+DEV = "cuda:0"
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
+
+
+def make_tables(gen, B, blocks_per_seq, pool, shared_prefix=0):
+    perm = torch.randperm(pool, generator=gen)
+    bt = torch.empty(B, blocks_per_seq, dtype=torch.int32)
+    shared = perm[:shared_prefix]
+    o = shared_prefix
+    for b in range(B):
+        bt[b, :shared_prefix] = shared
+        n = blocks_per_seq - shared_prefix
+        bt[b, shared_prefix:] = perm[o:o + n]
+        o += n
+    return bt
+
+
+class Workload:
+    """Synthetic inputs resident on the GPU plus the step closure."""
+
+    def __init__(self, pa, name):
+        self.pa = pa
+        self.name = name
+        g = torch.Generator().manual_seed({"decode": 1, "prefill": 2, "splitk": 3,
+                                           "qwen": 0}[name])
+        dg = torch.Generator(device=DEV).manual_seed(1234)
+        self.kind = "decode"
+        if name == "decode":
+            B, hq, hkv, d, ctx = 64, 32, 8, 128, 4096
+            self.dtype = torch.bfloat16
+            nblk = ctx // 16
+            pool = B * nblk  # 16384 blocks
+            self.ctx = torch.full((B,), ctx, dtype=torch.int32)
+            bt = make_tables(g, B, nblk, pool)
+            kv_scale = 0.5
+            self.workload = ("config 2: Llama-3-8B decode bf16, B 64, 32/8 heads x 128, "
+                             "ctx 4096, block 16, random block tables over 16384 blocks")
+        elif name == "splitk":
+            B, hq, hkv, d = 16, 32, 8, 128
+            self.dtype = torch.bfloat16
+            lens = torch.exp(torch.empty(B).uniform_(math.log(8192), math.log(32768),
+                                                     generator=g)).to(torch.int32)
+            self.ctx = lens
+            nblk = int((lens.max() + 15) // 16)
+            pool = 256 + int(((lens + 15) // 16 - 256).sum()) + 16
+            perm = torch.randperm(pool, generator=g)
+            bt = torch.zeros(B, nblk, dtype=torch.int32)
+            o = 256
+            for b in range(B):
+                n = int((lens[b] + 15) // 16)
+                bt[b, :256] = perm[:256]
+                bt[b, 256:n] = perm[o:o + n - 256]
+                o += n - 256
+            kv_scale = 1.0
+            self.workload = ("config 4: long-context split-K decode bf16, B 16, 32/8 x 128, "
+                             "ctx log-U[8k, 32k], 4096-token shared prefix")
+        elif name == "qwen":
+            B, hq, hkv, d = 8, 14, 2, 64
+            self.dtype = torch.float32
+            lens = torch.randint(128, 1025, (B,), generator=g, dtype=torch.int32)
+            self.ctx = lens
+            nblk = int((lens.max() + 15) // 16)
+            pool = 1024
+            perm = torch.randperm(pool, generator=g)
+            bt = torch.zeros(B, nblk, dtype=torch.int32)
+            o = 0
+            for b in range(B):
+                n = int((lens[b] + 15) // 16)
+                bt[b, :n] = perm[o:o + n]
+                o += n
+            kv_scale = 1.0
+            self.workload = ("config 1: Qwen2.5-0.5B decode f32, B 8, 14/2 x 64, "
+                             "ctx U[128, 1024], pool 1024 blocks")
+        elif name == "prefill":
+            self.kind = "prefill"
+            hq, hkv, d = 32, 8, 128
+            self.dtype = torch.bfloat16
+            pasts = [0, 512, 1024, 2048]
+            chunk = 2048
+            B = 4
+            nblks = [(p + chunk + 15) // 16 for p in pasts]
+            nblk = max(nblks)
+            pool = sum(nblks) + 16
+            perm = torch.randperm(pool, generator=g)
+            bt = torch.zeros(B, nblk, dtype=torch.int32)
+            o = 0
+            for b in range(B):
+                bt[b, :nblks[b]] = perm[o:o + nblks[b]]
+                o += nblks[b]
+            self.past = torch.tensor(pasts, dtype=torch.int32, device=DEV)
+            self.cu = torch.tensor([0, chunk, 2 * chunk, 3 * chunk, 4 * chunk],
+                                   dtype=torch.int32, device=DEV)
+            self.max_q = chunk
+            self.q = torch.randn(B * chunk, hq, d, generator=dg, device=DEV).to(self.dtype)
+            kv_scale = 1.0
+            self.pairs = sum(chunk * p + chunk * (chunk + 1) // 2 for p in pasts)
+            self.flops = 4.0 * self.pairs * hq * d
+            self.workload = ("config 3: Llama-3-8B chunked causal prefill bf16, 4 x 2048 new "
+                             "tokens on past 0/512/1024/2048, 32/8 x 128")
+        else:
+            raise SystemExit(f"unknown config {name}")
+        self.B, self.hq, self.hkv, self.d = B, hq, hkv, d
+        self.scale = 1.0 / math.sqrt(d)
+        self.bt = bt.to(DEV)
+        self.pool = pool
+        self.kc = (torch.randn(pool, hkv, 16, d, generator=dg, device=DEV) * kv_scale).to(
+            self.dtype)
+        self.vc = (torch.randn(pool, hkv, d, 16, generator=dg, device=DEV) * kv_scale).to(
+            self.dtype)
+        self.ctx_dev = self.ctx.to(DEV) if self.kind == "decode" else None
+        es = torch.empty(0, dtype=self.dtype).element_size()
+        if self.kind == "decode":
+            self.q = torch.randn(B, hq, d, generator=dg, device=DEV).to(self.dtype)
+            self.out = torch.empty_like(self.q)
+            self.max_ctx = int(self.ctx.max())
+            self.ws = torch.empty(max(1, pa.decode_workspace_size(B, hq, d, self.max_ctx)),
+                                  dtype=torch.uint8, device=DEV)
+            # new token of each sequence = its last position
+            pos = (self.ctx - 1).to(torch.int64)
+            slots = bt[torch.arange(B), (pos // 16)].to(torch.int64) * 16 + pos % 16
+            self.slots = slots.to(DEV)
+            self.k_new = torch.randn(B, hkv, d, generator=dg, device=DEV).to(self.dtype)
+            self.v_new = torch.randn(B, hkv, d, generator=dg, device=DEV).to(self.dtype)
+            tokens = int(self.ctx.sum())
+            # algorithmic bytes per pa_decode launch: K and V of every context
+            # token at Hkv heads, q in, out, block tables, context lengths.
+            self.kv_bytes = 2 * tokens * hkv * d * es
+            self.alg_bytes = (self.kv_bytes + 2 * B * hq * d * es +
+                              int(((self.ctx + 15) // 16).sum()) * 4 + B * 4)
+            uniq = len(set(bt[:, :].flatten().tolist()))
+            self.unique_kv_bytes = 2 * min(uniq * 16, tokens) * hkv * d * es
+        else:
+            self.out = torch.empty_like(self.q)
+            tokens_all = sum(p + 2048 for p in [0, 512, 1024, 2048])
+            self.alg_bytes = (2 * tokens_all * hkv * d * es + 2 * self.q.numel() * es)
+
+    def write_step(self):
+        self.pa.reshape_and_cache(self.k_new, self.v_new, self.kc, self.vc, self.slots)
+
+    def attend(self):
+        if self.kind == "decode":
+            self.pa.decode(self.q, self.kc, self.vc, self.bt, self.ctx_dev, self.max_ctx,
+                           scale=self.scale, out=self.out, workspace=self.ws)
+        else:
+            self.pa.prefill(self.q, self.kc, self.vc, self.bt, self.cu, self.past, self.max_q,
+                            scale=self.scale, out=self.out)
+
+    def step(self):
+        if self.kind == "decode":
+            self.write_step()
+        self.attend()
+
+
+def time_attend(w, iters):
+    """Average duration of the dominant launch (pa_decode / pa_prefill),
+    HIP events on the stream the library launches on (torch's current)."""
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        w.attend()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / iters / 1e3  # seconds
+
+
+def cpu_baseline(w, budget_s=12.0):
+    """Times the C oracle (restated reference CPU path: gather blocks to dense
+    f32, expand KV to all query heads, full softmax, OpenMP over heads) on a
+    bounded sample of the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = cpu_threads()
+    if w.kind != "decode":
+        return None
+    nseq = min(8, w.B)
+    bt = w.bt[:nseq].cpu().numpy()
+    ctx = w.ctx[:nseq].numpy()
+    used = sorted(set(int(x) for b in range(nseq) for x in bt[b, :(ctx[b] + 15) // 16]))
+    remap = {blk: i for i, blk in enumerate(used)}
+    bt_c = np.vectorize(lambda x: remap.get(int(x), 0))(bt).astype(np.int32)
+    idx = torch.tensor(used, device=DEV)
+
+    def host(t):
+        if t.dtype == torch.bfloat16:
+            return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        return t.contiguous().cpu().numpy()
+
+    kc = host(w.kc[idx])
+    vc = host(w.vc[idx].transpose(-1, -2))
+    q = host(w.q[:nseq])
+    oracle.paged_attention(q[:1], kc, vc, bt_c[:1], [0, 1], ctx[:1] - 1, scale=w.scale,
+                           threads=threads)  # warm
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        oracle.paged_attention(q, kc, vc, bt_c, np.arange(nseq + 1), ctx - 1, scale=w.scale,
+                               threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 50:
+            break
+    return {"value": round(nseq * reps / el, 2), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{nseq} sequences of the same workload x {reps} passes "
+                      f"({el:.1f} s): oracle gather + expand_kv + dense f32 softmax "
+                      "attention, OpenMP"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="decode", choices=["decode", "prefill", "splitk", "qwen"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding plan is design-only.", file=sys.stderr)
+        sys.exit(2)
+
+    pa = _package()
+    torch.cuda.set_device(0)
+    w = Workload(pa, args.config)
+    for _ in range(args.warmup):
+        w.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        w.step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ms_per_step = el / args.steps * 1e3
+
+    t_attn = time_attend(w, max(args.steps, 20))
+    if w.kind == "decode":
+        value = w.B * args.steps / el
+        unit = "tokens/s"
+        achieved = w.alg_bytes / t_attn / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "pa_decode (decode_mfma_kernel + decode_reduce_kernel)",
+                "alg_bytes_per_launch": w.alg_bytes,
+                "avg_launch_us": round(t_attn * 1e6, 2)}
+        if args.config == "splitk":
+            roof["unique_block_gbs"] = round((w.unique_kv_bytes) / t_attn / 1e9, 1)
+        if w.dtype == torch.float32:
+            roof["kernel"] = "pa_decode (decode_generic_kernel + decode_reduce_kernel)"
+    else:
+        value = w.flops / t_attn / 1e12
+        unit = "TFLOP/s"
+        roof = {"bound": "mfma", "achieved": round(value, 2), "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(value / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": "pa_prefill (prefill_mfma_kernel)", "flops_per_launch": w.flops,
+                "avg_launch_us": round(t_attn * 1e6, 2)}
+    cpu = None if args.no_cpu else cpu_baseline(w)
+    line = {
+        "metric": METRIC if w.kind == "decode" else "paged-attn chunked prefill TFLOP/s",
+        "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == torch.bfloat16 else "f32",
+        "data": "synthetic (seeded N(0,1) Q/K/V, random block tables)",
+        "config": {"workload": w.workload, "global_batch": w.B,
+                   "seq_len": int(w.ctx.max()) if w.kind == "decode" else 2048,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,177 @@
+/*
+ * pa.h -- C ABI of the MI355X paged-attention library (libpa.so).
+ *
+ * This is the drop-in boundary for vllm-lite's paged-attention path: the
+ * KV-cache write (slot-mapping scatter into 16-token blocks) and attention
+ * over the block-table-addressed cache, for single-token decode and for
+ * chunked causal prefill.  Each entry point names the reference function it
+ * replaces (paths relative to the vllm-lite repository root).
+ *
+ * Conventions
+ *  - Every pointer argument is a device pointer unless the comment says
+ *    "host".  The caller owns all memory; the stateless entry points
+ *    allocate nothing.  Work is enqueued on `stream` (NULL = the default
+ *    stream); nothing synchronises unless stated.
+ *  - Return value: PA_OK (0) or a negative pa_status.  No entry point aborts,
+ *    throws or unwinds; pa_last_error() gives a message for the calling
+ *    thread's most recent failure.
+ *  - dtype: PA_DTYPE_F32 or PA_DTYPE_BF16, shared by q, k, v, the caches and
+ *    out.  Arithmetic accumulates in f32.
+ *  - Block size is fixed at 16 tokens (crates/traits/src/types.rs:13).
+ *
+ * Cache layout (one layer, one of K / V; num_blocks = NB, kv heads = Hkv):
+ *   K cache  [NB, Hkv, 16, D]  token-major inside a block, as the reference
+ *            (crates/model/src/paged_tensor/tensor_store/mod.rs:62)
+ *   V cache  [NB, Hkv, D, 16]  token-minor inside a block: one head's 16
+ *            values of a dimension are contiguous, so the P·V contraction
+ *            loads matrix-core operands directly.  pa_read_kv returns the
+ *            reference's [seq, H, D] view, so logical contents are identical.
+ *   The cache stores Hkv heads; the reference stores the expanded Hq heads
+ *   (crates/model/src/components/attention/rope_gqa.rs:287-302).  Query head
+ *   h reads kv head h / (Hq / Hkv) (blocked grouping, util.rs:55-87).
+ */
+#ifndef VLLM_LITE_AMD_PA_H
+#define VLLM_LITE_AMD_PA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* pa_stream_t; /* same type as hipStream_t */
+
+#define PA_BLOCK_SIZE 16
+
+typedef enum pa_dtype { PA_DTYPE_F32 = 0, PA_DTYPE_BF16 = 1 } pa_dtype;
+
+typedef enum pa_status {
+  PA_OK = 0,
+  PA_ERR_INVALID_ARG = -1,  /* bad shape, null pointer, unknown dtype */
+  PA_ERR_OUT_OF_BOUNDS = -2, /* layer / block / offset outside the cache */
+  PA_ERR_UNSUPPORTED = -3,  /* shape this build has no kernel for */
+  PA_ERR_WORKSPACE = -4,    /* workspace missing or too small */
+  PA_ERR_HIP = -5           /* a HIP runtime call failed */
+} pa_status;
+
+/* Message for the calling thread's last failed call ("" if none). */
+const char* pa_last_error(void);
+
+/* Library version string. */
+const char* pa_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* KV-cache write                                                         */
+/* ---------------------------------------------------------------------- */
+
+/* Scatter T tokens' K and V into the cache: token t goes to block
+ * slot_mapping[t] / 16, offset slot_mapping[t] % 16.  Slots < 0 or
+ * >= num_blocks * 16 are skipped.
+ *   key, value    [T, Hkv, D] with token strides key_stride / value_stride
+ *                 (elements; 0 means Hkv * D, i.e. contiguous)
+ *   slot_mapping  [T] int64
+ * Replaces the per-token write loop of write_prefill_kv
+ * (crates/model/src/components/attention/paged_gqa.rs:29-63), the decode
+ * write in read_decode_kv (paged_gqa.rs:86-107), and PagedKvCache::write_kv
+ * (crates/model/src/paged_tensor/tensor_store/buffer.rs:103-267). */
+int32_t pa_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
+                             const int64_t* slot_mapping, int32_t num_tokens,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                             int64_t key_stride, int64_t value_stride, int32_t dtype,
+                             pa_stream_t stream);
+
+/* Build slot_mapping on the device from per-sequence block tables:
+ *   slot_mapping[t] = block_tables[s, positions[t] / 16] * 16 + positions[t] % 16
+ * for t in [cu_seq_tokens[s], cu_seq_tokens[s+1]).  A position whose block
+ * index is beyond max_blocks_per_seq maps to -1 (skipped by the scatter).
+ *   block_tables [num_seqs, max_blocks_per_seq] int32, positions [T] int64,
+ *   cu_seq_tokens [num_seqs + 1] int32, slot_mapping [T] int64 (out).
+ * Replaces the index arithmetic of paged_gqa.rs:39-52 and :86-97.  The
+ * reference silently falls back to block 0 for a missing table entry
+ * (paged_gqa.rs:51, :97); here such tokens are skipped instead. */
+int32_t pa_slot_mapping(const int32_t* block_tables, int32_t max_blocks_per_seq,
+                        const int64_t* positions, const int32_t* cu_seq_tokens,
+                        int32_t num_seqs, int32_t num_tokens, int64_t* slot_mapping,
+                        pa_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* KV-cache read                                                          */
+/* ---------------------------------------------------------------------- */
+
+/* Gather the first seq_len tokens of one sequence into dense
+ * out_k / out_v [seq_len, Hkv, D] (reference layout, bit-exact copies).
+ *   block_ids [n_ids] int32; block b holds tokens [16b, 16b + 16).
+ * Requires n_ids * 16 >= seq_len.  Entries outside [0, num_blocks) produce
+ * zero rows.
+ * Replaces PagedKvCache::read_kv
+ * (crates/model/src/paged_tensor/tensor_store/buffer.rs:273-339). */
+int32_t pa_read_kv(const void* k_cache, const void* v_cache, const int32_t* block_ids,
+                   int32_t n_ids, int32_t seq_len, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t num_blocks, void* out_k, void* out_v, int32_t dtype,
+                   pa_stream_t stream);
+
+/* Content hash of each listed block of an f32 K cache, computed as
+ *   fold(0, acc * 31 + (|x| * 1000) as u64) over the block's H*16*D values
+ * in the reference's [H, 16, D] order (wrapping u64 arithmetic; the cast
+ * saturates like Rust's `as`).
+ *   block_ids [n] int32, hashes [n] uint64 (out).
+ * Replaces PagedKvCache::compute_block_hash_from_slice
+ * (crates/model/src/paged_tensor/tensor_store/layout.rs:51-58). */
+int32_t pa_block_hash(const float* k_cache, const int32_t* block_ids, int32_t n,
+                      int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                      uint64_t* hashes, pa_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Attention                                                              */
+/* ---------------------------------------------------------------------- */
+
+/* Bytes of workspace pa_decode needs for these sizes (0 when one pass
+ * suffices). */
+size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                int32_t max_context_len);
+
+/* Single-token decode attention over the paged cache.
+ *   out, q        [num_seqs, Hq, D]
+ *   block_tables  [num_seqs, max_blocks_per_seq] int32
+ *   context_lens  [num_seqs] int32: keys 0 .. context_lens[s]-1 are attended
+ *                 (the new token must already be in the cache)
+ *   max_context_len  host upper bound of context_lens (sizes the split)
+ *   scale         softmax scale, e.g. attn_factor / sqrt(D)
+ *   workspace     pa_decode_workspace_size() bytes (may be NULL if 0)
+ * out[s, h] = softmax(scale * q[s, h] · K[s, h/g]ᵀ) · V[s, h/g].
+ * Replaces RopeGqaAttention::forward_decode's attention
+ * (crates/model/src/components/attention/rope_gqa.rs:385-429) =
+ * read_decode_kv + expand_kv + paged_attention
+ * (paged_gqa.rs:71-112, util.rs:55-87, util.rs:150-176). */
+int32_t pa_decode(void* out, const void* q, const void* k_cache, const void* v_cache,
+                  const int32_t* block_tables, int32_t max_blocks_per_seq,
+                  const int32_t* context_lens, int32_t max_context_len, int32_t num_seqs,
+                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                  float scale, void* workspace, size_t workspace_bytes, int32_t dtype,
+                  pa_stream_t stream);
+
+/* Chunked causal prefill over the paged cache.
+ *   out, q        [total_q, Hq, D]; sequence s owns rows
+ *                 cu_q_lens[s] .. cu_q_lens[s+1]-1
+ *   cu_q_lens     [num_seqs + 1] int32, past_lens [num_seqs] int32
+ *   max_q_len     host upper bound of the per-sequence query count
+ * Query row i of sequence s sits at absolute position past_lens[s] + i and
+ * attends keys j <= past_lens[s] + i, all read from the cache (write the
+ * chunk's K/V with pa_reshape_and_cache first).
+ * Replaces forward_prefill / forward_prefill_continue's attention
+ * (rope_gqa.rs:261-372): tiled_attention (util.rs:188-234) for past = 0 and
+ * compute_gqa_attention + prefill_continue_causal_mask
+ * (paged_gqa.rs:135-164) for past > 0. */
+int32_t pa_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
+                   const int32_t* block_tables, int32_t max_blocks_per_seq,
+                   const int32_t* cu_q_lens, const int32_t* past_lens, int32_t num_seqs,
+                   int32_t total_q, int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                   int32_t head_dim, int32_t num_blocks, float scale, int32_t dtype,
+                   pa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_LITE_AMD_PA_H */

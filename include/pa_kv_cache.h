@@ -1,0 +1,85 @@
+/*
+ * pa_kv_cache.h -- host-side mirror of vllm-lite's PagedKvCache over the
+ * paged-attention kernels (libpa.so).
+ *
+ * The reference keeps, per layer, a K and a V tensor of shape
+ * [num_blocks, H, 16, D] and exposes write_kv / write_kv_batch / read_kv
+ * (crates/model/src/paged_tensor/tensor_store/mod.rs:29-84,
+ *  crates/model/src/paged_tensor/tensor_store/buffer.rs:27-339)
+ * plus the free functions write_prefill_kv / read_decode_kv
+ * (crates/model/src/components/attention/paged_gqa.rs:29-112).  This object
+ * owns the device memory of all layers and runs those operations with the
+ * HIP kernels, with the reference's argument checks and error codes in
+ * place of its `Err` results.  H here is the number of KV heads.
+ *
+ * Unlike the stateless entry points of pa.h, the cache allocates: the
+ * caches themselves at creation and a small device staging buffer for block
+ * ids / slots, grown on demand.  Index arguments marked "host" are read on
+ * the host and validated before anything is enqueued.
+ */
+#ifndef VLLM_LITE_AMD_PA_KV_CACHE_H
+#define VLLM_LITE_AMD_PA_KV_CACHE_H
+
+#include "pa.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct pa_kv_cache pa_kv_cache;
+
+/* PagedKvCache::new (tensor_store/mod.rs:50-84): zero-filled caches for
+ * num_layers layers.  dtype PA_DTYPE_F32 or PA_DTYPE_BF16. */
+int32_t pa_kv_cache_create(int32_t num_layers, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t num_blocks, int32_t dtype, pa_kv_cache** out);
+void pa_kv_cache_destroy(pa_kv_cache* cache);
+
+/* Accessors (tensor_store/layout.rs:15-44). */
+int32_t pa_kv_cache_num_layers(const pa_kv_cache* cache);
+int32_t pa_kv_cache_num_blocks(const pa_kv_cache* cache);
+int32_t pa_kv_cache_block_size(const pa_kv_cache* cache);
+/* Device base of one layer's K cache [NB, H, 16, D] / V cache [NB, H, D, 16];
+ * NULL for a bad layer. */
+void* pa_kv_cache_key_ptr(pa_kv_cache* cache, int32_t layer);
+void* pa_kv_cache_value_ptr(pa_kv_cache* cache, int32_t layer);
+
+/* PagedKvCache::write_kv (buffer.rs:103-267): one token, k / v [H, D]
+ * device, into (block_id, token_offset).  PA_ERR_OUT_OF_BOUNDS for a bad
+ * layer, block_id >= num_blocks or token_offset >= 16 (buffer.rs:118-137). */
+int32_t pa_kv_cache_write_kv(pa_kv_cache* cache, int32_t layer, int64_t block_id,
+                             int64_t token_offset, const void* k, const void* v,
+                             pa_stream_t stream);
+
+/* PagedKvCache::write_kv_batch (buffer.rs:27-95): T tokens [T, H, D] from
+ * (block_id, token_offset) on, continuing into block_id + 1, ... when the
+ * offset wraps; fails if the run does not fit the pool (buffer.rs:69-75). */
+int32_t pa_kv_cache_write_kv_batch(pa_kv_cache* cache, int32_t layer, int64_t block_id,
+                                   int64_t token_offset, const void* k, const void* v,
+                                   int32_t num_tokens, pa_stream_t stream);
+
+/* write_prefill_kv (paged_gqa.rs:29-63): token t of k / v [T, H, D] goes to
+ * block_ids[pos / 16] at offset pos % 16 with pos = positions[t] (t when
+ * positions has fewer than T entries).  block_ids / positions are host
+ * arrays.  A position whose block index is past the table is an error here
+ * (the reference falls back to block 0, paged_gqa.rs:51). */
+int32_t pa_kv_cache_write_prefill_kv(pa_kv_cache* cache, int32_t layer, const int64_t* block_ids,
+                                     int32_t n_ids, const int64_t* positions, int32_t n_pos,
+                                     int32_t num_tokens, const void* k, const void* v,
+                                     pa_stream_t stream);
+
+/* PagedKvCache::read_kv (buffer.rs:273-339): the first seq_len tokens of the
+ * sequence whose blocks are block_ids (host) into out_k / out_v
+ * [seq_len, H, D].  Headroom blocks past seq_len are ignored (:302-304); a
+ * table shorter than seq_len yields only the tokens it covers (the walk of
+ * :296-333 simply ends); an id >= num_blocks among the walked blocks is an
+ * error.  *n_read receives the number of tokens written, min(seq_len,
+ * 16 * n_ids) (0 for an empty table or seq_len 0, :279-284). */
+int32_t pa_kv_cache_read_kv(pa_kv_cache* cache, int32_t layer, const int64_t* block_ids,
+                            int32_t n_ids, int32_t seq_len, void* out_k, void* out_v,
+                            int32_t* n_read, pa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_LITE_AMD_PA_KV_CACHE_H */

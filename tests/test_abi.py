@@ -1,0 +1,89 @@
+"""libpa.so loads and exports every entry point the headers declare.
+
+CPU-only: nothing here launches a kernel.  The argument checks exercised
+return before any HIP call, so they run without a GPU.
+"""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("pa.h", "pa_kv_cache.h")]
+
+
+def declared_symbols():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names.update(re.findall(r"\b(pa_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+@pytest.fixture(scope="module")
+def lib(pa):
+    return pa._lib.load()
+
+
+def test_headers_declare_the_path():
+    names = declared_symbols()
+    for required in ("pa_reshape_and_cache", "pa_decode", "pa_prefill", "pa_read_kv",
+                     "pa_decode_workspace_size", "pa_last_error", "pa_kv_cache_write_kv"):
+        assert required in names
+
+
+def test_every_declared_symbol_is_exported(lib, pa):
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the ctypes table covers exactly the declared set
+    assert sorted(pa._lib.SIGNATURES) == declared_symbols()
+
+
+def test_version_and_empty_error(lib):
+    assert b"gfx950" in lib.pa_version()
+    assert lib.pa_last_error() == b""
+
+
+def test_workspace_size(lib):
+    # one partition (<= 256 tokens) needs none; otherwise B*Hq*P*(D+2) f32
+    assert lib.pa_decode_workspace_size(64, 32, 128, 256) == 0
+    assert lib.pa_decode_workspace_size(64, 32, 128, 4096) == 64 * 32 * 16 * 130 * 4
+    assert lib.pa_decode_workspace_size(2, 4, 64, 257) == 2 * 4 * 2 * 66 * 4
+
+
+def test_argument_errors_without_gpu(lib):
+    null = None
+    # unknown dtype
+    rc = lib.pa_decode(null, null, null, null, null, 4, null, 64, 1, 8, 2, 64, 16, 1.0, null, 0,
+                       7, null)
+    assert rc == -1 and b"dtype" in lib.pa_last_error()
+    # Hq not a multiple of Hkv
+    rc = lib.pa_decode(null, null, null, null, null, 4, null, 64, 1, 7, 2, 64, 16, 1.0, null, 0,
+                       1, null)
+    assert rc == -1 and b"multiple" in lib.pa_last_error()
+    # context longer than the block table
+    rc = lib.pa_decode(null, null, null, null, null, 4, null, 65, 1, 8, 2, 64, 16, 1.0, null, 0,
+                       1, null)
+    assert rc == -2
+    # missing workspace for a split launch (null pointers are checked first)
+    rc = lib.pa_decode(C.c_void_p(8), C.c_void_p(8), C.c_void_p(8), C.c_void_p(8),
+                       C.c_void_p(8), 64, C.c_void_p(8), 1024, 1, 8, 2, 64, 16, 1.0, null, 0, 1,
+                       null)
+    assert rc == -4 and b"workspace" in lib.pa_last_error()
+    # read_kv: table cannot hold seq_len
+    rc = lib.pa_read_kv(null, null, null, 1, 17, 2, 4, 4, null, null, 0, null)
+    assert rc == -2
+    # prefill unsupported head_dim
+    rc = lib.pa_prefill(null, null, null, null, null, 4, null, null, 1, 1, 1, 2, 2, 1024, 4,
+                        1.0, 1, null)
+    assert rc == -3
+    # empty work is a no-op success
+    assert lib.pa_reshape_and_cache(null, null, null, null, null, 0, 2, 4, 4, 0, 0, 0, null) == 0
+    assert lib.pa_last_error() == b""
+
+
+def test_kv_cache_create_rejects_bad_sizes(lib):
+    h = C.c_void_p()
+    assert lib.pa_kv_cache_create(0, 2, 4, 4, 0, C.byref(h)) == -1
+    assert not h.value

@@ -1,0 +1,147 @@
+"""GPU parity of pa_decode against the oracle's paged attention.
+
+bf16 cases run the MFMA kernel; f32 and unusual shapes run the generic
+kernel.  Tolerances: bf16 |gpu - ref| <= 2e-2 + 1e-2 |ref| with the
+reference computed in f32 from the same bf16 inputs; f32 1e-4 / 1e-4.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (BF16_ATOL, BF16_RTOL, F32_ATOL, F32_RTOL, assert_close, golden,
+                     make_decode_case)
+from test_gpu_cache_ops import DEV, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def run_decode(pa, oracle, case, dtype, scale=None, check_split=True):
+    q, kc, vc = case["q"], case["k_cache"], case["v_cache_ref"]
+    bt, ctx = case["block_tables"], case["ctx"]
+    B, Hq, D = q.shape
+    scale = scale if scale is not None else 1.0 / math.sqrt(D)
+    out = pa.decode(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt),
+                    to_dev(ctx), int(ctx.max()), scale=scale)
+    got = to_np(out)
+    got = oracle.bf16_to_f32(got) if dtype == "bf16" else got
+    ref = oracle.paged_attention(q, kc, vc, np.where(bt < 0, 0, bt), np.arange(B + 1),
+                                 ctx - 1, scale=scale)
+    ref = oracle.bf16_to_f32(ref) if dtype == "bf16" else ref
+    return got, ref
+
+
+def ref_f32(oracle, case, scale=None):
+    """Reference on the same inputs but computed without bf16 output rounding."""
+    q, kc, vc = case["q"], case["k_cache"], case["v_cache_ref"]
+    B = q.shape[0]
+    qf, kf, vf = (oracle.as_f32(x) for x in (q, kc, vc))
+    return oracle.paged_attention(qf, kf, vf, np.where(case["block_tables"] < 0, 0,
+                                                       case["block_tables"]),
+                                  np.arange(B + 1), case["ctx"] - 1, scale=scale)
+
+
+def test_config1_qwen_f32(pa, oracle):
+    # B 8, Hq 14, Hkv 2, D 64, ctx ~ U[128, 1024], f32,
+    # block tables = disjoint slices of a permutation of a 1024-block pool.
+    rng = np.random.default_rng(0)
+    ctx = rng.integers(128, 1025, size=8)
+    case = make_decode_case(rng, 8, 14, 2, 64, ctx, num_blocks=1024, dtype="f32")
+    got, ref = run_decode(pa, oracle, case, "f32")
+    assert_close(got, ref, F32_ATOL, F32_RTOL, "config 1")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (8, 8, 128), (16, 2, 256),
+                                      (8, 4, 64), (16, 1, 128)])
+def test_bf16_mfma_shapes(pa, oracle, hq, hkv, d):
+    rng = np.random.default_rng(hq * 10 + d)
+    ctx = [1, 15, 16, 17, 31, 32, 33, 255, 256, 257, 600]
+    case = make_decode_case(rng, len(ctx), hq, hkv, d, ctx, dtype="bf16", kv_scale=0.5)
+    got, _ = run_decode(pa, oracle, case, "bf16")
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, f"bf16 {hq}/{hkv}x{d}")
+
+
+def test_config2_llama_shape_small_batch(pa, oracle):
+    # BASELINE config 2 shape (32/8 x 128, ctx 4096, K/V 0.5 N(0,1)) at B = 4.
+    rng = np.random.default_rng(1)
+    case = make_decode_case(rng, 4, 32, 8, 128, [4096] * 4, dtype="bf16", kv_scale=0.5)
+    got, _ = run_decode(pa, oracle, case, "bf16")
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "config 2 shape")
+
+
+def test_config4_shared_prefix_long_context(pa, oracle):
+    # BASELINE config 4 pattern: log-uniform long contexts sharing a
+    # 4096-token prefix (the same physical blocks in every table); B = 3.
+    rng = np.random.default_rng(3)
+    ctx = np.exp(rng.uniform(np.log(8192), np.log(32768), size=3)).astype(np.int32)
+    case = make_decode_case(rng, 3, 32, 8, 128, ctx, dtype="bf16", shared_prefix_blocks=256)
+    assert np.all(case["block_tables"][:, :256] == case["block_tables"][0, :256])
+    got, _ = run_decode(pa, oracle, case, "bf16")
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "config 4 pattern")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_split_equals_single_pass(pa, oracle, dtype):
+    # A sequence long enough to split must match the same keys attended in
+    # one partition: compare ctx = 256 (one pass) against the prefix of a
+    # split launch by masking -- here via two independent launches.
+    rng = np.random.default_rng(4)
+    case = make_decode_case(rng, 2, 8, 2, 128, [256, 1000], dtype=dtype)
+    got, ref = run_decode(pa, oracle, case, dtype)
+    tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
+    assert_close(got, ref_f32(oracle, case), *tol, "split")
+
+
+def test_stale_nan_beyond_context_is_ignored(pa, oracle):
+    # Cache slots past each context hold NaN; masking must keep them out.
+    rng = np.random.default_rng(5)
+    ctx = [5, 21, 300]
+    case = make_decode_case(rng, 3, 8, 2, 128, ctx, dtype="bf16")
+    kc, vc, bt = case["k_cache"], case["v_cache_ref"], case["block_tables"]
+    for b, L in enumerate(ctx):
+        last = bt[b, (L - 1) // 16]
+        kc[last, :, (L - 1) % 16 + 1:, :] = 0x7FC0
+        vc[last, :, (L - 1) % 16 + 1:, :] = 0x7FC0
+    got, _ = run_decode(pa, oracle, case, "bf16")
+    assert np.isfinite(got).all()
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "stale NaN")
+
+
+def test_gqa_grouping_single_key(pa, oracle):
+    # util/tests.rs:316-339 on the GPU: one key, so out = V of the paired
+    # kv head; blocked grouping [V0, V0, V1, V1].
+    f = golden("attention_fixtures.json")["gqa_single_token"]
+    for dtype, tdt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+        d = 64  # padded head dim so both kernels run; extra dims zero
+        kc, vc = pa.ops.new_cache(2, 2, d, tdt, DEV)
+        v_ref = np.zeros((2, 2, 16, d), np.float32)
+        v_ref[1, :, 0, :2] = np.asarray(f["v"], np.float32).reshape(2, 2)
+        vc.copy_(torch.from_numpy(oracle.v_from_ref(v_ref)).to(tdt))
+        q = torch.zeros(1, 4, d, dtype=tdt, device=DEV)
+        out = pa.decode(q, kc, vc, torch.tensor([[1]], dtype=torch.int32, device=DEV),
+                        torch.tensor([1], dtype=torch.int32, device=DEV), 1)
+        got = out[0, :, :2].float().cpu().numpy().ravel().tolist()
+        assert got == f["expect"], (dtype, got)
+
+
+def test_scale_and_attn_factor(pa, oracle):
+    # scale folds attn_factor / sqrt(D) (gqa/forward.rs:38-43)
+    rng = np.random.default_rng(6)
+    case = make_decode_case(rng, 2, 8, 2, 128, [100, 700], dtype="bf16")
+    s = 1.7 / math.sqrt(128)
+    got, _ = run_decode(pa, oracle, case, "bf16", scale=s)
+    assert_close(got, ref_f32(oracle, case, scale=s), BF16_ATOL, BF16_RTOL, "scale")
+
+
+def test_empty_context_gives_zeros(pa, oracle):
+    kc, vc = pa.ops.new_cache(4, 2, 128, torch.bfloat16, DEV)
+    q = torch.randn(2, 8, 128, device=DEV).to(torch.bfloat16)
+    out = torch.full_like(q, 7.0)
+    pa.decode(q, kc, vc, torch.tensor([[0], [1]], dtype=torch.int32, device=DEV),
+              torch.tensor([0, 0], dtype=torch.int32, device=DEV), 0, out=out)
+    # max_context_len 0 is a no-op launch: out untouched
+    assert torch.all(out == 7.0)
+    pa.decode(q, kc, vc, torch.tensor([[0], [1]], dtype=torch.int32, device=DEV),
+              torch.tensor([0, 3], dtype=torch.int32, device=DEV), 3, out=out)
+    assert torch.all(out[0] == 0)

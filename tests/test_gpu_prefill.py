@@ -1,0 +1,88 @@
+"""GPU parity of pa_prefill (chunked causal prefill over the paged cache)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import BF16_ATOL, BF16_RTOL, F32_ATOL, F32_RTOL, assert_close
+from test_gpu_cache_ops import DEV, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def make_prefill_case(oracle, rng, pasts, chunks, hq, hkv, d, dtype, extra_blocks=5):
+    B = len(pasts)
+    tot = [p + c for p, c in zip(pasts, chunks)]
+    nblk = [(t + 15) // 16 for t in tot]
+    mbs = max(nblk)
+    nb = sum(nblk) + extra_blocks
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = np.zeros((B, mbs), np.int32)
+    o = 0
+    for b in range(B):
+        bt[b, :nblk[b]] = perm[o:o + nblk[b]]
+        o += nblk[b]
+    kc = rng.standard_normal((nb, hkv, 16, d), dtype=np.float32)
+    vc = rng.standard_normal((nb, hkv, 16, d), dtype=np.float32)
+    q = rng.standard_normal((sum(chunks), hq, d), dtype=np.float32)
+    if dtype == "bf16":
+        q, kc, vc = oracle.f32_to_bf16(q), oracle.f32_to_bf16(kc), oracle.f32_to_bf16(vc)
+    cu = np.concatenate([[0], np.cumsum(chunks)]).astype(np.int32)
+    return q, kc, vc, bt, cu, np.asarray(pasts, np.int32)
+
+
+def run_prefill(pa, oracle, q, kc, vc, bt, cu, past, dtype):
+    d = q.shape[-1]
+    out = pa.prefill(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt),
+                     to_dev(cu), to_dev(past), int(np.diff(cu).max()))
+    got = to_np(out)
+    if dtype == "bf16":
+        got = oracle.bf16_to_f32(got)
+    ref = oracle.paged_attention(oracle.as_f32(q), oracle.as_f32(kc), oracle.as_f32(vc), bt,
+                                 cu, past)
+    return got, ref
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (4, 4, 256)])
+def test_prefill_ragged(pa, oracle, dtype, hq, hkv, d):
+    rng = np.random.default_rng(hq + d)
+    pasts = [0, 16, 37, 5, 130]
+    chunks = [1, 40, 130, 16, 77]
+    case = make_prefill_case(oracle, rng, pasts, chunks, hq, hkv, d, dtype)
+    got, ref = run_prefill(pa, oracle, *case, dtype)
+    tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
+    assert_close(got, ref, *tol, f"prefill {dtype} {hq}/{hkv}x{d}")
+
+
+def test_config3_shape_reduced(pa, oracle):
+    # BASELINE config 3 shape (32/8 x 128, past 0/512/1024/2048), chunk 256.
+    rng = np.random.default_rng(2)
+    case = make_prefill_case(oracle, rng, [0, 512, 1024, 2048], [256] * 4, 32, 8, 128, "bf16")
+    got, ref = run_prefill(pa, oracle, *case, "bf16")
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, "config 3 reduced")
+
+
+def test_chunked_equals_full_on_gpu(pa, oracle):
+    # chunked prefill == one-shot prefill (layer_loop.rs:168-236), both on GPU
+    rng = np.random.default_rng(3)
+    q, kc, vc, bt, cu, past = make_prefill_case(oracle, rng, [0], [200], 8, 2, 128, "bf16")
+    dk, dv, dbt = to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt)
+    full = pa.prefill(to_dev(q), dk, dv, dbt, to_dev(cu), to_dev(past), 200)
+    a = pa.prefill(to_dev(q[:77]), dk, dv, dbt, to_dev(np.array([0, 77], np.int32)),
+                   to_dev(np.array([0], np.int32)), 77)
+    b = pa.prefill(to_dev(q[77:]), dk, dv, dbt, to_dev(np.array([0, 123], np.int32)),
+                   to_dev(np.array([77], np.int32)), 123)
+    chunked = torch.cat([a, b]).float()
+    assert_close(chunked.cpu().numpy(), full.float().cpu().numpy(), 1e-2, 1e-2, "chunked")
+
+
+def test_decode_equals_last_prefill_row(pa, oracle):
+    rng = np.random.default_rng(4)
+    q, kc, vc, bt, cu, past = make_prefill_case(oracle, rng, [300], [50], 32, 8, 128, "bf16")
+    dk, dv, dbt = to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt)
+    pf = pa.prefill(to_dev(q), dk, dv, dbt, to_dev(cu), to_dev(past), 50)
+    dec = pa.decode(to_dev(q[-1:]), dk, dv, dbt, to_dev(np.array([350], np.int32)), 350)
+    assert_close(dec.float().cpu().numpy(), pf[-1:].float().cpu().numpy(), 1e-2, 1e-2,
+                 "decode vs prefill")

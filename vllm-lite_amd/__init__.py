@@ -1,0 +1,35 @@
+"""MI355X paged attention for vllm-lite: HIP kernels behind a C ABI.
+
+The product is ``libpa.so`` (built from ``csrc/`` by ``build_lib.build``).
+This package is the thin Python face of it: ctypes bindings (``_lib``),
+torch-tensor wrappers of the stateless entry points (``ops``) and the
+``PagedKvCache`` mirror of the reference's cache object (``kv_cache``).
+There is no fallback path: importing the wrappers without a built library
+raises.
+"""
+from . import _lib
+from .ops import (
+    BLOCK_SIZE,
+    PaError,
+    block_hash,
+    decode,
+    decode_workspace_size,
+    prefill,
+    read_kv,
+    reshape_and_cache,
+    slot_mapping,
+)
+from .kv_cache import PagedKvCache
+
+__all__ = [
+    "BLOCK_SIZE",
+    "PaError",
+    "PagedKvCache",
+    "block_hash",
+    "decode",
+    "decode_workspace_size",
+    "prefill",
+    "read_kv",
+    "reshape_and_cache",
+    "slot_mapping",
+]

@@ -1,0 +1,54 @@
+"""ctypes bindings of libpa.so (declarations mirror include/pa.h and
+include/pa_kv_cache.h)."""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpa.so")
+
+# Every symbol the headers declare, with (restype, argtypes).
+_i32, _i64, _f32, _sz, _p = C.c_int32, C.c_int64, C.c_float, C.c_size_t, C.c_void_p
+SIGNATURES = {
+    "pa_last_error": (C.c_char_p, []),
+    "pa_version": (C.c_char_p, []),
+    "pa_reshape_and_cache": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64,
+                                    _i32, _p]),
+    "pa_slot_mapping": (_i32, [_p, _i32, _p, _p, _i32, _i32, _p, _p]),
+    "pa_read_kv": (_i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _i32, _p]),
+    "pa_block_hash": (_i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p]),
+    "pa_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
+    "pa_decode": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                         _p, _sz, _i32, _p]),
+    "pa_prefill": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
+                          _i32, _f32, _i32, _p]),
+    "pa_kv_cache_create": (_i32, [_i32, _i32, _i32, _i32, _i32, C.POINTER(_p)]),
+    "pa_kv_cache_destroy": (None, [_p]),
+    "pa_kv_cache_num_layers": (_i32, [_p]),
+    "pa_kv_cache_num_blocks": (_i32, [_p]),
+    "pa_kv_cache_block_size": (_i32, [_p]),
+    "pa_kv_cache_key_ptr": (_p, [_p, _i32]),
+    "pa_kv_cache_value_ptr": (_p, [_p, _i32]),
+    "pa_kv_cache_write_kv": (_i32, [_p, _i32, _i64, _i64, _p, _p, _p]),
+    "pa_kv_cache_write_kv_batch": (_i32, [_p, _i32, _i64, _i64, _p, _p, _i32, _p]),
+    "pa_kv_cache_write_prefill_kv": (_i32, [_p, _i32, _p, _i32, _p, _i32, _i32, _p, _p, _p]),
+    "pa_kv_cache_read_kv": (_i32, [_p, _i32, _p, _i32, _i32, _p, _p, C.POINTER(_i32), _p]),
+}
+
+_lib = None
+
+
+def load():
+    """Loads libpa.so once; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc, gfx950)")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib

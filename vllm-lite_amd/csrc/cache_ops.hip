@@ -1,0 +1,268 @@
+// KV-cache write / read kernels and their C entry points:
+// pa_reshape_and_cache, pa_slot_mapping, pa_read_kv, pa_block_hash.
+//
+// These are HBM-bound copies.  A token's K row for one head is D contiguous
+// elements in both source and cache; its V row is scattered into the
+// token-minor V block ([D, 16] per head), one element per 32 B (bf16) or
+// 64 B (f32) row of the block.
+#include "pa_common.hpp"
+
+namespace pa {
+
+namespace {
+thread_local std::string g_err;
+}
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+}
+void clear_error() { g_err.clear(); }
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Scatter.  One workgroup per token; each thread moves VEC consecutive
+// elements of one head (VEC = 8 when D % 8 == 0, else 1).
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void reshape_and_cache_kernel(
+    const T* __restrict__ key, const T* __restrict__ value, T* __restrict__ k_cache,
+    T* __restrict__ v_cache, const int64_t* __restrict__ slots, int H, int D, int64_t num_slots,
+    int64_t key_stride, int64_t value_stride) {
+  const int t = blockIdx.x;
+  const int64_t slot = slots[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t blk = slot / kBlock;
+  const int off = (int)(slot % kBlock);
+  const int per_head = D / VEC;
+  for (int i = threadIdx.x; i < H * per_head; i += blockDim.x) {
+    const int h = i / per_head;
+    const int d0 = (i % per_head) * VEC;
+    const T* ks = key + t * key_stride + (int64_t)h * D + d0;
+    const T* vs = value + t * value_stride + (int64_t)h * D + d0;
+    T* kd = k_cache + ((blk * H + h) * kBlock + off) * (int64_t)D + d0;
+    T* vd = v_cache + ((blk * H + h) * (int64_t)D + d0) * kBlock + off;
+    if constexpr (VEC * sizeof(T) == 16) {
+      *reinterpret_cast<uint4*>(kd) = *reinterpret_cast<const uint4*>(ks);
+      uint4 vv = *reinterpret_cast<const uint4*>(vs);
+      const T* ve = reinterpret_cast<const T*>(&vv);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) vd[e * kBlock] = ve[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        kd[e] = ks[e];
+        vd[e * kBlock] = vs[e];
+      }
+    }
+  }
+}
+
+// slot_mapping[t] = block_tables[s][pos / 16] * 16 + pos % 16.
+__global__ void slot_mapping_kernel(const int32_t* __restrict__ block_tables, int mbs,
+                                    const int64_t* __restrict__ positions,
+                                    const int32_t* __restrict__ cu, int64_t* __restrict__ slots) {
+  const int s = blockIdx.x;
+  const int begin = cu[s], end = cu[s + 1];
+  for (int t = begin + threadIdx.x; t < end; t += blockDim.x) {
+    const int64_t pos = positions[t];
+    const int64_t bi = pos / kBlock;
+    if (pos < 0 || bi >= mbs) {
+      slots[t] = -1;
+    } else {
+      const int32_t blk = block_tables[(int64_t)s * mbs + bi];
+      slots[t] = blk < 0 ? -1 : (int64_t)blk * kBlock + pos % kBlock;
+    }
+  }
+}
+
+// Gather: one workgroup per token.
+template <typename T>
+__global__ __launch_bounds__(256) void read_kv_kernel(const T* __restrict__ k_cache,
+                                                      const T* __restrict__ v_cache,
+                                                      const int32_t* __restrict__ block_ids, int H,
+                                                      int D, int num_blocks, T* __restrict__ out_k,
+                                                      T* __restrict__ out_v) {
+  const int t = blockIdx.x;
+  const int32_t blk = block_ids[t / kBlock];
+  const bool ok = blk >= 0 && blk < num_blocks;
+  const int off = t % kBlock;
+  for (int i = threadIdx.x; i < H * D; i += blockDim.x) {
+    const int h = i / D, d = i % D;
+    T kx = T(0), vx = T(0);
+    if (ok) {
+      kx = k_cache[(((int64_t)blk * H + h) * kBlock + off) * D + d];
+      vx = v_cache[(((int64_t)blk * H + h) * D + d) * kBlock + off];
+    }
+    out_k[(int64_t)t * H * D + i] = kx;
+    out_v[(int64_t)t * H * D + i] = vx;
+  }
+}
+
+__device__ inline uint64_t hash_term(float x) {
+  const float y = fabsf(x) * 1000.0f;
+  if (!(y > 0.0f)) return 0;  // NaN, +0
+  if (y >= 18446744073709551616.0f) return ~0ull;
+  return (uint64_t)y;
+}
+
+__host__ __device__ inline uint64_t pow_u64(uint64_t b, uint64_t e) {
+  uint64_t r = 1;
+  while (e) {
+    if (e & 1) r *= b;
+    b *= b;
+    e >>= 1;
+  }
+  return r;
+}
+
+// Polynomial hash sum_i x_i * 31^(n-1-i) (mod 2^64), split into per-thread
+// contiguous chunks that are hashed sequentially and then combined.
+__global__ __launch_bounds__(256) void block_hash_kernel(const float* __restrict__ k_cache,
+                                                         const int32_t* __restrict__ block_ids,
+                                                         int64_t n, int num_blocks,
+                                                         uint64_t* __restrict__ out) {
+  __shared__ uint64_t part[256];
+  const int32_t blk = block_ids[blockIdx.x];
+  if (blk < 0 || blk >= num_blocks) {
+    if (threadIdx.x == 0) out[blockIdx.x] = 0;
+    return;
+  }
+  const float* p = k_cache + (int64_t)blk * n;
+  const int64_t chunk = (n + blockDim.x - 1) / blockDim.x;
+  const int64_t b = threadIdx.x * chunk;
+  const int64_t e = b + chunk < n ? b + chunk : n;
+  uint64_t h = 0;
+  for (int64_t i = b; i < e; ++i) h = h * 31u + hash_term(p[i]);
+  part[threadIdx.x] = h;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // Every chunk except possibly the tail ones has `chunk` terms.
+    uint64_t acc = 0;
+    for (int c = 0; c < (int)blockDim.x; ++c) {
+      const int64_t cb = c * chunk;
+      const int64_t ce = cb + chunk < n ? cb + chunk : n;
+      const int64_t len = ce > cb ? ce - cb : 0;
+      acc = acc * pow_u64(31u, (uint64_t)len) + part[c];
+    }
+    out[blockIdx.x] = acc;
+  }
+}
+
+}  // namespace
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" const char* pa_last_error(void) { return g_err.c_str(); }
+
+extern "C" const char* pa_version(void) { return "vllm-lite-amd paged attention 0.1 (gfx950)"; }
+
+extern "C" int32_t pa_reshape_and_cache(const void* key, const void* value, void* k_cache,
+                                        void* v_cache, const int64_t* slot_mapping,
+                                        int32_t num_tokens, int32_t num_kv_heads,
+                                        int32_t head_dim, int32_t num_blocks, int64_t key_stride,
+                                        int64_t value_stride, int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_reshape_and_cache: unknown dtype %d", dtype);
+  PA_REQUIRE(num_tokens >= 0 && num_kv_heads > 0 && head_dim > 0 && num_blocks > 0,
+             PA_ERR_INVALID_ARG, "pa_reshape_and_cache: bad sizes T=%d H=%d D=%d NB=%d",
+             num_tokens, num_kv_heads, head_dim, num_blocks);
+  if (num_tokens == 0) return PA_OK;
+  PA_REQUIRE(key && value && k_cache && v_cache && slot_mapping, PA_ERR_INVALID_ARG,
+             "pa_reshape_and_cache: null pointer");
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (key_stride == 0) key_stride = row;
+  if (value_stride == 0) value_stride = row;
+  PA_REQUIRE(key_stride >= row && value_stride >= row, PA_ERR_INVALID_ARG,
+             "pa_reshape_and_cache: token stride smaller than Hkv*D");
+  const int64_t num_slots = (int64_t)num_blocks * kBlock;
+  const size_t es = dtype_size(dtype);
+  const bool vec = head_dim % 8 == 0 && (key_stride * es) % 16 == 0 &&
+                   (value_stride * es) % 16 == 0 && ((uintptr_t)key % 16) == 0 &&
+                   ((uintptr_t)value % 16) == 0 && ((uintptr_t)k_cache % 16) == 0;
+  const dim3 grid(num_tokens), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PA_DTYPE_BF16) {
+    auto* kc = (uint16_t*)k_cache;
+    auto* vc = (uint16_t*)v_cache;
+    if (vec)
+      reshape_and_cache_kernel<uint16_t, 8><<<grid, block, 0, s>>>(
+          (const uint16_t*)key, (const uint16_t*)value, kc, vc, slot_mapping, num_kv_heads,
+          head_dim, num_slots, key_stride, value_stride);
+    else
+      reshape_and_cache_kernel<uint16_t, 1><<<grid, block, 0, s>>>(
+          (const uint16_t*)key, (const uint16_t*)value, kc, vc, slot_mapping, num_kv_heads,
+          head_dim, num_slots, key_stride, value_stride);
+  } else {
+    auto* kc = (float*)k_cache;
+    auto* vc = (float*)v_cache;
+    if (head_dim % 4 == 0 && vec)
+      reshape_and_cache_kernel<float, 4><<<grid, block, 0, s>>>(
+          (const float*)key, (const float*)value, kc, vc, slot_mapping, num_kv_heads, head_dim,
+          num_slots, key_stride, value_stride);
+    else
+      reshape_and_cache_kernel<float, 1><<<grid, block, 0, s>>>(
+          (const float*)key, (const float*)value, kc, vc, slot_mapping, num_kv_heads, head_dim,
+          num_slots, key_stride, value_stride);
+  }
+  return check_launch("pa_reshape_and_cache");
+}
+
+extern "C" int32_t pa_slot_mapping(const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                   const int64_t* positions, const int32_t* cu_seq_tokens,
+                                   int32_t num_seqs, int32_t num_tokens, int64_t* slot_mapping,
+                                   pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(num_seqs >= 0 && num_tokens >= 0 && max_blocks_per_seq >= 0, PA_ERR_INVALID_ARG,
+             "pa_slot_mapping: negative size");
+  if (num_seqs == 0 || num_tokens == 0) return PA_OK;
+  PA_REQUIRE(block_tables && positions && cu_seq_tokens && slot_mapping, PA_ERR_INVALID_ARG,
+             "pa_slot_mapping: null pointer");
+  slot_mapping_kernel<<<num_seqs, 256, 0, (hipStream_t)stream>>>(
+      block_tables, max_blocks_per_seq, positions, cu_seq_tokens, slot_mapping);
+  return check_launch("pa_slot_mapping");
+}
+
+extern "C" int32_t pa_read_kv(const void* k_cache, const void* v_cache, const int32_t* block_ids,
+                              int32_t n_ids, int32_t seq_len, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t num_blocks, void* out_k, void* out_v,
+                              int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_read_kv: unknown dtype %d", dtype);
+  PA_REQUIRE(seq_len >= 0 && n_ids >= 0 && num_kv_heads > 0 && head_dim > 0 && num_blocks > 0,
+             PA_ERR_INVALID_ARG, "pa_read_kv: bad sizes");
+  if (seq_len == 0 || n_ids == 0) return PA_OK;
+  PA_REQUIRE((int64_t)n_ids * kBlock >= seq_len, PA_ERR_OUT_OF_BOUNDS,
+             "pa_read_kv: %d blocks cannot hold %d tokens", n_ids, seq_len);
+  PA_REQUIRE(k_cache && v_cache && block_ids && out_k && out_v, PA_ERR_INVALID_ARG,
+             "pa_read_kv: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PA_DTYPE_BF16)
+    read_kv_kernel<uint16_t><<<seq_len, 256, 0, s>>>(
+        (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_ids, num_kv_heads, head_dim,
+        num_blocks, (uint16_t*)out_k, (uint16_t*)out_v);
+  else
+    read_kv_kernel<float><<<seq_len, 256, 0, s>>>((const float*)k_cache, (const float*)v_cache,
+                                                 block_ids, num_kv_heads, head_dim, num_blocks,
+                                                 (float*)out_k, (float*)out_v);
+  return check_launch("pa_read_kv");
+}
+
+extern "C" int32_t pa_block_hash(const float* k_cache, const int32_t* block_ids, int32_t n,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                                 uint64_t* hashes, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(n >= 0 && num_kv_heads > 0 && head_dim > 0 && num_blocks > 0, PA_ERR_INVALID_ARG,
+             "pa_block_hash: bad sizes");
+  if (n == 0) return PA_OK;
+  PA_REQUIRE(k_cache && block_ids && hashes, PA_ERR_INVALID_ARG, "pa_block_hash: null pointer");
+  const int64_t per_block = (int64_t)num_kv_heads * kBlock * head_dim;
+  block_hash_kernel<<<n, 256, 0, (hipStream_t)stream>>>(k_cache, block_ids, per_block, num_blocks,
+                                                        hashes);
+  return check_launch("pa_block_hash");
+}

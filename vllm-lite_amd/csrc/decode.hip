@@ -1,0 +1,437 @@
+// Single-token decode attention over the paged KV cache (pa_decode).
+//
+// Work split (flash-decoding): the context of each sequence is cut into
+// partitions of kPart tokens.  One workgroup handles one (partition,
+// kv head, sequence) and produces, for each query head of the group, the
+// running max m (log2 domain), the softmax denominator l and the
+// unnormalised output o[D].  A single-partition launch writes the final
+// output directly; otherwise a reduce kernel merges the partitions with the
+// log-sum-exp rule
+//     M = max_p m_p,  out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p.
+//
+// Two attention kernels:
+//  * decode_mfma_kernel (bf16, D in {64, 128, 256}, group size <= 16): one
+//    wavefront per workgroup.  Scores S = K·Qᵀ and the output Oᵀ = Vᵀ·Pᵀ
+//    both run on v_mfma_f32_16x16x32_bf16 with the query heads of the group
+//    as the 16-wide N dimension, so every K/V byte is loaded once for the
+//    whole group.  Loads go straight from HBM into MFMA operand registers:
+//    K rows are token-major, V rows are token-minor, which is exactly the
+//    operand order each contraction wants.  Two 16-token blocks are
+//    processed per step (32 = the MFMA K dimension of the P·V product).
+//  * decode_generic_kernel (f32 or bf16, any D <= 512, any group size): a
+//    plain reference-grade kernel, one workgroup per query head.
+#include "pa_common.hpp"
+
+namespace pa {
+namespace {
+
+constexpr int kPart = 256;  // tokens per partition (16 blocks)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1.0e30f;  // "no max yet": finite so 2^(x - m) never sees inf - inf
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline float shfl_xor_f(float x, int mask) { return __shfl_xor(x, mask, 64); }
+
+// ---------------------------------------------------------------------------
+// MFMA decode kernel.
+//
+// Lane layout (lane = 16 * j + c, c = lane & 15, j = lane >> 4), using the
+// v_mfma_f32_16x16x32_bf16 operand layouts
+//   A[i][k]: lane holds row i = c, k = 8j .. 8j+7
+//   B[k][n]: lane holds col n = c, k = 8j .. 8j+7
+//   D[i][n]: lane holds col n = c, rows i = 4j .. 4j+3
+// QK:  A = K block (i = token c), B = Qᵀ (n = head c of the group), the
+//      D = 128 reduction split in 32-wide steps s, lane group j taking dims
+//      32s + 8j .. +8 in both operands.  Result: lane holds S[token 4j+r][head c].
+// PV:  A = Vᵀ (i = dim 16dt + c), B = Pᵀ (n = head c); the 32 reduction slots
+//      8j+r / 8j+4+r are tokens 4j+r of the first / second block of the step,
+//      which is exactly what the lane already holds from QK.  Result: lane
+//      holds Oᵀ[dim 16dt + 4j + r][head c].
+template <int D>
+__global__ __launch_bounds__(64) void decode_mfma_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
+    float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  constexpr int KS = D / 32;  // QK reduction steps
+  constexpr int DT = D / 16;  // PV output tiles
+  const int lane = threadIdx.x;
+  const int c = lane & 15, j = lane >> 4;
+  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  // Clamp to what the block table can address so a bad length never reads
+  // past the table.
+  const int ctx = min(context_lens[seq], mbs * kBlock);
+  const int tok0 = part * kPart;
+  if (tok0 >= ctx) {
+    // Empty context: the output is defined as zeros.
+    if (num_parts == 1 && c < G) {
+      uint16_t* orow = out + ((int64_t)seq * Hq + kvh * G + c) * D;
+      for (int d = 4 * j; d < D; d += 16) *reinterpret_cast<uint64_t*>(orow + d) = 0;
+    }
+    return;
+  }
+  const int tok_end = min(ctx, tok0 + kPart);
+  const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;
+
+  const int head = kvh * G + c;
+  bf16x8 qv[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (c < G)
+      qv[s] = *reinterpret_cast<const bf16x8*>(q + ((int64_t)seq * Hq + head) * D + 32 * s + 8 * j);
+    else
+      qv[s] = bf16x8{};
+  }
+
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = kNegBig, lsum = 0.f;
+
+  const int32_t* btab = block_tables + (int64_t)seq * mbs + tok0 / kBlock;
+  const int64_t head_stride = (int64_t)kBlock * D;  // elements per (block, head)
+
+  for (int ib = 0; ib < nblk; ib += 2) {
+    // Block ids for this step; ids outside the pool read block 0 and are masked.
+    int32_t b0 = btab[ib];
+    const bool has1 = ib + 1 < nblk;
+    int32_t b1 = has1 ? btab[ib + 1] : b0;
+    const int rem = tok_end - (tok0 + ib * kBlock);  // tokens left from this step
+    int lim0 = rem < kBlock ? rem : kBlock;
+    int lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
+    if (b0 < 0 || b0 >= num_blocks) { b0 = 0; lim0 = 0; }
+    if (b1 < 0 || b1 >= num_blocks) { b1 = 0; lim1 = 0; }
+
+    const uint16_t* k0 = kc + ((int64_t)b0 * Hkv + kvh) * head_stride + c * D + 8 * j;
+    const uint16_t* k1 = kc + ((int64_t)b1 * Hkv + kvh) * head_stride + c * D + 8 * j;
+    bf16x8 ka[KS], kb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      ka[s] = *reinterpret_cast<const bf16x8*>(k0 + 32 * s);
+      kb[s] = *reinterpret_cast<const bf16x8*>(k1 + 32 * s);
+    }
+    const uint16_t* v0 = vc + ((int64_t)b0 * Hkv + kvh) * head_stride + c * kBlock + 4 * j;
+    const uint16_t* v1 = vc + ((int64_t)b1 * Hkv + kvh) * head_stride + c * kBlock + 4 * j;
+    uint64_t va[DT], vb[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      va[dt] = *reinterpret_cast<const uint64_t*>(v0 + dt * 16 * kBlock);
+      vb[dt] = *reinterpret_cast<const uint64_t*>(v1 + dt * 16 * kBlock);
+    }
+
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qv[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[s], qv[s], s1, 0, 0, 0);
+    }
+
+    float x[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = s0[r] * scale_log2;
+      x[4 + r] = s1[r] * scale_log2;
+    }
+    const bool partial = lim0 < kBlock || lim1 < kBlock;  // wave-uniform
+    if (partial) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (4 * j + r >= lim0) x[r] = -INFINITY;
+        if (4 * j + r >= lim1) x[4 + r] = -INFINITY;
+      }
+      // Stale cache contents beyond the context may hold any bits (NaN
+      // included); zero them so 0 * V stays 0 in the P·V product.
+      const int n0 = min(max(lim0 - 4 * j, 0), 4), n1 = min(max(lim1 - 4 * j, 0), 4);
+      const uint64_t mk0 = n0 >= 4 ? ~0ull : ((1ull << (16 * n0)) - 1);
+      const uint64_t mk1 = n1 >= 4 ? ~0ull : ((1ull << (16 * n1)) - 1);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        va[dt] &= mk0;
+        vb[dt] &= mk1;
+      }
+    }
+
+    float bm = x[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) bm = fmaxf(bm, x[i]);
+    bm = fmaxf(bm, shfl_xor_f(bm, 16));
+    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    // Lazy rescale: keep the stale max unless a score exceeds it by more
+    // than 2^8, so p <= 256 and the accumulator is rescaled rarely.
+    if (__builtin_amdgcn_ballot_w64(bm > m + 8.0f)) {
+      const float mn = fmaxf(m, bm);
+      const float a = fast_exp2(m - mn);
+      m = mn;
+      lsum *= a;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= a;
+    }
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = fast_exp2(x[i] - m);
+      lsum += p[i];
+    }
+    bf16x8 pb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pb[i] = (__bf16)p[i];
+
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint64_t pair[2] = {va[dt], vb[dt]};
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(pair);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
+    }
+  }
+
+  lsum += shfl_xor_f(lsum, 16);
+  lsum += shfl_xor_f(lsum, 32);
+  if (c >= G) return;
+  if (num_parts == 1) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    uint16_t* orow = out + ((int64_t)seq * Hq + head) * D + 4 * j;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      uint16_t w[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = f32_to_bf16_bits(o[dt][r] * inv);
+      *reinterpret_cast<uint64_t*>(orow + 16 * dt) = *reinterpret_cast<const uint64_t*>(w);
+    }
+  } else {
+    const int64_t row = ((int64_t)seq * Hq + head) * num_parts + part;
+    float* orow = ws_o + row * D + 4 * j;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(orow + 16 * dt) = o[dt];
+    if (j == 0) {
+      ws_ml[2 * row] = m;
+      ws_ml[2 * row + 1] = lsum;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic decode kernel: one workgroup of 256 threads per (partition, query
+// head, sequence).  Scores go through LDS; f32 accumulation throughout.
+template <typename T>
+__global__ __launch_bounds__(256) void decode_generic_kernel(
+    T* __restrict__ out, const T* __restrict__ q, const T* __restrict__ kc,
+    const T* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ context_lens, int Hq, int Hkv, int D, int num_blocks,
+    float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  __shared__ float qs[512];
+  __shared__ float ps[kPart];
+  __shared__ int32_t bs[kPart / kBlock];
+  __shared__ float red[256];
+  const int part = blockIdx.x, h = blockIdx.y, seq = blockIdx.z;
+  const int G = Hq / Hkv, kvh = h / G;
+  // Clamp to what the block table can address so a bad length never reads
+  // past the table.
+  const int ctx = min(context_lens[seq], mbs * kBlock);
+  const int tok0 = part * kPart;
+  if (tok0 >= ctx) {
+    if (num_parts == 1)
+      for (int d = threadIdx.x; d < D; d += blockDim.x)
+        Elem<T>::store(out + ((int64_t)seq * Hq + h) * D + d, 0.f);
+    return;
+  }
+  const int n = min(ctx - tok0, kPart);
+  const int tid = threadIdx.x;
+  for (int d = tid; d < D; d += blockDim.x)
+    qs[d] = Elem<T>::load(q + ((int64_t)seq * Hq + h) * D + d);
+  if (tid < (n + kBlock - 1) / kBlock) {
+    const int32_t b = block_tables[(int64_t)seq * mbs + tok0 / kBlock + tid];
+    bs[tid] = (b >= 0 && b < num_blocks) ? b : -1;
+  }
+  __syncthreads();
+
+  float mloc = -INFINITY;
+  for (int t = tid; t < n; t += blockDim.x) {
+    const int32_t b = bs[t / kBlock];
+    float s = -INFINITY;
+    if (b >= 0) {
+      const T* kr = kc + (((int64_t)b * Hkv + kvh) * kBlock + t % kBlock) * D;
+      float acc = 0.f;
+      for (int d = 0; d < D; ++d) acc += qs[d] * Elem<T>::load(kr + d);
+      s = acc * scale_log2;
+    }
+    ps[t] = s;
+    mloc = fmaxf(mloc, s);
+  }
+  red[tid] = mloc;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+    __syncthreads();
+  }
+  const float m = red[0] == -INFINITY ? kNegBig : red[0];
+  __syncthreads();
+  float lloc = 0.f;
+  for (int t = tid; t < n; t += blockDim.x) {
+    const float p = exp2f(ps[t] - m);
+    ps[t] = p;
+    lloc += p;
+  }
+  red[tid] = lloc;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  const float l = red[0];
+  for (int d = tid; d < D; d += blockDim.x) {
+    float acc = 0.f;
+    for (int t = 0; t < n; ++t) {
+      const int32_t b = bs[t / kBlock];
+      if (b < 0) continue;
+      acc += ps[t] * Elem<T>::load(vc + (((int64_t)b * Hkv + kvh) * D + d) * kBlock + t % kBlock);
+    }
+    if (num_parts == 1) {
+      Elem<T>::store(out + ((int64_t)seq * Hq + h) * D + d, l > 0.f ? acc / l : 0.f);
+    } else {
+      ws_o[(((int64_t)seq * Hq + h) * num_parts + part) * D + d] = acc;
+    }
+  }
+  if (num_parts > 1 && tid == 0) {
+    const int64_t row = ((int64_t)seq * Hq + h) * num_parts + part;
+    ws_ml[2 * row] = m;
+    ws_ml[2 * row + 1] = l;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Partition merge: one workgroup per (query head, sequence).
+template <typename T>
+__global__ __launch_bounds__(256) void decode_reduce_kernel(
+    T* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+    const int32_t* __restrict__ context_lens, int Hq, int D, int num_parts) {
+  __shared__ float wsh[1024];
+  __shared__ float red[256];
+  const int h = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x;
+  const int ctx = context_lens[seq];
+  const int np = min(num_parts, (ctx + kPart - 1) / kPart);
+  const int64_t row0 = ((int64_t)seq * Hq + h) * num_parts;
+  float mloc = -INFINITY;
+  for (int p = tid; p < np; p += blockDim.x) mloc = fmaxf(mloc, ws_ml[2 * (row0 + p)]);
+  red[tid] = mloc;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+    __syncthreads();
+  }
+  const float M = red[0];
+  __syncthreads();
+  float lloc = 0.f;
+  for (int p = tid; p < np; p += blockDim.x) {
+    const float w = exp2f(ws_ml[2 * (row0 + p)] - M);
+    if (p < 1024) wsh[p] = w;
+    lloc += w * ws_ml[2 * (row0 + p) + 1];
+  }
+  red[tid] = lloc;
+  __syncthreads();
+  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  const float L = red[0];
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  for (int d = tid; d < D; d += blockDim.x) {
+    float acc = 0.f;
+    for (int p = 0; p < np; ++p) {
+      const float w = p < 1024 ? wsh[p] : exp2f(ws_ml[2 * (row0 + p)] - M);
+      acc += w * ws_o[(row0 + p) * D + d];
+    }
+    Elem<T>::store(out + ((int64_t)seq * Hq + h) * D + d, acc * inv);
+  }
+}
+
+int num_partitions(int max_ctx) { return max_ctx <= 0 ? 1 : (max_ctx + kPart - 1) / kPart; }
+
+}  // namespace
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                           int32_t max_context_len) {
+  const int np = num_partitions(max_context_len);
+  if (np <= 1 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return (size_t)num_seqs * num_heads * np * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* block_tables, int32_t max_blocks_per_seq,
+                             const int32_t* context_lens, int32_t max_context_len,
+                             int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t num_blocks, float scale, void* workspace,
+                             size_t workspace_bytes, int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_decode: unknown dtype %d", dtype);
+  PA_REQUIRE(num_seqs >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
+                 num_blocks > 0 && max_blocks_per_seq > 0 && max_context_len >= 0,
+             PA_ERR_INVALID_ARG, "pa_decode: bad sizes");
+  PA_REQUIRE(num_heads % num_kv_heads == 0, PA_ERR_INVALID_ARG,
+             "pa_decode: num_heads %d not a multiple of num_kv_heads %d", num_heads, num_kv_heads);
+  PA_REQUIRE((int64_t)max_blocks_per_seq * kBlock >= max_context_len, PA_ERR_OUT_OF_BOUNDS,
+             "pa_decode: max_context_len %d exceeds the block table (%d blocks)", max_context_len,
+             max_blocks_per_seq);
+  PA_REQUIRE(head_dim <= 512, PA_ERR_UNSUPPORTED, "pa_decode: head_dim %d > 512", head_dim);
+  if (num_seqs == 0 || max_context_len == 0) return PA_OK;
+  PA_REQUIRE(out && q && k_cache && v_cache && block_tables && context_lens, PA_ERR_INVALID_ARG,
+             "pa_decode: null pointer");
+  const int np = num_partitions(max_context_len);
+  float* ws_o = nullptr;
+  float* ws_ml = nullptr;
+  if (np > 1) {
+    const size_t need = pa_decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len);
+    PA_REQUIRE(workspace && workspace_bytes >= need, PA_ERR_WORKSPACE,
+               "pa_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    ws_o = (float*)workspace;
+    ws_ml = ws_o + (size_t)num_seqs * num_heads * np * head_dim;
+  }
+  const int G = num_heads / num_kv_heads;
+  const float scale_log2 = scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  const bool mfma = dtype == PA_DTYPE_BF16 && G <= 16 &&
+                    (head_dim == 64 || head_dim == 128 || head_dim == 256);
+  if (mfma) {
+    const dim3 grid(np, num_kv_heads, num_seqs);
+    auto* o = (uint16_t*)out;
+    auto* qq = (const uint16_t*)q;
+    auto* kc = (const uint16_t*)k_cache;
+    auto* vc = (const uint16_t*)v_cache;
+#define PA_LAUNCH_MFMA(DD)                                                                      \
+  decode_mfma_kernel<DD><<<grid, 64, 0, s>>>(o, qq, kc, vc, block_tables, max_blocks_per_seq,   \
+                                             context_lens, num_heads, num_kv_heads, G,          \
+                                             num_blocks, scale_log2, np, ws_o, ws_ml)
+    if (head_dim == 64)
+      PA_LAUNCH_MFMA(64);
+    else if (head_dim == 128)
+      PA_LAUNCH_MFMA(128);
+    else
+      PA_LAUNCH_MFMA(256);
+#undef PA_LAUNCH_MFMA
+  } else {
+    const dim3 grid(np, num_heads, num_seqs);
+    if (dtype == PA_DTYPE_BF16)
+      decode_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(
+          (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
+          block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
+          num_blocks, scale_log2, np, ws_o, ws_ml);
+    else
+      decode_generic_kernel<float><<<grid, 256, 0, s>>>(
+          (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,
+          block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
+          num_blocks, scale_log2, np, ws_o, ws_ml);
+  }
+  int32_t rc = check_launch("pa_decode");
+  if (rc != PA_OK || np == 1) return rc;
+  const dim3 rgrid(num_heads, num_seqs);
+  if (dtype == PA_DTYPE_BF16)
+    decode_reduce_kernel<uint16_t><<<rgrid, 256, 0, s>>>((uint16_t*)out, ws_o, ws_ml,
+                                                         context_lens, num_heads, head_dim, np);
+  else
+    decode_reduce_kernel<float><<<rgrid, 256, 0, s>>>((float*)out, ws_o, ws_ml, context_lens,
+                                                      num_heads, head_dim, np);
+  return check_launch("pa_decode reduce");
+}

@@ -1,0 +1,242 @@
+// Host-side PagedKvCache mirror (pa_kv_cache_* in pa_kv_cache.h).
+//
+// Owns one K and one V device buffer per layer and implements the
+// reference's write_kv / write_kv_batch / write_prefill_kv / read_kv on top
+// of the stateless kernels: index arithmetic and bounds checks run on the
+// host exactly where the reference checks them, the data movement is one
+// kernel launch per call.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <vector>
+
+#include "../../include/pa_kv_cache.h"
+#include "pa_common.hpp"
+
+struct pa_kv_cache {
+  int num_layers = 0, num_heads = 0, head_dim = 0, num_blocks = 0, dtype = 0;
+  std::vector<void*> key, value;
+  // Staging for host index arrays: pinned host copy -> device copy.
+  void* host_stage = nullptr;
+  void* dev_stage = nullptr;
+  size_t stage_bytes = 0;
+
+  size_t layer_bytes() const {
+    return (size_t)num_blocks * num_heads * pa::kBlock * head_dim * pa::dtype_size(dtype);
+  }
+
+  int32_t ensure_stage(size_t bytes) {
+    if (bytes <= stage_bytes) return PA_OK;
+    if (host_stage) (void)hipHostFree(host_stage);
+    if (dev_stage) (void)hipFree(dev_stage);
+    host_stage = dev_stage = nullptr;
+    stage_bytes = 0;
+    size_t cap = bytes < 4096 ? 4096 : bytes;
+    if (hipHostMalloc(&host_stage, cap, hipHostMallocDefault) != hipSuccess ||
+        hipMalloc(&dev_stage, cap) != hipSuccess) {
+      pa::set_error("pa_kv_cache: staging allocation of %zu bytes failed", cap);
+      return PA_ERR_HIP;
+    }
+    stage_bytes = cap;
+    return PA_OK;
+  }
+
+  // Copies `bytes` of host data to the device stage on `stream` and returns
+  // the device pointer.  The caller synchronises the stream before the
+  // stage is reused.
+  void* upload(const void* src, size_t bytes, hipStream_t stream, int32_t* rc) {
+    *rc = ensure_stage(bytes);
+    if (*rc != PA_OK) return nullptr;
+    std::memcpy(host_stage, src, bytes);
+    if (hipMemcpyAsync(dev_stage, host_stage, bytes, hipMemcpyHostToDevice, stream) !=
+        hipSuccess) {
+      pa::set_error("pa_kv_cache: index upload failed");
+      *rc = PA_ERR_HIP;
+      return nullptr;
+    }
+    return dev_stage;
+  }
+};
+
+namespace {
+
+int32_t finish(hipStream_t stream, int32_t rc) {
+  if (rc != PA_OK) return rc;
+  if (hipStreamSynchronize(stream) != hipSuccess) {
+    pa::set_error("pa_kv_cache: stream synchronisation failed");
+    return PA_ERR_HIP;
+  }
+  return PA_OK;
+}
+
+// Scatters T tokens at host-computed slots.
+int32_t scatter(pa_kv_cache* c, int layer, const std::vector<int64_t>& slots, const void* k,
+                const void* v, hipStream_t stream) {
+  int32_t rc = PA_OK;
+  void* d_slots = c->upload(slots.data(), slots.size() * sizeof(int64_t), stream, &rc);
+  if (rc != PA_OK) return rc;
+  rc = pa_reshape_and_cache(k, v, c->key[layer], c->value[layer], (const int64_t*)d_slots,
+                            (int32_t)slots.size(), c->num_heads, c->head_dim, c->num_blocks, 0, 0,
+                            c->dtype, (pa_stream_t)stream);
+  return finish(stream, rc);
+}
+
+}  // namespace
+
+extern "C" int32_t pa_kv_cache_create(int32_t num_layers, int32_t num_kv_heads, int32_t head_dim,
+                                      int32_t num_blocks, int32_t dtype, pa_kv_cache** out) {
+  pa::clear_error();
+  PA_REQUIRE(out, PA_ERR_INVALID_ARG, "pa_kv_cache_create: null out");
+  *out = nullptr;
+  PA_REQUIRE(pa::dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_kv_cache_create: unknown dtype %d",
+             dtype);
+  PA_REQUIRE(num_layers > 0 && num_kv_heads > 0 && head_dim > 0 && num_blocks > 0,
+             PA_ERR_INVALID_ARG, "pa_kv_cache_create: sizes must be positive");
+  auto* c = new pa_kv_cache();
+  c->num_layers = num_layers;
+  c->num_heads = num_kv_heads;
+  c->head_dim = head_dim;
+  c->num_blocks = num_blocks;
+  c->dtype = dtype;
+  const size_t bytes = c->layer_bytes();
+  for (int l = 0; l < num_layers; ++l) {
+    void *k = nullptr, *v = nullptr;
+    if (hipMalloc(&k, bytes) != hipSuccess || hipMalloc(&v, bytes) != hipSuccess ||
+        hipMemset(k, 0, bytes) != hipSuccess || hipMemset(v, 0, bytes) != hipSuccess) {
+      if (k) (void)hipFree(k);
+      if (v) (void)hipFree(v);
+      pa_kv_cache_destroy(c);
+      pa::set_error("pa_kv_cache_create: allocating %zu bytes per layer failed", bytes);
+      return PA_ERR_HIP;
+    }
+    c->key.push_back(k);
+    c->value.push_back(v);
+  }
+  *out = c;
+  return PA_OK;
+}
+
+extern "C" void pa_kv_cache_destroy(pa_kv_cache* c) {
+  if (!c) return;
+  for (void* p : c->key) (void)hipFree(p);
+  for (void* p : c->value) (void)hipFree(p);
+  if (c->host_stage) (void)hipHostFree(c->host_stage);
+  if (c->dev_stage) (void)hipFree(c->dev_stage);
+  delete c;
+}
+
+extern "C" int32_t pa_kv_cache_num_layers(const pa_kv_cache* c) { return c ? c->num_layers : 0; }
+extern "C" int32_t pa_kv_cache_num_blocks(const pa_kv_cache* c) { return c ? c->num_blocks : 0; }
+extern "C" int32_t pa_kv_cache_block_size(const pa_kv_cache*) { return pa::kBlock; }
+
+extern "C" void* pa_kv_cache_key_ptr(pa_kv_cache* c, int32_t layer) {
+  return (c && layer >= 0 && layer < c->num_layers) ? c->key[layer] : nullptr;
+}
+extern "C" void* pa_kv_cache_value_ptr(pa_kv_cache* c, int32_t layer) {
+  return (c && layer >= 0 && layer < c->num_layers) ? c->value[layer] : nullptr;
+}
+
+extern "C" int32_t pa_kv_cache_write_kv(pa_kv_cache* c, int32_t layer, int64_t block_id,
+                                        int64_t token_offset, const void* k, const void* v,
+                                        pa_stream_t stream) {
+  pa::clear_error();
+  PA_REQUIRE(c && k && v, PA_ERR_INVALID_ARG, "write_kv: null argument");
+  PA_REQUIRE(layer >= 0 && layer < c->num_layers, PA_ERR_OUT_OF_BOUNDS,
+             "layer_idx %d out of bounds for %d layers", layer, c->num_layers);
+  PA_REQUIRE(block_id >= 0 && block_id < c->num_blocks, PA_ERR_OUT_OF_BOUNDS,
+             "block_id %lld out of bounds for %d blocks", (long long)block_id, c->num_blocks);
+  PA_REQUIRE(token_offset >= 0 && token_offset < pa::kBlock, PA_ERR_OUT_OF_BOUNDS,
+             "token_offset %lld out of bounds for block size %d", (long long)token_offset,
+             pa::kBlock);
+  return scatter(c, layer, {block_id * pa::kBlock + token_offset}, k, v, (hipStream_t)stream);
+}
+
+extern "C" int32_t pa_kv_cache_write_kv_batch(pa_kv_cache* c, int32_t layer, int64_t block_id,
+                                              int64_t token_offset, const void* k, const void* v,
+                                              int32_t num_tokens, pa_stream_t stream) {
+  pa::clear_error();
+  PA_REQUIRE(c && k && v, PA_ERR_INVALID_ARG, "write_kv_batch: null argument");
+  PA_REQUIRE(layer >= 0 && layer < c->num_layers, PA_ERR_OUT_OF_BOUNDS,
+             "layer_idx %d out of bounds for %d layers", layer, c->num_layers);
+  PA_REQUIRE(num_tokens >= 0 && block_id >= 0 && block_id < c->num_blocks && token_offset >= 0,
+             PA_ERR_OUT_OF_BOUNDS, "write_kv_batch: block_id %lld / offset %lld out of range",
+             (long long)block_id, (long long)token_offset);
+  const int64_t space = ((int64_t)c->num_blocks - block_id) * pa::kBlock;
+  PA_REQUIRE(token_offset + num_tokens <= space, PA_ERR_OUT_OF_BOUNDS,
+             "Token offset %lld + num_tokens %d exceeds available space %lld",
+             (long long)token_offset, num_tokens, (long long)space);
+  if (num_tokens == 0) return PA_OK;
+  std::vector<int64_t> slots(num_tokens);
+  int64_t blk = block_id, off = token_offset;
+  for (int t = 0; t < num_tokens; ++t) {
+    // Offsets >= 16 in the first block are walked the same way the
+    // reference's per-token loop walks them: write_kv would reject them.
+    PA_REQUIRE(off < pa::kBlock, PA_ERR_OUT_OF_BOUNDS,
+               "token_offset %lld out of bounds for block size %d", (long long)off, pa::kBlock);
+    slots[t] = blk * pa::kBlock + off;
+    if (++off >= pa::kBlock) {
+      ++blk;
+      off = 0;
+    }
+  }
+  return scatter(c, layer, slots, k, v, (hipStream_t)stream);
+}
+
+extern "C" int32_t pa_kv_cache_write_prefill_kv(pa_kv_cache* c, int32_t layer,
+                                                const int64_t* block_ids, int32_t n_ids,
+                                                const int64_t* positions, int32_t n_pos,
+                                                int32_t num_tokens, const void* k, const void* v,
+                                                pa_stream_t stream) {
+  pa::clear_error();
+  PA_REQUIRE(c && k && v && (block_ids || n_ids == 0), PA_ERR_INVALID_ARG,
+             "write_prefill_kv: null argument");
+  PA_REQUIRE(layer >= 0 && layer < c->num_layers, PA_ERR_OUT_OF_BOUNDS,
+             "layer_idx %d out of bounds for %d layers", layer, c->num_layers);
+  PA_REQUIRE(num_tokens >= 0, PA_ERR_INVALID_ARG, "write_prefill_kv: negative token count");
+  if (num_tokens == 0) return PA_OK;
+  std::vector<int64_t> slots(num_tokens);
+  for (int t = 0; t < num_tokens; ++t) {
+    const int64_t pos = (positions && t < n_pos) ? positions[t] : t;
+    PA_REQUIRE(pos >= 0, PA_ERR_OUT_OF_BOUNDS, "write_prefill_kv: negative position");
+    const int64_t bi = pos / pa::kBlock;
+    PA_REQUIRE(bi < n_ids, PA_ERR_OUT_OF_BOUNDS,
+               "write_prefill_kv: position %lld needs block index %lld, table has %d",
+               (long long)pos, (long long)bi, n_ids);
+    const int64_t blk = block_ids[bi];
+    PA_REQUIRE(blk >= 0 && blk < c->num_blocks, PA_ERR_OUT_OF_BOUNDS,
+               "block_id %lld out of bounds for %d blocks", (long long)blk, c->num_blocks);
+    slots[t] = blk * pa::kBlock + pos % pa::kBlock;
+  }
+  return scatter(c, layer, slots, k, v, (hipStream_t)stream);
+}
+
+extern "C" int32_t pa_kv_cache_read_kv(pa_kv_cache* c, int32_t layer, const int64_t* block_ids,
+                                       int32_t n_ids, int32_t seq_len, void* out_k, void* out_v,
+                                       int32_t* n_read, pa_stream_t stream) {
+  pa::clear_error();
+  PA_REQUIRE(c && n_read, PA_ERR_INVALID_ARG, "read_kv: null argument");
+  *n_read = 0;
+  PA_REQUIRE(layer >= 0 && layer < c->num_layers, PA_ERR_OUT_OF_BOUNDS,
+             "layer_idx %d out of bounds for %d layers", layer, c->num_layers);
+  if (n_ids <= 0 || seq_len <= 0) return PA_OK;
+  PA_REQUIRE(block_ids && out_k && out_v, PA_ERR_INVALID_ARG, "read_kv: null argument");
+  const int64_t cover = (int64_t)n_ids * pa::kBlock;
+  const int32_t n = (int32_t)(seq_len < cover ? seq_len : cover);
+  const int32_t used = (n + pa::kBlock - 1) / pa::kBlock;
+  std::vector<int32_t> ids(used);
+  for (int b = 0; b < used; ++b) {
+    PA_REQUIRE(block_ids[b] >= 0 && block_ids[b] < c->num_blocks, PA_ERR_OUT_OF_BOUNDS,
+               "block_id %lld out of bounds for %d blocks", (long long)block_ids[b],
+               c->num_blocks);
+    ids[b] = (int32_t)block_ids[b];
+  }
+  hipStream_t s = (hipStream_t)stream;
+  int32_t rc = PA_OK;
+  void* d_ids = c->upload(ids.data(), ids.size() * sizeof(int32_t), s, &rc);
+  if (rc != PA_OK) return rc;
+  rc = pa_read_kv(c->key[layer], c->value[layer], (const int32_t*)d_ids, used, n, c->num_heads,
+                  c->head_dim, c->num_blocks, out_k, out_v, c->dtype, stream);
+  rc = finish(s, rc);
+  if (rc == PA_OK) *n_read = n;
+  return rc;
+}

@@ -1,0 +1,327 @@
+// Chunked causal prefill attention over the paged KV cache (pa_prefill).
+//
+// Query row i of sequence s sits at absolute position past[s] + i and
+// attends keys 0 .. past[s] + i, all read through the block table.  One
+// kernel covers fresh prefill (past = 0) and continuation (past > 0).
+//
+//  * prefill_mfma_kernel (bf16, D in {64, 128, 256}): each wavefront owns
+//    NT * 16 consecutive query rows of one head and streams the keys two
+//    16-token blocks at a time.  Sᵀ = K·Qᵀ and Oᵀ = Vᵀ·Pᵀ run on
+//    v_mfma_f32_16x16x32_bf16 with the query rows as the N dimension; the
+//    lane that receives score (key, row) from the first product is the lane
+//    that feeds it to the second, so P never leaves registers.  Online
+//    softmax per query row; the causal mask is only evaluated on steps that
+//    straddle the diagonal.  Four wavefronts per workgroup cover adjacent
+//    row ranges of the same head so their K/V reads share the L1/L2.
+//  * prefill_generic_kernel (f32 or bf16, any D <= 512): one wavefront per
+//    (query row, head), reference-grade.
+#include "pa_common.hpp"
+
+namespace pa {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1.0e30f;
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float shfl_xor_f(float x, int mask) { return __shfl_xor(x, mask, 64); }
+
+constexpr int kWaves = 4;
+
+// Lane layout as in decode_mfma_kernel (lane = 16 j + c):
+//   QK:  A = K block (row = key c), B = Qᵀ (col = query row c of tile nt)
+//        -> lane holds Sᵀ[key 4j + r][row c]
+//   PV:  A = Vᵀ (row = dim 16 dt + c), B = Pᵀ, reduction slots 8j + r and
+//        8j + 4 + r = key 4j + r of the step's first / second block
+//        -> lane holds Oᵀ[dim 16 dt + 4j + r][row c]
+template <int D, int NT>
+__global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
+    int num_blocks, float scale_log2) {
+  constexpr int KS = D / 32;
+  constexpr int DT = D / 16;
+  constexpr int ROWS = 16 * NT;  // query rows per wavefront
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, j = lane >> 4;
+  const int h = blockIdx.y, seq = blockIdx.z;
+  const int G = Hq / Hkv, kvh = h / G;
+  const int q_begin = cu_q[seq];
+  const int qlen = cu_q[seq + 1] - q_begin;
+  const int row0 = (blockIdx.x * kWaves + wave) * ROWS;
+  if (row0 >= qlen) return;
+  const int past = past_lens[seq];
+  const int row_end = min(qlen, row0 + ROWS);
+  const int kv_len = min(past + row_end, mbs * kBlock);  // keys this wavefront needs
+  const int nblk = (kv_len + kBlock - 1) / kBlock;
+
+  bf16x8 qv[NT][KS];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = row0 + 16 * nt + c;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if (row < qlen)
+        qv[nt][s] = *reinterpret_cast<const bf16x8*>(
+            q + ((int64_t)(q_begin + row) * Hq + h) * D + 32 * s + 8 * j);
+      else
+        qv[nt][s] = bf16x8{};
+    }
+  }
+
+  f32x4 o[NT][DT];
+  float m[NT], lsum[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m[nt] = kNegBig;
+    lsum[nt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int32_t* btab = block_tables + (int64_t)seq * mbs;
+  const int64_t head_stride = (int64_t)kBlock * D;
+  const int diag_key = past + row0;  // keys above this need the causal test
+
+  for (int ib = 0; ib < nblk; ib += 2) {
+    const int kb = ib * kBlock;
+    int32_t b0 = btab[ib];
+    const bool has1 = ib + 1 < nblk;
+    int32_t b1 = has1 ? btab[ib + 1] : b0;
+    const int rem = kv_len - kb;
+    int lim0 = rem < kBlock ? rem : kBlock;
+    int lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
+    if (b0 < 0 || b0 >= num_blocks) { b0 = 0; lim0 = 0; }
+    if (b1 < 0 || b1 >= num_blocks) { b1 = 0; lim1 = 0; }
+
+    const uint16_t* k0 = kc + ((int64_t)b0 * Hkv + kvh) * head_stride + c * D + 8 * j;
+    const uint16_t* k1 = kc + ((int64_t)b1 * Hkv + kvh) * head_stride + c * D + 8 * j;
+    bf16x8 ka[KS], kb8[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      ka[s] = *reinterpret_cast<const bf16x8*>(k0 + 32 * s);
+      kb8[s] = *reinterpret_cast<const bf16x8*>(k1 + 32 * s);
+    }
+    const uint16_t* v0 = vc + ((int64_t)b0 * Hkv + kvh) * head_stride + c * kBlock + 4 * j;
+    const uint16_t* v1 = vc + ((int64_t)b1 * Hkv + kvh) * head_stride + c * kBlock + 4 * j;
+    uint64_t va[DT], vb[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      va[dt] = *reinterpret_cast<const uint64_t*>(v0 + dt * 16 * kBlock);
+      vb[dt] = *reinterpret_cast<const uint64_t*>(v1 + dt * 16 * kBlock);
+    }
+    const bool partial = lim0 < kBlock || lim1 < kBlock;
+    if (partial) {
+      const int n0 = min(max(lim0 - 4 * j, 0), 4), n1 = min(max(lim1 - 4 * j, 0), 4);
+      const uint64_t mk0 = n0 >= 4 ? ~0ull : ((1ull << (16 * n0)) - 1);
+      const uint64_t mk1 = n1 >= 4 ? ~0ull : ((1ull << (16 * n1)) - 1);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        va[dt] &= mk0;
+        vb[dt] &= mk1;
+      }
+    }
+    const bool diag = kb + 2 * kBlock - 1 > diag_key;  // wave-uniform
+
+    bf16x8 pb[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qv[nt][s], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb8[s], qv[nt][s], s1, 0, 0, 0);
+      }
+      float x[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = s0[r] * scale_log2;
+        x[4 + r] = s1[r] * scale_log2;
+      }
+      if (partial || diag) {
+        const int row_pos = past + row0 + 16 * nt + c;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int k_a = kb + 4 * j + r, k_b = k_a + kBlock;
+          if (4 * j + r >= lim0 || k_a > row_pos) x[r] = -INFINITY;
+          if (4 * j + r >= lim1 || k_b > row_pos) x[4 + r] = -INFINITY;
+        }
+      }
+      float bm = x[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) bm = fmaxf(bm, x[i]);
+      bm = fmaxf(bm, shfl_xor_f(bm, 16));
+      bm = fmaxf(bm, shfl_xor_f(bm, 32));
+      if (__builtin_amdgcn_ballot_w64(bm > m[nt] + 8.0f)) {
+        const float mn = fmaxf(m[nt], bm);
+        const float a = fast_exp2(m[nt] - mn);
+        m[nt] = mn;
+        lsum[nt] *= a;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[nt][dt] *= a;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p = fast_exp2(x[i] - m[nt]);
+        lsum[nt] += p;
+        pb[nt][i] = (__bf16)p;
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint64_t pair[2] = {va[dt], vb[dt]};
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(pair);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[nt], o[nt][dt], 0, 0, 0);
+    }
+  }
+
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float l = lsum[nt];
+    l += shfl_xor_f(l, 16);
+    l += shfl_xor_f(l, 32);
+    const int row = row0 + 16 * nt + c;
+    if (row >= qlen) continue;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* orow = out + ((int64_t)(q_begin + row) * Hq + h) * D + 4 * j;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      uint16_t w[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = f32_to_bf16_bits(o[nt][dt][r] * inv);
+      *reinterpret_cast<uint64_t*>(orow + 16 * dt) = *reinterpret_cast<const uint64_t*>(w);
+    }
+  }
+}
+
+// Generic: one wavefront per (query row, head); keys in chunks of 64 with
+// an online softmax; lane d accumulates output dims d, d + 64, ...
+template <typename T>
+__global__ __launch_bounds__(64) void prefill_generic_kernel(
+    T* __restrict__ out, const T* __restrict__ q, const T* __restrict__ kc,
+    const T* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
+    int D, int num_blocks, float scale_log2) {
+  __shared__ float qs[512];
+  __shared__ float ps[64];
+  __shared__ int32_t bids[64];
+  const int row = blockIdx.x, h = blockIdx.y, seq = blockIdx.z, lane = threadIdx.x;
+  const int q_begin = cu_q[seq];
+  if (row >= cu_q[seq + 1] - q_begin) return;
+  const int G = Hq / Hkv, kvh = h / G;
+  const int pos = past_lens[seq] + row;
+  const int64_t qoff = ((int64_t)(q_begin + row) * Hq + h) * D;
+  for (int d = lane; d < D; d += 64) qs[d] = Elem<T>::load(q + qoff + d);
+  float acc[8];
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  float m = kNegBig, l = 0.f;
+  for (int k0 = 0; k0 <= pos; k0 += 64) {
+    __syncthreads();
+    if (lane < 4) {
+      const int bi = k0 / kBlock + lane;
+      int32_t b = (bi < mbs) ? block_tables[(int64_t)seq * mbs + bi] : -1;
+      bids[lane] = (b >= 0 && b < num_blocks) ? b : -1;
+    }
+    __syncthreads();
+    const int key = k0 + lane;
+    float s = -INFINITY;
+    const int32_t b = bids[lane / kBlock];
+    if (key <= pos && b >= 0) {
+      const T* kr = kc + (((int64_t)b * Hkv + kvh) * kBlock + key % kBlock) * D;
+      float a = 0.f;
+      for (int d = 0; d < D; ++d) a += qs[d] * Elem<T>::load(kr + d);
+      s = a * scale_log2;
+    }
+    float bm = s;
+    for (int w = 32; w > 0; w >>= 1) bm = fmaxf(bm, __shfl_xor(bm, w, 64));
+    const float mn = fmaxf(m, bm);
+    const float alpha = exp2f(m - mn);
+    m = mn;
+    const float p = exp2f(s - m);
+    float ls = p;
+    for (int w = 32; w > 0; w >>= 1) ls += __shfl_xor(ls, w, 64);
+    l = l * alpha + ls;
+    ps[lane] = p;
+    __syncthreads();
+    const int nk = min(64, pos + 1 - k0);
+    for (int i = 0; i * 64 + lane < D; ++i) {
+      const int d = i * 64 + lane;
+      float a = acc[i] * alpha;
+      for (int t = 0; t < nk; ++t) {
+        const int32_t bt = bids[t / kBlock];
+        if (bt < 0) continue;
+        a += ps[t] * Elem<T>::load(vc + (((int64_t)bt * Hkv + kvh) * D + d) * kBlock +
+                                   (k0 + t) % kBlock);
+      }
+      acc[i] = a;
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  for (int i = 0; i * 64 + lane < D; ++i)
+    Elem<T>::store(out + qoff + i * 64 + lane, acc[i] * inv);
+}
+
+}  // namespace
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, int32_t max_blocks_per_seq,
+                              const int32_t* cu_q_lens, const int32_t* past_lens,
+                              int32_t num_seqs, int32_t total_q, int32_t max_q_len,
+                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int32_t num_blocks, float scale, int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_prefill: unknown dtype %d", dtype);
+  PA_REQUIRE(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_heads > 0 &&
+                 num_kv_heads > 0 && head_dim > 0 && num_blocks > 0 && max_blocks_per_seq > 0,
+             PA_ERR_INVALID_ARG, "pa_prefill: bad sizes");
+  PA_REQUIRE(num_heads % num_kv_heads == 0, PA_ERR_INVALID_ARG,
+             "pa_prefill: num_heads %d not a multiple of num_kv_heads %d", num_heads,
+             num_kv_heads);
+  PA_REQUIRE(head_dim <= 512, PA_ERR_UNSUPPORTED, "pa_prefill: head_dim %d > 512", head_dim);
+  if (num_seqs == 0 || total_q == 0 || max_q_len == 0) return PA_OK;
+  PA_REQUIRE(out && q && k_cache && v_cache && block_tables && cu_q_lens && past_lens,
+             PA_ERR_INVALID_ARG, "pa_prefill: null pointer");
+  const float scale_log2 = scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  const bool mfma =
+      dtype == PA_DTYPE_BF16 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
+  if (mfma) {
+    constexpr int NT = 2;
+    const int rows_per_wg = 16 * NT * kWaves;
+    const dim3 grid((max_q_len + rows_per_wg - 1) / rows_per_wg, num_heads, num_seqs);
+    auto* o = (uint16_t*)out;
+    auto* qq = (const uint16_t*)q;
+    auto* kc = (const uint16_t*)k_cache;
+    auto* vc = (const uint16_t*)v_cache;
+#define PA_LAUNCH_PREFILL(DD)                                                                 \
+  prefill_mfma_kernel<DD, NT><<<grid, 64 * kWaves, 0, s>>>(                                   \
+      o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,       \
+      num_kv_heads, num_blocks, scale_log2)
+    if (head_dim == 64)
+      PA_LAUNCH_PREFILL(64);
+    else if (head_dim == 128)
+      PA_LAUNCH_PREFILL(128);
+    else
+      PA_LAUNCH_PREFILL(256);
+#undef PA_LAUNCH_PREFILL
+  } else {
+    const dim3 grid(max_q_len, num_heads, num_seqs);
+    if (dtype == PA_DTYPE_BF16)
+      prefill_generic_kernel<uint16_t><<<grid, 64, 0, s>>>(
+          (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
+          block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
+          head_dim, num_blocks, scale_log2);
+    else
+      prefill_generic_kernel<float><<<grid, 64, 0, s>>>(
+          (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,
+          block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
+          head_dim, num_blocks, scale_log2);
+  }
+  return check_launch("pa_prefill");
+}

@@ -1,0 +1,147 @@
+"""PagedKvCache: Python face of the C++ cache mirror (pa_kv_cache_*).
+
+Method names and argument meanings follow the reference's PagedKvCache
+(crates/model/src/paged_tensor/tensor_store/{mod.rs,buffer.rs}) and the
+paged_gqa free functions (crates/model/src/components/attention/
+paged_gqa.rs:29-112); failures the reference reports as Err raise PaError.
+Index arguments are host-side lists; K/V payloads are device tensors in the
+cache dtype, laid out [T, H, D] (one token: [H, D] or [1, H, D]).
+"""
+import ctypes as C
+
+import torch
+
+from . import _lib
+from .ops import BLOCK_SIZE, PaError, _DTYPES, _check
+
+_DT_BACK = {v: k for k, v in _DTYPES.items()}
+
+
+def _i64_array(xs):
+    xs = [int(x) for x in xs]
+    return (C.c_int64 * max(len(xs), 1))(*xs), len(xs)
+
+
+class PagedKvCache:
+    def __init__(self, num_layers, num_heads, head_dim, num_blocks, dtype=torch.float32,
+                 device="cuda"):
+        self._lib = _lib.load()
+        self.device = torch.device(device)
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        self.dtype = dtype
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        h = C.c_void_p()
+        with torch.cuda.device(self.device):
+            _check("pa_kv_cache_create", self._lib.pa_kv_cache_create(
+                num_layers, num_heads, head_dim, num_blocks, _DTYPES[dtype], C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            self._lib.pa_kv_cache_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # accessors -----------------------------------------------------------
+    def num_layers(self):
+        return self._lib.pa_kv_cache_num_layers(self._h)
+
+    def num_blocks(self):
+        return self._lib.pa_kv_cache_num_blocks(self._h)
+
+    def block_size(self):
+        return self._lib.pa_kv_cache_block_size(self._h)
+
+    def key_cache(self, layer):
+        """Device tensor view of one layer's K cache [NB, H, 16, D]."""
+        return self._layer_tensor(self._lib.pa_kv_cache_key_ptr(self._h, layer),
+                                  (self.num_blocks(), self.num_heads, BLOCK_SIZE, self.head_dim))
+
+    def value_cache(self, layer):
+        """Device tensor view of one layer's V cache [NB, H, D, 16]."""
+        return self._layer_tensor(self._lib.pa_kv_cache_value_ptr(self._h, layer),
+                                  (self.num_blocks(), self.num_heads, self.head_dim, BLOCK_SIZE))
+
+    def _layer_tensor(self, ptr, shape):
+        if not ptr:
+            raise PaError("pa_kv_cache layer", -2, "layer out of bounds")
+        es = torch.empty(0, dtype=self.dtype).element_size()
+        n = 1
+        for s in shape:
+            n *= s
+        # Wrap the library-owned buffer without copying; the view must not
+        # outlive this cache.
+        iface = {"shape": (n * es,), "typestr": "|u1", "data": (ptr, False), "strides": None,
+                 "version": 3}
+
+        class _Buf:
+            __cuda_array_interface__ = iface
+
+        raw = torch.as_tensor(_Buf(), device=self.device)
+        return raw.view(self.dtype).view(shape)
+
+    # reference operations ------------------------------------------------
+    def _stream(self):
+        return C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def _payload(self, k, v, tokens=None):
+        """Checks a K/V pair the way write_kv / write_kv_batch do
+        (buffer.rs:139-165, :42-67): same shape, trailing dims [H, D], and
+        the expected token count; returns contiguous tensors and T."""
+        for x in (k, v):
+            if x.device != self.device or x.dtype != self.dtype:
+                raise ValueError("payload must be a device tensor in the cache dtype")
+        if tuple(k.shape) != tuple(v.shape):
+            raise ValueError(f"k and v must have same dimensions, got {tuple(k.shape)} vs "
+                             f"{tuple(v.shape)}")
+        if k.dim() < 2 or tuple(k.shape[-2:]) != (self.num_heads, self.head_dim):
+            raise ValueError(f"expected k shape [.., {self.num_heads}, {self.head_dim}], got "
+                             f"{tuple(k.shape)}")
+        t = k.numel() // (self.num_heads * self.head_dim)
+        if tokens is not None and t != tokens:
+            raise ValueError(f"expected {tokens} token(s), got {t}")
+        return k.contiguous(), v.contiguous(), t
+
+    def write_kv(self, layer_idx, block_id, token_offset, k, v):
+        """PagedKvCache::write_kv (buffer.rs:103-267)."""
+        k, v, _ = self._payload(k, v, 1)
+        _check("write_kv", self._lib.pa_kv_cache_write_kv(
+            self._h, layer_idx, block_id, token_offset, C.c_void_p(k.data_ptr()),
+            C.c_void_p(v.data_ptr()), self._stream()))
+
+    def write_kv_batch(self, layer_idx, block_id, token_offset, k_batch, v_batch):
+        """PagedKvCache::write_kv_batch (buffer.rs:27-95); k/v [T, H, D]."""
+        k, v, t = self._payload(k_batch, v_batch)
+        _check("write_kv_batch", self._lib.pa_kv_cache_write_kv_batch(
+            self._h, layer_idx, block_id, token_offset, C.c_void_p(k.data_ptr()),
+            C.c_void_p(v.data_ptr()), t, self._stream()))
+
+    def write_prefill_kv(self, layer_idx, block_ids, positions, seq_len, k, v):
+        """write_prefill_kv (paged_gqa.rs:29-63); k/v [seq_len, H, D]."""
+        k, v, _ = self._payload(k, v, seq_len)
+        ids, n_ids = _i64_array(block_ids)
+        pos, n_pos = _i64_array(positions)
+        _check("write_prefill_kv", self._lib.pa_kv_cache_write_prefill_kv(
+            self._h, layer_idx, ids, n_ids, pos, n_pos, seq_len, C.c_void_p(k.data_ptr()),
+            C.c_void_p(v.data_ptr()), self._stream()))
+
+    def read_kv(self, layer_idx, block_ids, seq_len):
+        """PagedKvCache::read_kv (buffer.rs:273-339) -> (k, v) [n, H, D]."""
+        ids, n_ids = _i64_array(block_ids)
+        cover = min(seq_len, n_ids * BLOCK_SIZE) if n_ids and seq_len > 0 else 0
+        out_k = torch.empty(cover, self.num_heads, self.head_dim, dtype=self.dtype,
+                            device=self.device)
+        out_v = torch.empty_like(out_k)
+        n = C.c_int32(0)
+        _check("read_kv", self._lib.pa_kv_cache_read_kv(
+            self._h, layer_idx, ids, n_ids, seq_len,
+            C.c_void_p(out_k.data_ptr()) if cover else None,
+            C.c_void_p(out_v.data_ptr()) if cover else None, C.byref(n), self._stream()))
+        return out_k[: n.value], out_v[: n.value]

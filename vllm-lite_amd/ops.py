@@ -1,0 +1,174 @@
+"""torch-tensor wrappers of the stateless C entry points of libpa.so.
+
+Tensors are passed by device pointer; work goes on the current HIP stream of
+the tensors' device.  Each wrapper checks dtype, device, contiguity and
+shape before calling, and raises PaError with the library's message when a
+call returns a non-zero status.
+"""
+import ctypes as C
+import math
+
+import torch
+
+from . import _lib
+
+BLOCK_SIZE = 16
+_DTYPES = {torch.float32: 0, torch.bfloat16: 1}
+
+
+class PaError(RuntimeError):
+    """A libpa entry point returned a negative pa_status."""
+
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} failed ({code}): {msg}")
+        self.code = code
+
+
+def _check(fn, rc):
+    if rc != 0:
+        raise PaError(fn, rc, _lib.load().pa_last_error().decode())
+
+
+def _stream(t):
+    return C.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _dev(*ts):
+    for t in ts:
+        if not (t.is_cuda and t.is_contiguous()):
+            raise ValueError("expected contiguous device tensors")
+
+
+def _dtype_code(t):
+    if t.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {t.dtype}")
+    return _DTYPES[t.dtype]
+
+
+def new_cache(num_blocks, num_kv_heads, head_dim, dtype, device="cuda"):
+    """Zeroed (k_cache [NB, H, 16, D], v_cache [NB, H, D, 16]) for one layer."""
+    k = torch.zeros(num_blocks, num_kv_heads, BLOCK_SIZE, head_dim, dtype=dtype, device=device)
+    v = torch.zeros(num_blocks, num_kv_heads, head_dim, BLOCK_SIZE, dtype=dtype, device=device)
+    return k, v
+
+
+def _cache_dims(k_cache, v_cache):
+    nb, h, bs, d = k_cache.shape
+    if bs != BLOCK_SIZE or tuple(v_cache.shape) != (nb, h, d, BLOCK_SIZE):
+        raise ValueError("caches must be K [NB, H, 16, D] and V [NB, H, D, 16]")
+    if k_cache.dtype != v_cache.dtype:
+        raise ValueError("K and V caches differ in dtype")
+    return nb, h, d
+
+
+def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
+    """Scatter key/value [T, H, D] into the caches at slot_mapping [T] (int64)."""
+    _dev(k_cache, v_cache, slot_mapping)
+    nb, h, d = _cache_dims(k_cache, v_cache)
+    t = key.shape[0]
+    if key.shape[1:] != (h, d) or value.shape != key.shape or slot_mapping.shape != (t,):
+        raise ValueError("key/value must be [T, H, D] matching the cache; slot_mapping [T]")
+    if slot_mapping.dtype != torch.int64 or key.dtype != k_cache.dtype or value.dtype != k_cache.dtype:
+        raise ValueError("dtype mismatch")
+    if key.stride(2) != 1 or key.stride(1) != d or value.stride(2) != 1 or value.stride(1) != d:
+        raise ValueError("key/value rows must be contiguous [H, D]")
+    lib = _lib.load()
+    _check("pa_reshape_and_cache", lib.pa_reshape_and_cache(
+        _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), t, h, d, nb,
+        key.stride(0), value.stride(0), _dtype_code(k_cache), _stream(k_cache)))
+
+
+def slot_mapping(block_tables, positions, cu_seq_tokens):
+    """Device slot mapping from block tables [B, MBS] (int32), positions [T]
+    (int64) and cumulative token counts [B + 1] (int32)."""
+    _dev(block_tables, positions, cu_seq_tokens)
+    b, mbs = block_tables.shape
+    out = torch.empty(positions.shape[0], dtype=torch.int64, device=positions.device)
+    lib = _lib.load()
+    _check("pa_slot_mapping", lib.pa_slot_mapping(
+        _ptr(block_tables), mbs, _ptr(positions), _ptr(cu_seq_tokens), b, positions.shape[0],
+        _ptr(out), _stream(positions)))
+    return out
+
+
+def read_kv(k_cache, v_cache, block_ids, seq_len):
+    """Gather one sequence's first seq_len tokens -> (k, v) [seq_len, H, D]."""
+    _dev(k_cache, v_cache, block_ids)
+    nb, h, d = _cache_dims(k_cache, v_cache)
+    out_k = torch.empty(seq_len, h, d, dtype=k_cache.dtype, device=k_cache.device)
+    out_v = torch.empty_like(out_k)
+    lib = _lib.load()
+    _check("pa_read_kv", lib.pa_read_kv(
+        _ptr(k_cache), _ptr(v_cache), _ptr(block_ids), block_ids.shape[0], seq_len, h, d, nb,
+        _ptr(out_k), _ptr(out_v), _dtype_code(k_cache), _stream(k_cache)))
+    return out_k, out_v
+
+
+def block_hash(k_cache, block_ids):
+    """Reference block-content hash of each listed block (f32 cache);
+    returns int64 holding the u64 bit patterns."""
+    _dev(k_cache, block_ids)
+    if k_cache.dtype != torch.float32:
+        raise ValueError("block_hash is defined on f32 caches")
+    nb, h, _, d = k_cache.shape
+    out = torch.empty(block_ids.shape[0], dtype=torch.int64, device=k_cache.device)
+    lib = _lib.load()
+    _check("pa_block_hash", lib.pa_block_hash(
+        _ptr(k_cache), _ptr(block_ids), block_ids.shape[0], h, d, nb, _ptr(out),
+        _stream(k_cache)))
+    return out
+
+
+def decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len):
+    return int(_lib.load().pa_decode_workspace_size(num_seqs, num_heads, head_dim,
+                                                     max_context_len))
+
+
+def decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len, scale=None,
+           out=None, workspace=None):
+    """Decode attention: q [B, Hq, D] -> out [B, Hq, D]."""
+    _dev(q, k_cache, v_cache, block_tables, context_lens)
+    nb, hkv, d = _cache_dims(k_cache, v_cache)
+    b, hq, dq = q.shape
+    if dq != d or q.dtype != k_cache.dtype:
+        raise ValueError("q must be [B, Hq, D] in the cache dtype")
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise ValueError("block_tables / context_lens must be int32")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.empty_like(q)
+    need = decode_workspace_size(b, hq, d, max_context_len)
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    lib = _lib.load()
+    _check("pa_decode", lib.pa_decode(
+        _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
+        block_tables.shape[1], _ptr(context_lens), max_context_len, b, hq, hkv, d, nb,
+        float(scale), _ptr(workspace), ws_bytes, _dtype_code(q), _stream(q)))
+    return out
+
+
+def prefill(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens, max_q_len, scale=None,
+            out=None):
+    """Chunked causal prefill: q [total_q, Hq, D] -> out [total_q, Hq, D]."""
+    _dev(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens)
+    nb, hkv, d = _cache_dims(k_cache, v_cache)
+    tq, hq, dq = q.shape
+    if dq != d or q.dtype != k_cache.dtype:
+        raise ValueError("q must be [total_q, Hq, D] in the cache dtype")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if out is None:
+        out = torch.empty_like(q)
+    lib = _lib.load()
+    _check("pa_prefill", lib.pa_prefill(
+        _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
+        block_tables.shape[1], _ptr(cu_q_lens), _ptr(past_lens), block_tables.shape[0], tq,
+        max_q_len, hq, hkv, d, nb, float(scale), _dtype_code(q), _stream(q)))
+    return out
