@@ -252,12 +252,35 @@ def cpu_baseline(w, budget_s=12.0):
                       "attention, OpenMP"}
 
 
+def copy_calibration(args):
+    """Plain 1 GiB device-to-device copy: the known-size reference for
+    scaling rocprof FETCH_SIZE / WRITE_SIZE, and the achievable-HBM check."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=DEV).random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    stop.record()
+    torch.cuda.synchronize()
+    t = start.elapsed_time(stop) / args.steps / 1e3
+    print(json.dumps({"config": "copy", "bytes_read": n, "bytes_written": n,
+                      "avg_launch_us": round(t * 1e6, 2),
+                      "gbs_read_plus_write": round(2 * n / t / 1e9, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="decode", choices=["decode", "prefill", "splitk", "qwen"])
+    ap.add_argument("--config", default="decode",
+                    choices=["decode", "prefill", "splitk", "qwen", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -267,6 +290,8 @@ def main():
 
     pa = _package()
     torch.cuda.set_device(0)
+    if args.config == "copy":
+        return copy_calibration(args)
     w = Workload(pa, args.config)
     for _ in range(args.warmup):
         w.step()

@@ -45,7 +45,8 @@ def run_prefill(pa, oracle, q, kc, vc, bt, cu, past, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (4, 4, 256)])
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (4, 4, 256), (8, 8, 128),
+                                      (16, 8, 64), (16, 2, 128), (28, 4, 128), (12, 4, 64)])
 def test_prefill_ragged(pa, oracle, dtype, hq, hkv, d):
     rng = np.random.default_rng(hq + d)
     pasts = [0, 16, 37, 5, 130]
@@ -86,3 +87,23 @@ def test_decode_equals_last_prefill_row(pa, oracle):
     dec = pa.decode(to_dev(q[-1:]), dk, dv, dbt, to_dev(np.array([350], np.int32)), 350)
     assert_close(dec.float().cpu().numpy(), pf[-1:].float().cpu().numpy(), 1e-2, 1e-2,
                  "decode vs prefill")
+
+
+def test_prefill_long_chunk_many_tiles(pa, oracle):
+    # several 64-key LDS tiles, query tiles of every wavefront, ragged end
+    rng = np.random.default_rng(5)
+    case = make_prefill_case(oracle, rng, [0, 333], [700, 290], 32, 8, 128, "bf16")
+    got, ref = run_prefill(pa, oracle, *case, "bf16")
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, "long chunk")
+
+
+def test_prefill_stale_nan_beyond_context(pa, oracle):
+    # keys past past+qlen in the last block hold NaN: must not leak
+    rng = np.random.default_rng(6)
+    q, kc, vc, bt, cu, past = make_prefill_case(oracle, rng, [7], [30], 8, 2, 128, "bf16")
+    last = bt[0, (7 + 30 - 1) // 16]
+    kc[last, :, (37 % 16):, :] = 0x7FC0
+    vc[last, :, (37 % 16):, :] = 0x7FC0
+    got, ref = run_prefill(pa, oracle, q, kc, vc, bt, cu, past, "bf16")
+    assert np.isfinite(got).all()
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, "stale NaN")

@@ -197,6 +197,258 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// LDS-tiled MFMA prefill (bf16, D in {64, 128}).
+//
+// Workgroup = 4 wavefronts sharing one kv head.  The keys are streamed in
+// tiles of 64 (4 cache blocks); each tile of K and V is copied HBM -> LDS
+// once per workgroup with global_load_lds (no register staging), double
+// buffered so the copy of tile t+1 overlaps the matrix work on tile t, and
+// then read by all four wavefronts.  Wavefront w owns 64 query rows (4 MFMA
+// column tiles) of one query head; with group size G the workgroup covers
+// min(G, 4) heads of the group x (256 / min(G, 4)) query tokens, so every K/V
+// byte brought into LDS feeds 256 query rows.
+//
+// LDS layouts (16-byte units, XOR-swizzled so the MFMA operand reads of 16
+// lanes hit distinct banks):
+//   K tile [64 keys][D]: key row r, 16-byte chunk ch stored at chunk
+//     position ch ^ (r % (D / 8)).
+//   V tile [4 blocks][D][16]: the two 16-byte halves of a 32-byte dim row d
+//     are swapped when bit 3 of d is set.
+//
+// Workgroup -> work mapping is XCD-aware: workgroups are dealt round-robin
+// to the 8 XCDs, so consecutive logical work items are remapped to the
+// same XCD; a logical chunk holds all query tiles of one kv head for all
+// sequences, and the tiles that share K/V then share that XCD's L2.  Within
+// a (sequence, head) the later (longer) query tiles go first.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_tiled_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
+    int num_blocks, float scale_log2, int B, int tiles_per_seq, int head_groups) {
+  constexpr int KS = D / 32;   // QK reduction steps
+  constexpr int DT = D / 16;   // PV output tiles
+  constexpr int CPR = D / 8;   // 16-byte chunks per K row
+  constexpr int KT = 64;       // keys per LDS tile
+  constexpr int NT = 4;        // 16-row column tiles per wavefront
+  constexpr int TILE_BYTES = KT * D * 2;  // one K (or V) tile
+  constexpr int DMA_PER_WAVE = TILE_BYTES / 1024 / 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2][2][TILE_BYTES];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, j = lane >> 4;
+  const int G = Hq / Hkv;
+  const int HW = G < 4 ? G : 4;        // heads per workgroup
+  const int TT = 64 * (4 / HW);        // query tokens per workgroup
+
+  // XCD-aware logical id.
+  const int total = B * Hkv * head_groups * tiles_per_seq;
+  const int per_xcd = (total + 7) / 8;
+  const int logical = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (logical >= total) return;
+  const int group = logical / tiles_per_seq;
+  const int tile = tiles_per_seq - 1 - logical % tiles_per_seq;
+  const int seq = group % B;
+  const int kvhg = group / B;
+  const int kvh = kvhg / head_groups, hg = kvhg % head_groups;
+
+  const int q_begin = cu_q[seq];
+  const int qlen = cu_q[seq + 1] - q_begin;
+  const int tok0 = tile * TT;
+  if (tok0 >= qlen) return;  // uniform over the workgroup
+  const int past = past_lens[seq];
+  const int key_end = min(past + min(qlen, tok0 + TT), mbs * kBlock);
+  const int n_kt = (key_end + KT - 1) / KT;
+  const int nblk = (key_end + kBlock - 1) / kBlock;
+
+  const int hl = wave % HW, tsub = wave / HW;
+  const int head_in_group = hg * 4 + hl;
+  const bool wave_active = wave < HW * (4 / HW) && head_in_group < G;
+  const int head = kvh * G + head_in_group;
+  const int r0 = tok0 + tsub * 64;  // first query row of this wavefront
+  const bool rows_active = wave_active && r0 < qlen;
+  const int wave_key_last = past + min(qlen, r0 + 64) - 1;  // last key any row needs
+
+  bf16x8 qv[NT][KS];
+  f32x4 o[NT][DT];
+  float m[NT], lsum[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int row = r0 + 16 * nt + c;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if (rows_active && row < qlen)
+        qv[nt][s] = *reinterpret_cast<const bf16x8*>(
+            q + ((int64_t)(q_begin + row) * Hq + head) * D + 32 * s + 8 * j);
+      else
+        qv[nt][s] = bf16x8{};
+    }
+    m[nt] = kNegBig;
+    lsum[nt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int32_t* btab = block_tables + (int64_t)seq * mbs;
+  const int64_t head_stride = (int64_t)kBlock * D;
+
+  // Issues this wavefront's share of the HBM -> LDS copies of key tile kt.
+  // Every index that selects a block is wave-uniform (scalar loads of the
+  // block table); only the within-block offsets vary per lane.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto block_id = [&](int bi) -> int32_t {
+    int32_t blk = bi < nblk ? btab[bi] : 0;
+    return (blk >= 0 && blk < num_blocks) ? blk : 0;
+  };
+  auto issue_tile = [&](int kt, int buf) {
+    constexpr int RPI = 64 / CPR;  // K rows per 1 KB chunk
+#pragma unroll
+    for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
+      const int i = wave_u * DMA_PER_WAVE + i0;  // 1 KB chunk of the tile
+      {
+        const int32_t blk = block_id(kt * (KT / kBlock) + (i * RPI) / kBlock);
+        const int r = i * RPI + lane / CPR;
+        const int ch = (lane % CPR) ^ (r % CPR);
+        const uint16_t* src =
+            kc + ((int64_t)blk * Hkv + kvh) * head_stride + (r % kBlock) * D + ch * 8;
+        __builtin_amdgcn_global_load_lds(
+            (const void*)src,
+            (__attribute__((address_space(3))) void*)(&smem[buf][0][i * 1024]), 16, 0, 0);
+      }
+      {
+        constexpr int CPB = D * 32 / 1024;  // 1 KB chunks per V block
+        const int32_t blk = block_id(kt * (KT / kBlock) + i / CPB);
+        const int d = (i % CPB) * 32 + lane / 2;
+        const int half = (lane & 1) ^ ((d >> 3) & 1);
+        const uint16_t* src = vc + ((int64_t)blk * Hkv + kvh) * head_stride + d * kBlock + half * 8;
+        __builtin_amdgcn_global_load_lds(
+            (const void*)src,
+            (__attribute__((address_space(3))) void*)(&smem[buf][1][i * 1024]), 16, 0, 0);
+      }
+    }
+  };
+
+  issue_tile(0, 0);
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int buf = kt & 1;
+    // Wait for this wavefront's copies of tile kt, then for everyone's.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    if (kt + 1 < n_kt) issue_tile(kt + 1, buf ^ 1);
+    if (!rows_active) continue;
+
+    const uint8_t* ks = &smem[buf][0][0];
+    const uint8_t* vs = &smem[buf][1][0];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int kb = kt * KT + half * 32;  // first key of this step
+      if (kb > wave_key_last) break;       // above the diagonal for every row
+      // Valid keys of the two 16-key blocks of this step (block ids outside
+      // the pool were redirected to block 0: mask them).
+      const int bi0 = kb / kBlock, bi1 = bi0 + 1;
+      int lim0 = min(max(key_end - kb, 0), kBlock);
+      int lim1 = min(max(key_end - kb - kBlock, 0), kBlock);
+      if (bi0 < nblk) { const int32_t b0 = btab[bi0]; if (b0 < 0 || b0 >= num_blocks) lim0 = 0; }
+      if (bi1 < nblk) { const int32_t b1 = btab[bi1]; if (b1 < 0 || b1 >= num_blocks) lim1 = 0; }
+      const bool partial = lim0 < kBlock || lim1 < kBlock;
+      const bool diag = kb + 31 > past + r0;
+
+      bf16x8 ka[2][KS];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int r = half * 32 + kk * 16 + c;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int ch = (4 * s + j) ^ (r % CPR);
+          ka[kk][s] = *reinterpret_cast<const bf16x8*>(ks + r * (D * 2) + ch * 16);
+        }
+      }
+      bf16x8 pb[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[0][s], qv[nt][s], s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[1][s], qv[nt][s], s1, 0, 0, 0);
+        }
+        float x[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          x[r] = s0[r] * scale_log2;
+          x[4 + r] = s1[r] * scale_log2;
+        }
+        if (partial || diag) {
+          const int row_pos = past + r0 + 16 * nt + c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int k_a = kb + 4 * j + r, k_b = k_a + kBlock;
+            if (4 * j + r >= lim0 || k_a > row_pos) x[r] = -INFINITY;
+            if (4 * j + r >= lim1 || k_b > row_pos) x[4 + r] = -INFINITY;
+          }
+        }
+        float bm = x[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) bm = fmaxf(bm, x[i]);
+        bm = fmaxf(bm, shfl_xor_f(bm, 16));
+        bm = fmaxf(bm, shfl_xor_f(bm, 32));
+        if (__builtin_amdgcn_ballot_w64(bm > m[nt] + 8.0f)) {
+          const float mn = fmaxf(m[nt], bm);
+          const float a = fast_exp2(m[nt] - mn);
+          m[nt] = mn;
+          lsum[nt] *= a;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) o[nt][dt] *= a;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p = fast_exp2(x[i] - m[nt]);
+          lsum[nt] += p;
+          pb[nt][i] = (__bf16)p;
+        }
+      }
+      uint64_t mk0 = ~0ull, mk1 = ~0ull;
+      if (partial) {
+        const int n0 = min(max(lim0 - 4 * j, 0), 4), n1 = min(max(lim1 - 4 * j, 0), 4);
+        mk0 = n0 >= 4 ? ~0ull : ((1ull << (16 * n0)) - 1);
+        mk1 = n1 >= 4 ? ~0ull : ((1ull << (16 * n1)) - 1);
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = 16 * dt + c;
+        const int u = (j ^ (((d >> 3) & 1) << 1)) * 8;
+        uint64_t pair[2];
+        pair[0] = *reinterpret_cast<const uint64_t*>(vs + (half * 2) * (D * 32) + d * 32 + u) & mk0;
+        pair[1] = *reinterpret_cast<const uint64_t*>(vs + (half * 2 + 1) * (D * 32) + d * 32 + u) & mk1;
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(pair);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[nt], o[nt][dt], 0, 0, 0);
+      }
+    }
+  }
+
+  if (!rows_active) return;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float l = lsum[nt];
+    l += shfl_xor_f(l, 16);
+    l += shfl_xor_f(l, 32);
+    const int row = r0 + 16 * nt + c;
+    if (row >= qlen) continue;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* orow = out + ((int64_t)(q_begin + row) * Hq + head) * D + 4 * j;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      uint16_t w[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = f32_to_bf16_bits(o[nt][dt][r] * inv);
+      *reinterpret_cast<uint64_t*>(orow + 16 * dt) = *reinterpret_cast<const uint64_t*>(w);
+    }
+  }
+}
+
 // Generic: one wavefront per (query row, head); keys in chunks of 64 with
 // an online softmax; lane d accumulates output dims d, d + 64, ...
 template <typename T>
@@ -289,9 +541,31 @@ extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, con
              PA_ERR_INVALID_ARG, "pa_prefill: null pointer");
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  const bool mfma =
-      dtype == PA_DTYPE_BF16 && (head_dim == 64 || head_dim == 128 || head_dim == 256);
-  if (mfma) {
+  const bool tiled = dtype == PA_DTYPE_BF16 && (head_dim == 64 || head_dim == 128);
+  const bool mfma = dtype == PA_DTYPE_BF16 && head_dim == 256;
+  if (tiled) {
+    const int G = num_heads / num_kv_heads;
+    const int HW = G < 4 ? G : 4;
+    const int TT = 64 * (4 / HW);
+    const int tiles_per_seq = (max_q_len + TT - 1) / TT;
+    const int head_groups = (G + 3) / 4;
+    const long long total = (long long)num_seqs * num_kv_heads * head_groups * tiles_per_seq;
+    PA_REQUIRE(total < (1ll << 31) / 8, PA_ERR_UNSUPPORTED, "pa_prefill: launch too large");
+    const int per_xcd = (int)((total + 7) / 8);
+    const dim3 grid(8 * per_xcd);
+    auto* o = (uint16_t*)out;
+    auto* qq = (const uint16_t*)q;
+    auto* kc = (const uint16_t*)k_cache;
+    auto* vc = (const uint16_t*)v_cache;
+    if (head_dim == 128)
+      prefill_tiled_kernel<128><<<grid, 256, 0, s>>>(
+          o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,
+          num_kv_heads, num_blocks, scale_log2, num_seqs, tiles_per_seq, head_groups);
+    else
+      prefill_tiled_kernel<64><<<grid, 256, 0, s>>>(
+          o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,
+          num_kv_heads, num_blocks, scale_log2, num_seqs, tiles_per_seq, head_groups);
+  } else if (mfma) {
     constexpr int NT = 2;
     const int rows_per_wg = 16 * NT * kWaves;
     const dim3 grid((max_q_len + rows_per_wg - 1) / rows_per_wg, num_heads, num_seqs);
@@ -303,12 +577,7 @@ extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, con
   prefill_mfma_kernel<DD, NT><<<grid, 64 * kWaves, 0, s>>>(                                   \
       o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,       \
       num_kv_heads, num_blocks, scale_log2)
-    if (head_dim == 64)
-      PA_LAUNCH_PREFILL(64);
-    else if (head_dim == 128)
-      PA_LAUNCH_PREFILL(128);
-    else
-      PA_LAUNCH_PREFILL(256);
+    PA_LAUNCH_PREFILL(256);
 #undef PA_LAUNCH_PREFILL
   } else {
     const dim3 grid(max_q_len, num_heads, num_seqs);
