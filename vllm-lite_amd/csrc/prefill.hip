@@ -200,17 +200,25 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
 // ---------------------------------------------------------------------------
 // LDS-tiled MFMA prefill (bf16, D in {64, 128}).
 //
-// Workgroup = 4 wavefronts sharing one kv head.  The keys are streamed in
-// tiles of 64 (4 cache blocks); each tile of K and V is copied HBM -> LDS
-// once per workgroup with global_load_lds (no register staging), double
-// buffered so the copy of tile t+1 overlaps the matrix work on tile t, and
-// then read by all four wavefronts.  Wavefront w owns 64 query rows (4 MFMA
-// column tiles) of one query head; with group size G the workgroup covers
-// min(G, 4) heads of the group x (256 / min(G, 4)) query tokens, so every K/V
-// byte brought into LDS feeds 256 query rows.
+// Workgroup = 16 / NT wavefronts sharing one kv head.  Keys are streamed in tiles
+// of 64 (4 cache blocks).  Each tile of K and V is copied HBM -> LDS once per
+// workgroup with global_load_lds (no register staging) into one of three
+// LDS buffers, two tiles ahead of use, and read by all wavefronts.
+// Wavefront w owns 16 * NT query rows (NT MFMA column tiles) of one query
+// head; with group size G the workgroup covers min(G, 4) heads of the group
+// x (256 / min(G, 4)) query tokens, so every K/V byte brought into LDS feeds
+// 256 query rows.  NT = 2 keeps a wavefront within 256 registers, so two
+// wavefronts share each SIMD and one's softmax overlaps the other's MFMAs.
 //
-// LDS layouts (16-byte units, XOR-swizzled so the MFMA operand reads of 16
-// lanes hit distinct banks):
+// Per wavefront the 32-key steps form a software pipeline: the Sᵀ = K·Qᵀ
+// products of step n + 1 are issued in the same basic block as the
+// exponentials and the Oᵀ += Vᵀ·Pᵀ products of step n, so the matrix core
+// works while the VALU computes the softmax.  The row max is kept stale
+// until a score exceeds it by 2^8; only then (rarely) is the exact max
+// formed across lanes and the accumulator rescaled.
+//
+// LDS layouts (16-byte units, XOR-swizzled so the operand reads of 16 lanes
+// hit distinct banks):
 //   K tile [64 keys][D]: key row r, 16-byte chunk ch stored at chunk
 //     position ch ^ (r % (D / 8)).
 //   V tile [4 blocks][D][16]: the two 16-byte halves of a 32-byte dim row d
@@ -221,8 +229,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
 // same XCD; a logical chunk holds all query tiles of one kv head for all
 // sequences, and the tiles that share K/V then share that XCD's L2.  Within
 // a (sequence, head) the later (longer) query tiles go first.
-template <int D>
-__global__ __launch_bounds__(256) void prefill_tiled_kernel(
+template <int D, int NT>
+__global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
@@ -231,12 +239,14 @@ __global__ __launch_bounds__(256) void prefill_tiled_kernel(
   constexpr int DT = D / 16;   // PV output tiles
   constexpr int CPR = D / 8;   // 16-byte chunks per K row
   constexpr int KT = 64;       // keys per LDS tile
-  constexpr int NT = 4;        // 16-row column tiles per wavefront
+  constexpr int W = 16 / NT;   // wavefronts per workgroup (64 query rows x 4 heads)
+  constexpr int NBUF = 3;      // LDS tile buffers
   constexpr int TILE_BYTES = KT * D * 2;  // one K (or V) tile
-  constexpr int DMA_PER_WAVE = TILE_BYTES / 1024 / 4;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2][2][TILE_BYTES];
+  constexpr int DMA_PER_WAVE = TILE_BYTES / 1024 / W;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NBUF][2][TILE_BYTES];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int c = lane & 15, j = lane >> 4;
   const int G = Hq / Hkv;
   const int HW = G < 4 ? G : 4;        // heads per workgroup
@@ -262,13 +272,15 @@ __global__ __launch_bounds__(256) void prefill_tiled_kernel(
   const int n_kt = (key_end + KT - 1) / KT;
   const int nblk = (key_end + kBlock - 1) / kBlock;
 
-  const int hl = wave % HW, tsub = wave / HW;
+  const int hl = wave_s % HW, tsub = wave_s / HW;
   const int head_in_group = hg * 4 + hl;
-  const bool wave_active = wave < HW * (4 / HW) && head_in_group < G;
+  const bool wave_active = wave_s < HW * (TT / (16 * NT)) && head_in_group < G;
   const int head = kvh * G + head_in_group;
-  const int r0 = tok0 + tsub * 64;  // first query row of this wavefront
+  const int r0 = tok0 + tsub * 16 * NT;  // first query row of this wavefront
   const bool rows_active = wave_active && r0 < qlen;
-  const int wave_key_last = past + min(qlen, r0 + 64) - 1;  // last key any row needs
+  const int wave_key_last = min(past + min(qlen, r0 + 16 * NT), key_end) - 1;  // last key needed
+  const int n_steps = 2 * n_kt;                                     // workgroup steps
+  const int wave_steps = rows_active ? min(n_steps, wave_key_last / 32 + 1) : 0;
 
   bf16x8 qv[NT][KS];
   f32x4 o[NT][DT];
@@ -293,23 +305,33 @@ __global__ __launch_bounds__(256) void prefill_tiled_kernel(
   const int32_t* btab = block_tables + (int64_t)seq * mbs;
   const int64_t head_stride = (int64_t)kBlock * D;
 
-  // Issues this wavefront's share of the HBM -> LDS copies of key tile kt.
   // Every index that selects a block is wave-uniform (scalar loads of the
   // block table); only the within-block offsets vary per lane.
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto block_valid = [&](int bi) -> bool {
+    if (bi >= nblk) return false;
+    const int32_t id = btab[bi];
+    return id >= 0 && id < num_blocks;
+  };
   auto block_id = [&](int bi) -> int32_t {
     int32_t blk = bi < nblk ? btab[bi] : 0;
     return (blk >= 0 && blk < num_blocks) ? blk : 0;
   };
+  // K row swizzle: 16-byte chunk ch of tile row r sits at chunk position
+  // ch ^ kswz(r).  The rows one QK operand read touches (see qk) differ in
+  // bits 0-1 and 3-4, which kswz spreads over distinct chunk positions.
+  auto kswz = [](int r) -> int {
+    return CPR >= 16 ? (r & 3) | (((r >> 3) & 3) << 2) : (r & 3) | (((r >> 3) & 1) << 2);
+  };
+  // Issues this wavefront's share of the HBM -> LDS copies of key tile kt.
   auto issue_tile = [&](int kt, int buf) {
     constexpr int RPI = 64 / CPR;  // K rows per 1 KB chunk
 #pragma unroll
     for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
-      const int i = wave_u * DMA_PER_WAVE + i0;  // 1 KB chunk of the tile
+      const int i = wave_s * DMA_PER_WAVE + i0;  // 1 KB chunk of the tile
       {
         const int32_t blk = block_id(kt * (KT / kBlock) + (i * RPI) / kBlock);
         const int r = i * RPI + lane / CPR;
-        const int ch = (lane % CPR) ^ (r % CPR);
+        const int ch = (lane % CPR) ^ kswz(r);
         const uint16_t* src =
             kc + ((int64_t)blk * Hkv + kvh) * head_stride + (r % kBlock) * D + ch * 8;
         __builtin_amdgcn_global_load_lds(
@@ -328,105 +350,167 @@ __global__ __launch_bounds__(256) void prefill_tiled_kernel(
       }
     }
   };
-
-  issue_tile(0, 0);
-  for (int kt = 0; kt < n_kt; ++kt) {
-    const int buf = kt & 1;
-    // Wait for this wavefront's copies of tile kt, then for everyone's.
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    if (kt + 1 < n_kt) issue_tile(kt + 1, buf ^ 1);
-    if (!rows_active) continue;
-
-    const uint8_t* ks = &smem[buf][0][0];
-    const uint8_t* vs = &smem[buf][1][0];
+  // A tile that reaches past the last key, or holds a block id outside the
+  // pool, has V entries that are not this sequence's data (any bits, NaN
+  // included).  Zero them in LDS once, after the tile has landed, so P·V
+  // needs no per-step masking (their P is 0 and 0 * 0 = 0).  Uniform over
+  // the workgroup; ends with a barrier when it writes.  Returns whether the
+  // tile needs key masking.
+  auto zero_stale = [&](int kt, int buf) -> bool {
+    bool special = kt * KT + KT > key_end;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int kb = kt * KT + half * 32;  // first key of this step
-      if (kb > wave_key_last) break;       // above the diagonal for every row
-      // Valid keys of the two 16-key blocks of this step (block ids outside
-      // the pool were redirected to block 0: mask them).
-      const int bi0 = kb / kBlock, bi1 = bi0 + 1;
-      int lim0 = min(max(key_end - kb, 0), kBlock);
-      int lim1 = min(max(key_end - kb - kBlock, 0), kBlock);
-      if (bi0 < nblk) { const int32_t b0 = btab[bi0]; if (b0 < 0 || b0 >= num_blocks) lim0 = 0; }
-      if (bi1 < nblk) { const int32_t b1 = btab[bi1]; if (b1 < 0 || b1 >= num_blocks) lim1 = 0; }
-      const bool partial = lim0 < kBlock || lim1 < kBlock;
-      const bool diag = kb + 31 > past + r0;
-
-      bf16x8 ka[2][KS];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int r = half * 32 + kk * 16 + c;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const int ch = (4 * s + j) ^ (r % CPR);
-          ka[kk][s] = *reinterpret_cast<const bf16x8*>(ks + r * (D * 2) + ch * 16);
-        }
+    for (int b = 0; b < KT / kBlock; ++b) {
+      const int bi = kt * (KT / kBlock) + b;
+      if (bi < nblk) special |= !block_valid(bi);
+    }
+    if (!special) return false;
+    uint16_t* vz = reinterpret_cast<uint16_t*>(&smem[buf][1][0]);
+    for (int e = threadIdx.x; e < KT * D; e += blockDim.x) {
+      const int key = e / D, d = e % D;
+      const int b = key / kBlock, t = key % kBlock;
+      const bool ok = kt * KT + key < key_end && block_valid(kt * (KT / kBlock) + b);
+      if (!ok) {
+        const int half = (t / 8) ^ ((d >> 3) & 1);
+        vz[(b * D + d) * kBlock + half * 8 + t % 8] = 0;
       }
-      bf16x8 pb[NT];
+    }
+    __syncthreads();
+    return true;
+  };
+  // Sᵀ for the 32 keys of step `st` of the tile in buffer `buf`.  MFMA tile
+  // kk's row i holds key 8 (i / 4) + 4 kk + i % 4 of the step, so the lane
+  // (c, j) that receives rows 4j .. 4j+3 of both tiles holds keys
+  // 8j .. 8j+7: eight consecutive keys of block j / 2.
+  auto qk = [&](int buf, int st, f32x4 (&S)[NT][2]) {
+    const uint8_t* ks = &smem[buf][0][0];
+    bf16x8 ka[2][KS];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < 2; ++kk) {
+      const int r = st * 32 + 8 * (c >> 2) + 4 * kk + (c & 3);
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[0][s], qv[nt][s], s0, 0, 0, 0);
-          s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[1][s], qv[nt][s], s1, 0, 0, 0);
-        }
-        float x[8];
+      for (int s = 0; s < KS; ++s) {
+        const int ch = (4 * s + j) ^ kswz(r);
+        ka[kk][s] = *reinterpret_cast<const bf16x8*>(ks + r * (D * 2) + ch * 16);
+      }
+    }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          x[r] = s0[r] * scale_log2;
-          x[4 + r] = s1[r] * scale_log2;
-        }
-        if (partial || diag) {
+    for (int nt = 0; nt < NT; ++nt) {
+      S[nt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      S[nt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        S[nt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[0][s], qv[nt][s], S[nt][0], 0, 0, 0);
+        S[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[1][s], qv[nt][s], S[nt][1], 0, 0, 0);
+      }
+    }
+  };
+
+  int buf = 0;              // LDS buffer of the current tile
+  bool tile_special;        // current tile needs key masking
+  // Prologue: tiles 0 and 1 in flight, wait for tile 0.
+  issue_tile(0, 0);
+  if (n_kt > 1) {
+    issue_tile(1, 1);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DMA_PER_WAVE) & 0xF) | (((2 * DMA_PER_WAVE) >> 4) << 14));
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  }
+  __syncthreads();
+  tile_special = zero_stale(0, 0);
+
+  f32x4 S0[NT][2], S1[NT][2];
+  if (wave_steps > 0) qk(0, 0, S0);
+
+  // One 32-key step: softmax of S (already computed), then in one basic
+  // block the P·V products of this step and the Sᵀ products of the next.
+  auto step = [&](int n, f32x4 (&S)[NT][2], f32x4 (&Snext)[NT][2]) {
+    const int kt = n >> 1, st = n & 1;
+    const bool act = n < wave_steps;
+    if (act) {
+      const int kb = n * 32;  // first key of this step; x[i] <-> key kb + 8j + i
+      if (tile_special || kb + 31 > past + r0) {
+        // keys past the end, in invalid blocks, or above a row's diagonal
+        const int blk_lim = block_valid(kb / kBlock + (j >> 1)) ? key_end : 0;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
           const int row_pos = past + r0 + 16 * nt + c;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int k_a = kb + 4 * j + r, k_b = k_a + kBlock;
-            if (4 * j + r >= lim0 || k_a > row_pos) x[r] = -INFINITY;
-            if (4 * j + r >= lim1 || k_b > row_pos) x[4 + r] = -INFINITY;
+          for (int i = 0; i < 8; ++i) {
+            const int key = kb + 8 * j + i;
+            if (key >= blk_lim || key > row_pos) S[nt][i >> 2][i & 3] = -INFINITY;
           }
         }
-        float bm = x[0];
+      }
+      float lm[NT];
+      bool need = false;
 #pragma unroll
-        for (int i = 1; i < 8; ++i) bm = fmaxf(bm, x[i]);
-        bm = fmaxf(bm, shfl_xor_f(bm, 16));
-        bm = fmaxf(bm, shfl_xor_f(bm, 32));
-        if (__builtin_amdgcn_ballot_w64(bm > m[nt] + 8.0f)) {
-          const float mn = fmaxf(m[nt], bm);
+      for (int nt = 0; nt < NT; ++nt) {
+        lm[nt] = fmaxf(fmaxf(fmaxf(S[nt][0][0], S[nt][0][1]), fmaxf(S[nt][0][2], S[nt][0][3])),
+                       fmaxf(fmaxf(S[nt][1][0], S[nt][1][1]), fmaxf(S[nt][1][2], S[nt][1][3])));
+        need |= __builtin_fmaf(lm[nt], scale_log2, -m[nt]) > 8.0f;
+      }
+      // Rows keep a stale max until one of their scores exceeds it by 2^8;
+      // only then is the exact max formed across the four lanes of the row
+      // and the accumulator rescaled.
+      if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float bm = lm[nt];
+          bm = fmaxf(bm, shfl_xor_f(bm, 16));
+          bm = fmaxf(bm, shfl_xor_f(bm, 32));
+          const float mn = fmaxf(m[nt], bm * scale_log2);
           const float a = fast_exp2(m[nt] - mn);
           m[nt] = mn;
           lsum[nt] *= a;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) o[nt][dt] *= a;
         }
+      }
+    }
+
+    // Tile boundary: the next tile has landed (all waves), and the buffer
+    // two tiles ahead is free again.
+    int next_buf = buf;
+    if (st == 1 && kt + 1 < n_kt) {
+      next_buf = buf == NBUF - 1 ? 0 : buf + 1;
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): only tile kt + 1 is in flight
+      __syncthreads();
+      if (kt + 2 < n_kt) issue_tile(kt + 2, next_buf == NBUF - 1 ? 0 : next_buf + 1);
+    }
+
+    if (act) {
+      bf16x8 pb[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float p = fast_exp2(x[i] - m[nt]);
+          const float p = fast_exp2(__builtin_fmaf(S[nt][i >> 2][i & 3], scale_log2, -m[nt]));
           lsum[nt] += p;
           pb[nt][i] = (__bf16)p;
         }
-      }
-      uint64_t mk0 = ~0ull, mk1 = ~0ull;
-      if (partial) {
-        const int n0 = min(max(lim0 - 4 * j, 0), 4), n1 = min(max(lim1 - 4 * j, 0), 4);
-        mk0 = n0 >= 4 ? ~0ull : ((1ull << (16 * n0)) - 1);
-        mk1 = n1 >= 4 ? ~0ull : ((1ull << (16 * n1)) - 1);
-      }
+      // Vᵀ operand: dims 16 dt + c, keys 8j .. 8j+7 = one 16-byte half of
+      // the 32-byte row of block 2 st + j / 2.
+      const uint8_t* vrow = &smem[buf][1][0] + (2 * st + (j >> 1)) * (D * 32) + c * 32;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int d = 16 * dt + c;
-        const int u = (j ^ (((d >> 3) & 1) << 1)) * 8;
-        uint64_t pair[2];
-        pair[0] = *reinterpret_cast<const uint64_t*>(vs + (half * 2) * (D * 32) + d * 32 + u) & mk0;
-        pair[1] = *reinterpret_cast<const uint64_t*>(vs + (half * 2 + 1) * (D * 32) + d * 32 + u) & mk1;
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(pair);
+        const bf16x8 va = *reinterpret_cast<const bf16x8*>(
+            vrow + dt * 16 * 32 + (((j & 1) ^ ((d >> 3) & 1)) * 16));
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[nt], o[nt][dt], 0, 0, 0);
+          o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[nt], o[nt][dt], 0, 0, 0);
       }
+      if (n + 1 < wave_steps) qk(st == 0 ? buf : next_buf, st ^ 1, Snext);
     }
+    if (st == 1 && kt + 1 < n_kt) {
+      buf = next_buf;
+      tile_special = zero_stale(kt + 1, buf);
+    }
+  };
+
+  for (int kt = 0; kt < n_kt; ++kt) {
+    step(2 * kt, S0, S1);
+    step(2 * kt + 1, S1, S0);
   }
 
   if (!rows_active) return;
@@ -557,12 +641,13 @@ extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, con
     auto* qq = (const uint16_t*)q;
     auto* kc = (const uint16_t*)k_cache;
     auto* vc = (const uint16_t*)v_cache;
+    constexpr int NT = 2;
     if (head_dim == 128)
-      prefill_tiled_kernel<128><<<grid, 256, 0, s>>>(
+      prefill_tiled_kernel<128, NT><<<grid, 64 * (16 / NT), 0, s>>>(
           o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,
           num_kv_heads, num_blocks, scale_log2, num_seqs, tiles_per_seq, head_groups);
     else
-      prefill_tiled_kernel<64><<<grid, 256, 0, s>>>(
+      prefill_tiled_kernel<64, NT><<<grid, 64 * (16 / NT), 0, s>>>(
           o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,
           num_kv_heads, num_blocks, scale_log2, num_seqs, tiles_per_seq, head_groups);
   } else if (mfma) {
