@@ -215,7 +215,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
 // exponentials and the Oᵀ += Vᵀ·Pᵀ products of step n, so the matrix core
 // works while the VALU computes the softmax.  The row max is kept stale
 // until a score exceeds it by 2^8; only then (rarely) is the exact max
-// formed across lanes and the accumulator rescaled.
+// formed across lanes and the accumulator rescaled.  The softmax
+// denominators are accumulated by one more MFMA per column tile with an
+// all-ones operand, which keeps them off the VALU.
 //
 // LDS layouts (16-byte units, XOR-swizzled so the operand reads of 16 lanes
 // hit distinct banks):
@@ -228,7 +230,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
 // to the 8 XCDs, so consecutive logical work items are remapped to the
 // same XCD; a logical chunk holds all query tiles of one kv head for all
 // sequences, and the tiles that share K/V then share that XCD's L2.  Within
-// a (sequence, head) the later (longer) query tiles go first.
+// a chunk the sequences go from most to least work, and within a sequence
+// the later (longer) query tiles go first.
 template <int D, int NT>
 __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -257,10 +260,35 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   const int per_xcd = (total + 7) / 8;
   const int logical = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
   if (logical >= total) return;
-  const int group = logical / tiles_per_seq;
-  const int tile = tiles_per_seq - 1 - logical % tiles_per_seq;
-  const int seq = group % B;
-  const int kvhg = group / B;
+  // Logical order: kv head (group) major, then sequences from the most to
+  // the least attention work (so the tail is made of small sequences),
+  // then query tiles longest first.  Concurrent workgroups of one XCD then
+  // mostly stream the same sequence's K/V.  Every workgroup ranks the
+  // sequences the same way (work = q_len * (past + q_len / 2), ties by
+  // index); past 64 sequences the order is the index order.
+  const int kvhg = logical / (B * tiles_per_seq);
+  const int rem = logical % (B * tiles_per_seq);
+  const int tile = tiles_per_seq - 1 - rem % tiles_per_seq;
+  const int rank = rem / tiles_per_seq;
+  int seq = rank;
+  if (B <= 64) {
+    auto work = [&](int b) -> long long {
+      const long long ql = cu_q[b + 1] - cu_q[b];
+      return ql * (2 * (long long)past_lens[b] + ql);
+    };
+    for (int b = 0; b < B; ++b) {
+      const long long wb = work(b);
+      int r = 0;
+      for (int o2 = 0; o2 < B; ++o2) {
+        const long long wo = work(o2);
+        r += (wo > wb) || (wo == wb && o2 < b);
+      }
+      if (r == rank) {
+        seq = b;
+        break;
+      }
+    }
+  }
   const int kvh = kvhg / head_groups, hg = kvhg % head_groups;
 
   const int q_begin = cu_q[seq];
@@ -284,7 +312,8 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
 
   bf16x8 qv[NT][KS];
   f32x4 o[NT][DT];
-  float m[NT], lsum[NT];
+  f32x4 lacc[NT];  // softmax denominators, accumulated on the matrix core
+  float m[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int row = r0 + 16 * nt + c;
@@ -297,7 +326,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
         qv[nt][s] = bf16x8{};
     }
     m[nt] = kNegBig;
-    lsum[nt] = 0.f;
+    lacc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -322,32 +351,36 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   auto kswz = [](int r) -> int {
     return CPR >= 16 ? (r & 3) | (((r >> 3) & 3) << 2) : (r & 3) | (((r >> 3) & 1) << 2);
   };
+  // Per-lane element offsets of this wavefront's HBM -> LDS copies (the
+  // same for every tile) and the block each copy reads.
+  constexpr int RPI = 64 / CPR;        // K rows per 1 KB chunk
+  constexpr int CPB = D * 32 / 1024;   // 1 KB chunks per V block
+  int koff[DMA_PER_WAVE], voff[DMA_PER_WAVE], kblk[DMA_PER_WAVE], vblk[DMA_PER_WAVE];
+#pragma unroll
+  for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
+    const int i = wave_s * DMA_PER_WAVE + i0;  // 1 KB chunk of the tile
+    const int r = i * RPI + lane / CPR;
+    koff[i0] = (r % kBlock) * D + ((lane % CPR) ^ kswz(r)) * 8;
+    kblk[i0] = (i * RPI) / kBlock;
+    const int d = (i % CPB) * 32 + lane / 2;
+    voff[i0] = d * kBlock + ((lane & 1) ^ ((d >> 3) & 1)) * 8;
+    vblk[i0] = i / CPB;
+  }
   // Issues this wavefront's share of the HBM -> LDS copies of key tile kt.
   auto issue_tile = [&](int kt, int buf) {
-    constexpr int RPI = 64 / CPR;  // K rows per 1 KB chunk
 #pragma unroll
     for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
-      const int i = wave_s * DMA_PER_WAVE + i0;  // 1 KB chunk of the tile
-      {
-        const int32_t blk = block_id(kt * (KT / kBlock) + (i * RPI) / kBlock);
-        const int r = i * RPI + lane / CPR;
-        const int ch = (lane % CPR) ^ kswz(r);
-        const uint16_t* src =
-            kc + ((int64_t)blk * Hkv + kvh) * head_stride + (r % kBlock) * D + ch * 8;
-        __builtin_amdgcn_global_load_lds(
-            (const void*)src,
-            (__attribute__((address_space(3))) void*)(&smem[buf][0][i * 1024]), 16, 0, 0);
-      }
-      {
-        constexpr int CPB = D * 32 / 1024;  // 1 KB chunks per V block
-        const int32_t blk = block_id(kt * (KT / kBlock) + i / CPB);
-        const int d = (i % CPB) * 32 + lane / 2;
-        const int half = (lane & 1) ^ ((d >> 3) & 1);
-        const uint16_t* src = vc + ((int64_t)blk * Hkv + kvh) * head_stride + d * kBlock + half * 8;
-        __builtin_amdgcn_global_load_lds(
-            (const void*)src,
-            (__attribute__((address_space(3))) void*)(&smem[buf][1][i * 1024]), 16, 0, 0);
-      }
+      const int i = wave_s * DMA_PER_WAVE + i0;
+      const int32_t kb_id = block_id(kt * (KT / kBlock) + kblk[i0]);
+      const int32_t vb_id = block_id(kt * (KT / kBlock) + vblk[i0]);
+      const uint16_t* kbase = kc + ((int64_t)kb_id * Hkv + kvh) * head_stride;
+      const uint16_t* vbase = vc + ((int64_t)vb_id * Hkv + kvh) * head_stride;
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(kbase + koff[i0]),
+          (__attribute__((address_space(3))) void*)(&smem[buf][0][i * 1024]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(vbase + voff[i0]),
+          (__attribute__((address_space(3))) void*)(&smem[buf][1][i * 1024]), 16, 0, 0);
     }
   };
   // A tile that reaches past the last key, or holds a block id outside the
@@ -377,13 +410,12 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     __syncthreads();
     return true;
   };
-  // Sᵀ for the 32 keys of step `st` of the tile in buffer `buf`.  MFMA tile
+  // Sᵀ for the 32 keys of step `st` of the tile in buffer `b`.  MFMA tile
   // kk's row i holds key 8 (i / 4) + 4 kk + i % 4 of the step, so the lane
   // (c, j) that receives rows 4j .. 4j+3 of both tiles holds keys
   // 8j .. 8j+7: eight consecutive keys of block j / 2.
-  auto qk = [&](int buf, int st, f32x4 (&S)[NT][2]) {
-    const uint8_t* ks = &smem[buf][0][0];
-    bf16x8 ka[2][KS];
+  auto qk_load = [&](int b, int st, bf16x8 (&ka)[2][KS]) {
+    const uint8_t* ks = &smem[b][0][0];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int r = st * 32 + 8 * (c >> 2) + 4 * kk + (c & 3);
@@ -393,6 +425,8 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
         ka[kk][s] = *reinterpret_cast<const bf16x8*>(ks + r * (D * 2) + ch * 16);
       }
     }
+  };
+  auto qk_mfma = [&](const bf16x8 (&ka)[2][KS], f32x4 (&S)[NT][2]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       S[nt][0] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -418,14 +452,25 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   __syncthreads();
   tile_special = zero_stale(0, 0);
 
+  bf16x8 ones;  // all-ones MFMA operand for the row sums
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
   f32x4 S0[NT][2], S1[NT][2];
-  if (wave_steps > 0) qk(0, 0, S0);
+  if (wave_steps > 0) {
+    bf16x8 ka[2][KS];
+    qk_load(0, 0, ka);
+    qk_mfma(ka, S0);
+  }
 
   // One 32-key step: softmax of S (already computed), then in one basic
   // block the P·V products of this step and the Sᵀ products of the next.
   auto step = [&](int n, f32x4 (&S)[NT][2], f32x4 (&Snext)[NT][2]) {
     const int kt = n >> 1, st = n & 1;
     const bool act = n < wave_steps;
+    // K fragments of the next step: when it is in this tile they are read
+    // now, so the softmax prep below covers their LDS latency.
+    bf16x8 ka[2][KS];
+    if (act && st == 0) qk_load(buf, 1, ka);
     if (act) {
       const int kb = n * 32;  // first key of this step; x[i] <-> key kb + 8j + i
       if (tile_special || kb + 31 > past + r0) {
@@ -461,7 +506,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
           const float mn = fmaxf(m[nt], bm * scale_log2);
           const float a = fast_exp2(m[nt] - mn);
           m[nt] = mn;
-          lsum[nt] *= a;
+          lacc[nt] *= a;
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) o[nt][dt] *= a;
         }
@@ -479,28 +524,64 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     }
 
     if (act) {
+      // Operands first: this step's Vᵀ fragments and the next step's K
+      // fragments (dims 16 dt + c, keys 8j .. 8j+7 = one 16-byte half of
+      // the 32-byte row of block 2 st + j / 2).
+      const uint8_t* vrow = &smem[buf][1][0] + (2 * st + (j >> 1)) * (D * 32) + c * 32;
+      bf16x8 va[DT];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = 16 * dt + c;
+        va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 +
+                                                  (((j & 1) ^ ((d >> 3) & 1)) * 16));
+      }
+      // The next step's Sᵀ is computed even past this wavefront's last
+      // step (it is then unused): keeping it unconditional keeps this one
+      // basic block.  Its MFMAs are interleaved by hand with this step's
+      // exponentials, one MFMA then EPM exponentials, so the matrix core
+      // and the VALU of this wavefront work at the same time.  Consecutive
+      // MFMAs go to independent accumulators (s outer, (nt, kk) inner).
+      if (st == 1) qk_load(next_buf, 0, ka);
+      constexpr int NQK = 2 * KS * NT;  // next-step Sᵀ MFMAs
+      constexpr int NEXP = 8 * NT;      // exponentials per lane
+      constexpr int EPM = NEXP / NQK > 0 ? NEXP / NQK : 1;
+      float pv[NT][8];
+#pragma unroll
+      for (int g = 0; g < NQK; ++g) {
+        const int s_ = g / (2 * NT), q_ = g % (2 * NT), nt_ = q_ / 2, kk = q_ % 2;
+        Snext[nt_][kk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            ka[kk][s_], qv[nt_][s_], s_ == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : Snext[nt_][kk], 0,
+            0, 0);
+#pragma unroll
+        for (int e = 0; e < EPM; ++e) {
+          const int x = g * EPM + e;
+          if (x < NEXP) {
+            const int nt = x / 8, i = x % 8;
+            pv[nt][i] = fast_exp2(__builtin_fmaf(S[nt][i >> 2][i & 3], scale_log2, -m[nt]));
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int x = NQK * EPM; x < NEXP; ++x) {
+        const int nt = x / 8, i = x % 8;
+        pv[nt][i] = fast_exp2(__builtin_fmaf(S[nt][i >> 2][i & 3], scale_log2, -m[nt]));
+      }
       bf16x8 pb[NT];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float p = fast_exp2(__builtin_fmaf(S[nt][i >> 2][i & 3], scale_log2, -m[nt]));
-          lsum[nt] += p;
-          pb[nt][i] = (__bf16)p;
-        }
-      // Vᵀ operand: dims 16 dt + c, keys 8j .. 8j+7 = one 16-byte half of
-      // the 32-byte row of block 2 st + j / 2.
-      const uint8_t* vrow = &smem[buf][1][0] + (2 * st + (j >> 1)) * (D * 32) + c * 32;
+        for (int i = 0; i < 8; ++i) pb[nt][i] = (__bf16)pv[nt][i];
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int d = 16 * dt + c;
-        const bf16x8 va = *reinterpret_cast<const bf16x8*>(
-            vrow + dt * 16 * 32 + (((j & 1) ^ ((d >> 3) & 1)) * 16));
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[nt], o[nt][dt], 0, 0, 0);
-      }
-      if (n + 1 < wave_steps) qk(st == 0 ? buf : next_buf, st ^ 1, Snext);
+          o[nt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pb[nt], o[nt][dt], 0, 0, 0);
+      // Row sums of P: an all-ones operand makes every output row the sum
+      // over the 32 keys, from the same bf16 P the numerator uses.
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        lacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[nt], lacc[nt], 0, 0, 0);
     }
     if (st == 1 && kt + 1 < n_kt) {
       buf = next_buf;
@@ -516,9 +597,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   if (!rows_active) return;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    float l = lsum[nt];
-    l += shfl_xor_f(l, 16);
-    l += shfl_xor_f(l, 32);
+    const float l = lacc[nt][0];
     const int row = r0 + 16 * nt + c;
     if (row >= qlen) continue;
     const float inv = l > 0.f ? 1.f / l : 0.f;
