@@ -70,6 +70,24 @@ def test_config2_llama_shape_small_batch(pa, oracle):
     assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "config 2 shape")
 
 
+def test_config2_full_batch_long_partitions(pa, oracle):
+    # BASELINE config 2 at full size (B 64, ctx 4096): the launch uses
+    # 2048-token partitions.
+    rng = np.random.default_rng(11)
+    case = make_decode_case(rng, 64, 32, 8, 128, [4096] * 64, dtype="bf16", kv_scale=0.5)
+    got, _ = run_decode(pa, oracle, case, "bf16")
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "config 2 full")
+
+
+def test_long_ragged_contexts_512_partitions(pa, oracle):
+    # contexts past 8k with enough work items: 512-token partitions
+    rng = np.random.default_rng(12)
+    ctx = [9000, 8193, 5000, 1, 700, 8800, 9001, 4097]
+    case = make_decode_case(rng, 8, 32, 8, 128, ctx, dtype="bf16")
+    got, _ = run_decode(pa, oracle, case, "bf16")
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "512 partitions")
+
+
 def test_config4_shared_prefix_long_context(pa, oracle):
     # BASELINE config 4 pattern: log-uniform long contexts sharing a
     # 4096-token prefix (the same physical blocks in every table); B = 3.

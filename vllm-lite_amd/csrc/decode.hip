@@ -1,7 +1,8 @@
 // Single-token decode attention over the paged KV cache (pa_decode).
 //
 // Work split (flash-decoding): the context of each sequence is cut into
-// partitions of kPart tokens.  One workgroup handles one (partition,
+// partitions (kPart tokens, or longer for the MFMA kernel when that streams
+// faster; see choose_partition).  One workgroup handles one (partition,
 // kv head, sequence) and produces, for each query head of the group, the
 // running max m (log2 domain), the softmax denominator l and the
 // unnormalised output o[D].  A single-partition launch writes the final
@@ -25,7 +26,9 @@
 namespace pa {
 namespace {
 
-constexpr int kPart = 256;  // tokens per partition (16 blocks)
+// Tokens per partition.  The generic kernel always uses kPart; the MFMA
+// kernel picks a multiple of it per launch (choose_partition).
+constexpr int kPart = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;  // "no max yet": finite so 2^(x - m) never sees inf - inf
 
@@ -53,7 +56,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
-    float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+    float scale_log2, int num_parts, int part_len, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml) {
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
   const int lane = threadIdx.x;
@@ -62,7 +66,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
   // Clamp to what the block table can address so a bad length never reads
   // past the table.
   const int ctx = min(context_lens[seq], mbs * kBlock);
-  const int tok0 = part * kPart;
+  const int tok0 = part * part_len;
   if (tok0 >= ctx) {
     // Empty context: the output is defined as zeros.
     if (num_parts == 1 && c < G) {
@@ -71,7 +75,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
     }
     return;
   }
-  const int tok_end = min(ctx, tok0 + kPart);
+  const int tok_end = min(ctx, tok0 + part_len);
   const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;
 
   const int head = kvh * G + c;
@@ -152,14 +156,15 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
       }
     }
 
-    float bm = x[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) bm = fmaxf(bm, x[i]);
-    bm = fmaxf(bm, shfl_xor_f(bm, 16));
-    bm = fmaxf(bm, shfl_xor_f(bm, 32));
+    float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                     fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
     // Lazy rescale: keep the stale max unless a score exceeds it by more
-    // than 2^8, so p <= 256 and the accumulator is rescaled rarely.
+    // than 2^8, so p <= 256 and the accumulator is rescaled rarely.  Lanes
+    // of one head agree on m, so the exact (cross-lane) max is only needed
+    // then.
     if (__builtin_amdgcn_ballot_w64(bm > m + 8.0f)) {
+      bm = fmaxf(bm, shfl_xor_f(bm, 16));
+      bm = fmaxf(bm, shfl_xor_f(bm, 32));
       const float mn = fmaxf(m, bm);
       const float a = fast_exp2(m - mn);
       m = mn;
@@ -300,52 +305,70 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Partition merge: one workgroup per (query head, sequence).
+// Partition merge: one workgroup of 256 threads per (sequence, query head).
+// The partitions' (m, l) are reduced over the workgroup to M and L; thread
+// t then accumulates output dims of lane t % 64 over the partitions
+// p = t / 64, t / 64 + 4, ... (loads of four partitions in flight per
+// step), and the four partial sums are added through LDS.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(
     T* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-    const int32_t* __restrict__ context_lens, int Hq, int D, int num_parts) {
+    const int32_t* __restrict__ context_lens, int Hq, int D, int num_parts, int mbs,
+    int part_len) {
   __shared__ float wsh[1024];
-  __shared__ float red[256];
-  const int h = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x;
-  const int ctx = context_lens[seq];
-  const int np = min(num_parts, (ctx + kPart - 1) / kPart);
-  const int64_t row0 = ((int64_t)seq * Hq + h) * num_parts;
-  float mloc = -INFINITY;
-  for (int p = tid; p < np; p += blockDim.x) mloc = fmaxf(mloc, ws_ml[2 * (row0 + p)]);
-  red[tid] = mloc;
+  __shared__ float red[4][512];
+  __shared__ float ml[2][4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int row = blockIdx.x;  // seq * Hq + head
+  const int seq = row / Hq;
+  const int ctx = min(context_lens[seq], mbs * kBlock);
+  const int np = min(min(num_parts, (ctx + part_len - 1) / part_len), 1024);
+  const int64_t row0 = (int64_t)row * num_parts;
+  float M = -INFINITY;
+  for (int p = tid; p < np; p += 256) M = fmaxf(M, ws_ml[2 * (row0 + p)]);
+  for (int w = 32; w > 0; w >>= 1) M = fmaxf(M, __shfl_xor(M, w, 64));
+  if (lane == 0) ml[0][wave] = M;
   __syncthreads();
-  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
-    __syncthreads();
-  }
-  const float M = red[0];
-  __syncthreads();
-  float lloc = 0.f;
-  for (int p = tid; p < np; p += blockDim.x) {
+  M = fmaxf(fmaxf(ml[0][0], ml[0][1]), fmaxf(ml[0][2], ml[0][3]));
+  float L = 0.f;
+  for (int p = tid; p < np; p += 256) {
     const float w = exp2f(ws_ml[2 * (row0 + p)] - M);
-    if (p < 1024) wsh[p] = w;
-    lloc += w * ws_ml[2 * (row0 + p) + 1];
+    wsh[p] = w;
+    L += w * ws_ml[2 * (row0 + p) + 1];
   }
-  red[tid] = lloc;
+  for (int w = 32; w > 0; w >>= 1) L += __shfl_xor(L, w, 64);
+  if (lane == 0) ml[1][wave] = L;
   __syncthreads();
-  for (int w = blockDim.x / 2; w > 0; w >>= 1) {
-    if (tid < w) red[tid] += red[tid + w];
-    __syncthreads();
-  }
-  const float L = red[0];
+  L = ml[1][0] + ml[1][1] + ml[1][2] + ml[1][3];
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  for (int d = tid; d < D; d += blockDim.x) {
+  for (int d = lane; d < D; d += 64) {
     float acc = 0.f;
-    for (int p = 0; p < np; ++p) {
-      const float w = p < 1024 ? wsh[p] : exp2f(ws_ml[2 * (row0 + p)] - M);
-      acc += w * ws_o[(row0 + p) * D + d];
-    }
-    Elem<T>::store(out + ((int64_t)seq * Hq + h) * D + d, acc * inv);
+    for (int p = wave; p < np; p += 4) acc += wsh[p] * ws_o[(row0 + p) * D + d];
+    red[wave][d] = acc;
   }
+  __syncthreads();
+  for (int d = tid; d < D; d += 256)
+    Elem<T>::store(out + (int64_t)row * D + d,
+                   (red[0][d] + red[1][d] + red[2][d] + red[3][d]) * inv);
 }
 
-int num_partitions(int max_ctx) { return max_ctx <= 0 ? 1 : (max_ctx + kPart - 1) / kPart; }
+int num_partitions(int max_ctx, int part_len) {
+  return max_ctx <= 0 ? 1 : (max_ctx + part_len - 1) / part_len;
+}
+
+// Partition length for the MFMA kernel.  Measured on MI355X: contexts of a
+// few thousand tokens stream fastest with long partitions, about one
+// wavefront per SIMD (fewer partial results, no reduce-bound tail); long
+// and ragged contexts with 512-token partitions (several wavefronts per
+// SIMD balance the uneven lengths); small batches need short partitions to
+// fill the GPU at all.
+int choose_partition(int num_seqs, int num_kv_heads, int max_ctx) {
+  const long long units = (long long)num_seqs * num_kv_heads;
+  auto items = [&](int p) { return units * ((max_ctx + p - 1) / p); };
+  if (max_ctx <= 8192 && items(2048) >= 1024) return 2048;
+  if (items(512) >= 1024) return 512;
+  return kPart;
+}
 
 }  // namespace
 }  // namespace pa
@@ -354,7 +377,8 @@ using namespace pa;
 
 extern "C" size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
                                            int32_t max_context_len) {
-  const int np = num_partitions(max_context_len);
+  // Sized for the shortest partition any launch uses.
+  const int np = num_partitions(max_context_len, kPart);
   if (np <= 1 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
   return (size_t)num_seqs * num_heads * np * (head_dim + 2) * sizeof(float);
 }
@@ -379,21 +403,24 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
   if (num_seqs == 0 || max_context_len == 0) return PA_OK;
   PA_REQUIRE(out && q && k_cache && v_cache && block_tables && context_lens, PA_ERR_INVALID_ARG,
              "pa_decode: null pointer");
-  const int np = num_partitions(max_context_len);
+  const int G = num_heads / num_kv_heads;
+  const bool mfma = dtype == PA_DTYPE_BF16 && G <= 16 &&
+                    (head_dim == 64 || head_dim == 128 || head_dim == 256);
+  const int part_len = mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len) : kPart;
+  const int np = num_partitions(max_context_len, part_len);
+  PA_REQUIRE(np <= 1024, PA_ERR_UNSUPPORTED,
+             "pa_decode: context of %d tokens needs %d > 1024 partitions", max_context_len, np);
   float* ws_o = nullptr;
   float* ws_ml = nullptr;
   if (np > 1) {
-    const size_t need = pa_decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len);
+    const size_t need = (size_t)num_seqs * num_heads * np * (head_dim + 2) * sizeof(float);
     PA_REQUIRE(workspace && workspace_bytes >= need, PA_ERR_WORKSPACE,
                "pa_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
     ws_o = (float*)workspace;
     ws_ml = ws_o + (size_t)num_seqs * num_heads * np * head_dim;
   }
-  const int G = num_heads / num_kv_heads;
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  const bool mfma = dtype == PA_DTYPE_BF16 && G <= 16 &&
-                    (head_dim == 64 || head_dim == 128 || head_dim == 256);
   if (mfma) {
     const dim3 grid(np, num_kv_heads, num_seqs);
     auto* o = (uint16_t*)out;
@@ -403,7 +430,7 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
 #define PA_LAUNCH_MFMA(DD)                                                                      \
   decode_mfma_kernel<DD><<<grid, 64, 0, s>>>(o, qq, kc, vc, block_tables, max_blocks_per_seq,   \
                                              context_lens, num_heads, num_kv_heads, G,          \
-                                             num_blocks, scale_log2, np, ws_o, ws_ml)
+                                             num_blocks, scale_log2, np, part_len, ws_o, ws_ml)
     if (head_dim == 64)
       PA_LAUNCH_MFMA(64);
     else if (head_dim == 128)
@@ -426,12 +453,14 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
   }
   int32_t rc = check_launch("pa_decode");
   if (rc != PA_OK || np == 1) return rc;
-  const dim3 rgrid(num_heads, num_seqs);
+  const dim3 rgrid(num_seqs * num_heads);
   if (dtype == PA_DTYPE_BF16)
     decode_reduce_kernel<uint16_t><<<rgrid, 256, 0, s>>>((uint16_t*)out, ws_o, ws_ml,
-                                                         context_lens, num_heads, head_dim, np);
+                                                         context_lens, num_heads, head_dim, np,
+                                                         max_blocks_per_seq, part_len);
   else
     decode_reduce_kernel<float><<<rgrid, 256, 0, s>>>((float*)out, ws_o, ws_ml, context_lens,
-                                                      num_heads, head_dim, np);
+                                                      num_heads, head_dim, np,
+                                                      max_blocks_per_seq, part_len);
   return check_launch("pa_decode reduce");
 }
