@@ -194,6 +194,20 @@ class Workload:
         self.attend()
 
 
+def measured_traffic(config):
+    """HBM bytes per launch of the dominant call as last measured with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by the copy calibration),
+    from profiles/hbm_traffic.txt; None when that file has no entry."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        kv = dict(x.split("=", 1) for x in line.split() if "=" in x)
+        if kv.get("config") == config:
+            return int(kv["fetch_bytes"]) + int(kv["write_bytes"])
+    return None
+
+
 def time_attend(w, iters):
     """Average duration of the dominant launch (pa_decode / pa_prefill),
     HIP events on the stream the library launches on (torch's current)."""
@@ -309,7 +323,8 @@ def main():
         unit = "tokens/s"
         achieved = w.alg_bytes / t_attn / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(args.config),
                 "kernel": "pa_decode (decode_mfma_kernel + decode_reduce_kernel)",
                 "alg_bytes_per_launch": w.alg_bytes,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
@@ -321,8 +336,9 @@ def main():
         value = w.flops / t_attn / 1e12
         unit = "TFLOP/s"
         roof = {"bound": "mfma", "achieved": round(value, 2), "peak": BF16_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(value / BF16_PEAK_TFLOPS, 4), "traffic": None,
-                "kernel": "pa_prefill (prefill_mfma_kernel)", "flops_per_launch": w.flops,
+                "unit": "TFLOP/s", "frac": round(value / BF16_PEAK_TFLOPS, 4),
+                "traffic": measured_traffic(args.config),
+                "kernel": "pa_prefill (prefill_tiled_kernel)", "flops_per_launch": w.flops,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
     cpu = None if args.no_cpu else cpu_baseline(w)
     line = {
