@@ -224,7 +224,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
 //   K tile [64 keys][D]: key row r, 16-byte chunk ch stored at chunk
 //     position ch ^ (r % (D / 8)).
 //   V tile [4 blocks][D][16]: the two 16-byte halves of a 32-byte dim row d
-//     are swapped when bit 3 of d is set.
+//     are swapped when bits 2 and 3 of d differ.
 //
 // Workgroup -> work mapping is XCD-aware: workgroups are dealt round-robin
 // to the 8 XCDs, so consecutive logical work items are remapped to the
@@ -334,16 +334,34 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   const int32_t* btab = block_tables + (int64_t)seq * mbs;
   const int64_t head_stride = (int64_t)kBlock * D;
 
-  // Every index that selects a block is wave-uniform (scalar loads of the
-  // block table); only the within-block offsets vary per lane.
-  auto block_valid = [&](int bi) -> bool {
-    if (bi >= nblk) return false;
-    const int32_t id = btab[bi];
-    return id >= 0 && id < num_blocks;
+  // The 4 block ids of a key tile, fetched one tile ahead of their use
+  // (scalar loads, wave-uniform), with bit b of `valid` set when block b
+  // exists in the table and lies inside the pool.  Invalid ids read block 0
+  // and are masked.
+  struct TileIds {
+    int32_t id0, id1, id2, id3;
+    int valid;
   };
-  auto block_id = [&](int bi) -> int32_t {
-    int32_t blk = bi < nblk ? btab[bi] : 0;
-    return (blk >= 0 && blk < num_blocks) ? blk : 0;
+  auto fetch_ids = [&](int kt) -> TileIds {
+    TileIds t;
+    t.valid = 0;
+    int32_t raw[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int bi = kt * (KT / kBlock) + b;
+      raw[b] = bi < nblk ? btab[bi] : -1;
+      const bool ok = raw[b] >= 0 && raw[b] < num_blocks;
+      t.valid |= ok ? (1 << b) : 0;
+      raw[b] = ok ? raw[b] : 0;
+    }
+    t.id0 = raw[0];
+    t.id1 = raw[1];
+    t.id2 = raw[2];
+    t.id3 = raw[3];
+    return t;
+  };
+  auto pick = [](const TileIds& t, int b) -> int32_t {
+    return b == 0 ? t.id0 : b == 1 ? t.id1 : b == 2 ? t.id2 : t.id3;
   };
   // K row swizzle: 16-byte chunk ch of tile row r sits at chunk position
   // ch ^ kswz(r).  The rows one QK operand read touches (see qk) differ in
@@ -351,6 +369,10 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   auto kswz = [](int r) -> int {
     return CPR >= 16 ? (r & 3) | (((r >> 3) & 3) << 2) : (r & 3) | (((r >> 3) & 1) << 2);
   };
+  // V row swizzle: the two 16-byte halves of dim row d are swapped when
+  // bits 2 and 3 of d differ, so the 16 rows one operand read touches spread
+  // over all banks whether the LDS serves 8 or 16 lanes of 16 bytes a cycle.
+  auto vswz = [](int d) -> int { return ((d >> 2) ^ (d >> 3)) & 1; };
   // Per-lane element offsets of this wavefront's HBM -> LDS copies (the
   // same for every tile) and the block each copy reads.
   constexpr int RPI = 64 / CPR;        // K rows per 1 KB chunk
@@ -363,16 +385,16 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     koff[i0] = (r % kBlock) * D + ((lane % CPR) ^ kswz(r)) * 8;
     kblk[i0] = (i * RPI) / kBlock;
     const int d = (i % CPB) * 32 + lane / 2;
-    voff[i0] = d * kBlock + ((lane & 1) ^ ((d >> 3) & 1)) * 8;
+    voff[i0] = d * kBlock + ((lane & 1) ^ vswz(d)) * 8;
     vblk[i0] = i / CPB;
   }
   // Issues this wavefront's share of the HBM -> LDS copies of key tile kt.
-  auto issue_tile = [&](int kt, int buf) {
+  auto issue_tile = [&](const TileIds& t, int buf) {
 #pragma unroll
     for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
       const int i = wave_s * DMA_PER_WAVE + i0;
-      const int32_t kb_id = block_id(kt * (KT / kBlock) + kblk[i0]);
-      const int32_t vb_id = block_id(kt * (KT / kBlock) + vblk[i0]);
+      const int32_t kb_id = pick(t, kblk[i0]);
+      const int32_t vb_id = pick(t, vblk[i0]);
       const uint16_t* kbase = kc + ((int64_t)kb_id * Hkv + kvh) * head_stride;
       const uint16_t* vbase = vc + ((int64_t)vb_id * Hkv + kvh) * head_stride;
       __builtin_amdgcn_global_load_lds(
@@ -389,22 +411,17 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // needs no per-step masking (their P is 0 and 0 * 0 = 0).  Uniform over
   // the workgroup; ends with a barrier when it writes.  Returns whether the
   // tile needs key masking.
-  auto zero_stale = [&](int kt, int buf) -> bool {
-    bool special = kt * KT + KT > key_end;
-#pragma unroll
-    for (int b = 0; b < KT / kBlock; ++b) {
-      const int bi = kt * (KT / kBlock) + b;
-      if (bi < nblk) special |= !block_valid(bi);
-    }
+  auto zero_stale = [&](int kt, int buf, const TileIds& t) -> bool {
+    const bool special = kt * KT + KT > key_end || t.valid != (1 << (KT / kBlock)) - 1;
     if (!special) return false;
     uint16_t* vz = reinterpret_cast<uint16_t*>(&smem[buf][1][0]);
     for (int e = threadIdx.x; e < KT * D; e += blockDim.x) {
       const int key = e / D, d = e % D;
-      const int b = key / kBlock, t = key % kBlock;
-      const bool ok = kt * KT + key < key_end && block_valid(kt * (KT / kBlock) + b);
+      const int b = key / kBlock, t16 = key % kBlock;
+      const bool ok = kt * KT + key < key_end && ((t.valid >> b) & 1);
       if (!ok) {
-        const int half = (t / 8) ^ ((d >> 3) & 1);
-        vz[(b * D + d) * kBlock + half * 8 + t % 8] = 0;
+        const int half = (t16 / 8) ^ vswz(d);
+        vz[(b * D + d) * kBlock + half * 8 + t16 % 8] = 0;
       }
     }
     __syncthreads();
@@ -442,15 +459,18 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   int buf = 0;              // LDS buffer of the current tile
   bool tile_special;        // current tile needs key masking
   // Prologue: tiles 0 and 1 in flight, wait for tile 0.
-  issue_tile(0, 0);
+  TileIds ids_cur = fetch_ids(0);
+  TileIds ids_next = ids_cur, ids_next2 = ids_cur;
+  issue_tile(ids_cur, 0);
   if (n_kt > 1) {
-    issue_tile(1, 1);
+    ids_next = fetch_ids(1);
+    issue_tile(ids_next, 1);
     __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DMA_PER_WAVE) & 0xF) | (((2 * DMA_PER_WAVE) >> 4) << 14));
   } else {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   }
   __syncthreads();
-  tile_special = zero_stale(0, 0);
+  tile_special = zero_stale(0, 0, ids_cur);
 
   bf16x8 ones;  // all-ones MFMA operand for the row sums
 #pragma unroll
@@ -471,11 +491,13 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     // now, so the softmax prep below covers their LDS latency.
     bf16x8 ka[2][KS];
     if (act && st == 0) qk_load(buf, 1, ka);
+    // Block ids of the tile two ahead, loaded a step before they are needed.
+    if (st == 0 && kt + 2 < n_kt) ids_next2 = fetch_ids(kt + 2);
     if (act) {
       const int kb = n * 32;  // first key of this step; x[i] <-> key kb + 8j + i
       if (tile_special || kb + 31 > past + r0) {
         // keys past the end, in invalid blocks, or above a row's diagonal
-        const int blk_lim = block_valid(kb / kBlock + (j >> 1)) ? key_end : 0;
+        const int blk_lim = ((ids_cur.valid >> (2 * st + (j >> 1))) & 1) ? key_end : 0;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int row_pos = past + r0 + 16 * nt + c;
@@ -520,7 +542,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       next_buf = buf == NBUF - 1 ? 0 : buf + 1;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): only tile kt + 1 is in flight
       __syncthreads();
-      if (kt + 2 < n_kt) issue_tile(kt + 2, next_buf == NBUF - 1 ? 0 : next_buf + 1);
+      if (kt + 2 < n_kt) issue_tile(ids_next2, next_buf == NBUF - 1 ? 0 : next_buf + 1);
     }
 
     if (act) {
@@ -532,8 +554,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int d = 16 * dt + c;
-        va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 +
-                                                  (((j & 1) ^ ((d >> 3) & 1)) * 16));
+        va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 + (((j & 1) ^ vswz(d)) * 16));
       }
       // The next step's Sᵀ is computed even past this wavefront's last
       // step (it is then unused): keeping it unconditional keeps this one
@@ -585,7 +606,9 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     }
     if (st == 1 && kt + 1 < n_kt) {
       buf = next_buf;
-      tile_special = zero_stale(kt + 1, buf);
+      ids_cur = ids_next;
+      ids_next = ids_next2;
+      tile_special = zero_stale(kt + 1, buf, ids_cur);
     }
   };
 
