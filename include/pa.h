@@ -95,6 +95,47 @@ int32_t pa_slot_mapping(const int32_t* block_tables, int32_t max_blocks_per_seq,
                         int32_t num_seqs, int32_t num_tokens, int64_t* slot_mapping,
                         pa_stream_t stream);
 
+/* Rotary embedding fused with the cache write.  Token t (position
+ * positions[t], int64) has its query heads rotated in place in q
+ * [T, Hq, D] (token stride q_stride), its key heads rotated and written to
+ * the K cache at slot_mapping[t], and its value heads written to the V cache
+ * at the same slot (slots outside the pool write nothing; Q is still
+ * rotated).  Rotation of each head: with x1 = x[0:D/2], x2 = x[D/2:D],
+ * angle_i = positions[t] * inv_freq[i] (f32),
+ *   x1' = x1 cos - x2 sin,   x2' = x2 cos + x1 sin.
+ *   inv_freq  [D/2] f32 device array (see pa_rope_inv_freq).
+ * Strides of 0 mean contiguous.
+ * Replaces RoPE::apply_with_scaling on Q and K
+ * (crates/model/src/components/positional/rope.rs:171-174, 507-568)
+ * followed by the KV write of rope_gqa.rs:283-302 / paged_gqa.rs:29-63. */
+int32_t pa_rope_reshape_and_cache(void* q, int64_t q_stride, const void* key, int64_t key_stride,
+                                  const void* value, int64_t value_stride, void* k_cache,
+                                  void* v_cache, const int64_t* slot_mapping,
+                                  const int64_t* positions, const float* inv_freq,
+                                  int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t num_blocks, int32_t dtype,
+                                  pa_stream_t stream);
+
+typedef enum pa_rope_type {
+  PA_ROPE_DEFAULT = 0,
+  PA_ROPE_LINEAR = 1,
+  PA_ROPE_YARN = 2,
+  PA_ROPE_DYNAMIC = 3,
+  PA_ROPE_SU = 4
+} pa_rope_type;
+
+/* Host function: the RoPE inverse-frequency table out[D/2] (host memory)
+ * for the reference's scaling types (rope.rs:335-505): default
+ * theta^(-2i/D); linear divides by `factor`; YaRN uses
+ * theta * factor^(D/(D-2)); dynamic NTK recomputes the factor from
+ * cur_seq_len when it exceeds original_max_position; Su divides by
+ * short_factor / long_factor (host arrays of D/2, NULL = 1) on either side
+ * of the dimension whose wavelength first exceeds original_max_position.
+ * A factor within f32 epsilon of 1 keeps the default table. */
+int32_t pa_rope_inv_freq(int32_t head_dim, float theta, int32_t rope_type, float factor,
+                         int32_t original_max_position, int32_t cur_seq_len,
+                         const float* short_factor, const float* long_factor, float* out);
+
 /* ---------------------------------------------------------------------- */
 /* KV-cache read                                                          */
 /* ---------------------------------------------------------------------- */

@@ -48,6 +48,10 @@ def load():
                                                f32, i32, i32, i32, p]
         lib.oracle_quant_write_kv.argtypes = [p, p, p, i32, i32, i32, i64, i64, p, p]
         lib.oracle_quant_read_kv.argtypes = [p, p, p, i32, i32, i32, p, i32, i32, p, p]
+        lib.oracle_rope_inv_freq.argtypes = [i32, f32, i32, f32, i32, i32, p, p, p]
+        lib.oracle_rope_inv_freq.restype = None
+        lib.oracle_rope.argtypes = [p, i32, i32, i32, p, p, i32]
+        lib.oracle_rope.restype = None
         lib.oracle_f32_to_bf16.argtypes = [f32]
         lib.oracle_f32_to_bf16.restype = C.c_uint16
         _lib = lib
@@ -227,3 +231,28 @@ def quant_read_kv(k_cache, v_cache, scales, block_ids, seq_len):
     n = load().oracle_quant_read_kv(_p(k_cache), _p(v_cache), _p(scales), nb, h, d, _p(ids),
                                     len(ids), seq_len, _p(ok), _p(ov))
     return n, ok[: max(n, 0)], ov[: max(n, 0)]
+
+
+# ---- rotary embedding ------------------------------------------------------
+ROPE_TYPES = {"default": 0, "linear": 1, "yarn": 2, "dynamic": 3, "su": 4}
+
+
+def rope_inv_freq(head_dim, theta, rope_type="default", factor=1.0, original_max_position=0,
+                  cur_seq_len=0, short_factor=None, long_factor=None):
+    out = np.zeros(head_dim // 2, dtype=np.float32)
+    sf = None if short_factor is None else np.ascontiguousarray(short_factor, dtype=np.float32)
+    lf = None if long_factor is None else np.ascontiguousarray(long_factor, dtype=np.float32)
+    load().oracle_rope_inv_freq(head_dim, float(theta), ROPE_TYPES[rope_type], float(factor),
+                                int(original_max_position), int(cur_seq_len), _p(sf), _p(lf),
+                                _p(out))
+    return out
+
+
+def rope(x, positions, inv_freq):
+    """Rotate-half RoPE of x [T, H, D] (f32 or bf16 bits); returns a copy."""
+    x = np.array(x, copy=True)
+    t, h, d = x.shape
+    pos = np.ascontiguousarray(positions, dtype=np.int64)
+    inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    load().oracle_rope(_p(x), t, h, d, _p(pos), _p(inv), _code(x))
+    return x

@@ -513,3 +513,66 @@ int oracle_quant_read_kv(const float* k_cache, const float* v_cache, const float
   }
   return n;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Rotary position embedding                                               */
+/* ------------------------------------------------------------------------ */
+
+/* Inverse-frequency table of RoPE, crates/model/src/components/positional/
+ * rope.rs:335-505: default theta^(-2i/d) (:498-505); linear divides by the
+ * factor (:347-357); YaRN uses theta * factor^(d/(d-2)) (:367-392); dynamic
+ * NTK recomputes the factor from the current length (:405-443, scale =
+ * factor * cur/orig - (factor - 1) with one rounding); Su divides by
+ * short/long per-dim factors on either side of the wavelength boundary
+ * (:445-488).  Factors within f32 epsilon of 1 keep the default table.
+ * rope_type: 0 default, 1 linear, 2 yarn, 3 dynamic, 4 su. */
+void oracle_rope_inv_freq(int head_dim, float theta, int rope_type, float factor, int orig_max,
+                          int cur_seq_len, const float* short_factor, const float* long_factor,
+                          float* out) {
+  int half = head_dim / 2;
+  float th = theta;
+  int near_one = fabsf(factor - 1.0f) < 1.1920929e-07f;
+  if (rope_type == 2 && !near_one) {
+    float d = (float)head_dim;
+    th = theta * powf(factor, d / (d - 2.0f));
+  } else if (rope_type == 3 && orig_max > 0 && cur_seq_len > orig_max && !near_one) {
+    float scale = fmaf(factor, (float)cur_seq_len / (float)orig_max, -(factor - 1.0f));
+    float d = (float)head_dim;
+    th = theta * powf(scale, d / (d - 2.0f));
+  }
+  for (int i = 0; i < half; ++i) out[i] = powf(th, -2.0f * (float)i / (float)head_dim);
+  if (rope_type == 1 && !near_one)
+    for (int i = 0; i < half; ++i) out[i] = out[i] / factor;
+  if (rope_type == 4 && orig_max > 0) {
+    int boundary = half;
+    for (int i = 0; i < half; ++i)
+      if (2.0f * 3.14159265358979323846f / out[i] > (float)orig_max) {
+        boundary = i;
+        break;
+      }
+    for (int i = 0; i < half; ++i) {
+      const float* f = i < boundary ? short_factor : long_factor;
+      out[i] = out[i] / (f ? f[i] : 1.0f);
+    }
+  }
+}
+
+/* Rotate-half RoPE on x [T, H, D] (dtype), in place, token t at position
+ * positions[t].  crates/model/src/components/positional/rope.rs:507-568:
+ * angle = pos * inv_freq[i] (f32), x1' = x1 cos - x2 sin,
+ * x2' = x2 cos + x1 sin on the halves x1 = x[:D/2], x2 = x[D/2:]. */
+void oracle_rope(void* x, int T, int H, int D, const int64_t* positions, const float* inv_freq,
+                 int dtype) {
+  int half = D / 2;
+  for (int t = 0; t < T; ++t)
+    for (int h = 0; h < H; ++h) {
+      size_t base = ((size_t)t * H + h) * D;
+      for (int i = 0; i < half; ++i) {
+        float angle = (float)positions[t] * inv_freq[i];
+        float c = cosf(angle), s = sinf(angle);
+        float x1 = load_el(x, base + i, dtype), x2 = load_el(x, base + half + i, dtype);
+        store_el(x, base + i, x1 * c - x2 * s, dtype);
+        store_el(x, base + half + i, x2 * c + x1 * s, dtype);
+      }
+    }
+}

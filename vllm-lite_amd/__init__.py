@@ -17,6 +17,8 @@ from .ops import (
     prefill,
     read_kv,
     reshape_and_cache,
+    rope_inv_freq,
+    rope_reshape_and_cache,
     slot_mapping,
 )
 from .kv_cache import PagedKvCache
@@ -31,5 +33,7 @@ __all__ = [
     "prefill",
     "read_kv",
     "reshape_and_cache",
+    "rope_inv_freq",
+    "rope_reshape_and_cache",
     "slot_mapping",
 ]

@@ -21,6 +21,9 @@ SIGNATURES = {
                          _p, _sz, _i32, _p]),
     "pa_prefill": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                           _i32, _f32, _i32, _p]),
+    "pa_rope_reshape_and_cache": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i32,
+                                         _i32, _i32, _i32, _i32, _i32, _p]),
+    "pa_rope_inv_freq": (_i32, [_i32, _f32, _i32, _f32, _i32, _i32, _p, _p, _p]),
     "pa_kv_cache_create": (_i32, [_i32, _i32, _i32, _i32, _i32, C.POINTER(_p)]),
     "pa_kv_cache_destroy": (None, [_p]),
     "pa_kv_cache_num_layers": (_i32, [_p]),

@@ -172,3 +172,52 @@ def prefill(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens, max_q_len, 
         block_tables.shape[1], _ptr(cu_q_lens), _ptr(past_lens), block_tables.shape[0], tq,
         max_q_len, hq, hkv, d, nb, float(scale), _dtype_code(q), _stream(q)))
     return out
+
+
+ROPE_TYPES = {"default": 0, "linear": 1, "yarn": 2, "dynamic": 3, "su": 4}
+
+
+def rope_inv_freq(head_dim, theta, rope_type="default", factor=1.0, original_max_position=0,
+                  cur_seq_len=0, short_factor=None, long_factor=None):
+    """Host RoPE inverse-frequency table (numpy float32 [head_dim // 2])."""
+    import numpy as np
+
+    out = np.zeros(head_dim // 2, dtype=np.float32)
+
+    def arr(a):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        return a.ctypes.data_as(C.c_void_p)
+
+    sf = None if short_factor is None else np.ascontiguousarray(short_factor, dtype=np.float32)
+    lf = None if long_factor is None else np.ascontiguousarray(long_factor, dtype=np.float32)
+    lib = _lib.load()
+    _check("pa_rope_inv_freq", lib.pa_rope_inv_freq(
+        head_dim, float(theta), ROPE_TYPES[rope_type], float(factor), int(original_max_position),
+        int(cur_seq_len), arr(sf), arr(lf), out.ctypes.data_as(C.c_void_p)))
+    return out
+
+
+def rope_reshape_and_cache(q, key, value, k_cache, v_cache, slot_mapping, positions, inv_freq):
+    """Rotate q [T, Hq, D] in place; rotate key [T, Hkv, D] into the K cache
+    and copy value into the V cache at slot_mapping (int64); positions int64,
+    inv_freq float32 [D/2] on the device."""
+    _dev(k_cache, v_cache, slot_mapping, positions, inv_freq)
+    nb, h, d = _cache_dims(k_cache, v_cache)
+    t, hq, dq = q.shape
+    if dq != d or key.shape[1:] != (h, d) or value.shape != key.shape or key.shape[0] != t:
+        raise ValueError("q [T, Hq, D], key/value [T, Hkv, D] must match the cache")
+    if positions.shape != (t,) or slot_mapping.shape != (t,) or inv_freq.shape != (d // 2,):
+        raise ValueError("positions / slot_mapping [T], inv_freq [D/2]")
+    if positions.dtype != torch.int64 or slot_mapping.dtype != torch.int64 or \
+            inv_freq.dtype != torch.float32:
+        raise ValueError("positions / slot_mapping int64, inv_freq float32")
+    for x in (q, key, value):
+        if x.dtype != k_cache.dtype or not x.is_cuda or x.stride(2) != 1 or x.stride(1) != d:
+            raise ValueError("q/key/value rows must be contiguous [H, D] in the cache dtype")
+    lib = _lib.load()
+    _check("pa_rope_reshape_and_cache", lib.pa_rope_reshape_and_cache(
+        _ptr(q), q.stride(0), _ptr(key), key.stride(0), _ptr(value), value.stride(0),
+        _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), _ptr(positions), _ptr(inv_freq), t, hq,
+        h, d, nb, _dtype_code(k_cache), _stream(q)))
