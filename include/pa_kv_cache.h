@@ -38,6 +38,9 @@ void pa_kv_cache_destroy(pa_kv_cache* cache);
 int32_t pa_kv_cache_num_layers(const pa_kv_cache* cache);
 int32_t pa_kv_cache_num_blocks(const pa_kv_cache* cache);
 int32_t pa_kv_cache_block_size(const pa_kv_cache* cache);
+int32_t pa_kv_cache_num_heads(const pa_kv_cache* cache); /* kv heads */
+int32_t pa_kv_cache_head_dim(const pa_kv_cache* cache);
+int32_t pa_kv_cache_dtype(const pa_kv_cache* cache);
 /* Device base of one layer's K cache [NB, H, 16, D] / V cache [NB, H, D, 16];
  * NULL for a bad layer. */
 void* pa_kv_cache_key_ptr(pa_kv_cache* cache, int32_t layer);
@@ -77,6 +80,51 @@ int32_t pa_kv_cache_write_prefill_kv(pa_kv_cache* cache, int32_t layer, const in
 int32_t pa_kv_cache_read_kv(pa_kv_cache* cache, int32_t layer, const int64_t* block_ids,
                             int32_t n_ids, int32_t seq_len, void* out_k, void* out_v,
                             int32_t* n_read, pa_stream_t stream);
+
+/* ---------------------------------------------------------------------- */
+/* Batched step (replaces the per-sequence forward loop)                   */
+/* ---------------------------------------------------------------------- */
+
+/* One engine step's batch, built once and reused by every layer.  The
+ * reference runs attention one sequence at a time
+ * (crates/model/src/causal_lm/model/mod.rs:143-164 -> rope_gqa.rs:261-429);
+ * a pa_batch holds the device-side index arrays of all sequences so each
+ * layer is one scatter plus one attention launch. */
+typedef struct pa_batch pa_batch;
+
+int32_t pa_batch_create(pa_batch** out);
+void pa_batch_destroy(pa_batch* batch);
+
+/* Describes the step from the scheduler's per-sequence data (the Batch of
+ * crates/traits/src/types.rs:84-117), all host arrays:
+ *   num_tokens[s]     tokens fed this step (1 for decode)
+ *   num_computed[s]   tokens already in the cache (positions start here)
+ *   block_ids         all sequences' block tables concatenated (int64)
+ *   block_counts[s]   table length of sequence s
+ * Token rows of q / k / v / out are the sequences' tokens in order.
+ * Validates every table entry against num_blocks (PA_ERR_OUT_OF_BOUNDS) and
+ * that each table covers num_computed + num_tokens tokens.  Uploads the
+ * index arrays on `stream` and synchronises it before returning. */
+int32_t pa_batch_prepare(pa_batch* batch, int32_t num_seqs, const int32_t* num_tokens,
+                         const int32_t* num_computed, const int64_t* block_ids,
+                         const int32_t* block_counts, int32_t num_blocks, pa_stream_t stream);
+
+int32_t pa_batch_num_tokens(const pa_batch* batch);
+/* 1 when every sequence is a single-token decode step. */
+int32_t pa_batch_is_decode(const pa_batch* batch);
+
+/* One layer's attention for the prepared batch: writes the step's K / V
+ * into the cache (rotating K, and q in place, when inv_freq is non-NULL),
+ * then attends with pa_decode (all-decode batch) or pa_prefill (anything
+ * else; decode rows become one-row chunks) into out [T, Hq, D].
+ *   q [T, Hq, D] (rotated in place when inv_freq != NULL), key / value
+ *   [T, Hkv, D] with token strides (0 = contiguous), inv_freq [D/2] device
+ *   f32 or NULL, scale = attn_factor / sqrt(D).
+ * Allocates (once, grown on demand) the decode workspace. */
+int32_t pa_batch_attention(pa_batch* batch, pa_kv_cache* cache, int32_t layer, int32_t num_heads,
+                           void* q, int64_t q_stride, const void* key, int64_t key_stride,
+                           const void* value, int64_t value_stride, const float* inv_freq,
+                           float scale, void* out, pa_stream_t stream);
 
 #ifdef __cplusplus
 }

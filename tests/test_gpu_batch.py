@@ -1,0 +1,103 @@
+"""GPU parity of the batched step (pa_batch_*): an engine loop of mixed
+prefill chunks and decodes over several layers, each step's attention
+checked against the oracle run on its own cache."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import BF16_ATOL, BF16_RTOL, F32_ATOL, F32_RTOL, assert_close
+from test_gpu_cache_ops import DEV, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+# (sequence -> tokens fed) per step; a sequence's first step is its prefill
+# (chunked when it spans several steps), later single tokens are decodes.
+STEPS = [
+    {0: 40, 1: 20},
+    {0: 1, 1: 30},
+    {0: 1, 1: 1},
+    {0: 1, 1: 1, 2: 70},
+    {2: 1, 0: 1},
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("rope", [True, False])
+def test_engine_loop(pa, oracle, dtype, rope):
+    rng = np.random.default_rng(11 + rope)
+    layers, hq, hkv, d, nb = 2, 8, 2, 128, 48
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    cache = pa.PagedKvCache(layers, hkv, d, nb, tdt, DEV)
+    pool = list(rng.permutation(nb))
+    tables, computed = {}, {}
+    inv = oracle.rope_inv_freq(d, 1e4)
+    ref_k = [np.zeros((nb, hkv, 16, d), np.uint16 if dtype == "bf16" else np.float32)
+             for _ in range(layers)]
+    ref_v = [np.zeros_like(ref_k[0]) for _ in range(layers)]
+    batch = pa.StepBatch()
+    for step in STEPS:
+        seqs = list(step)
+        for s in seqs:
+            computed.setdefault(s, 0)
+            tables.setdefault(s, [])
+            while len(tables[s]) * 16 < computed[s] + step[s]:
+                tables[s].append(int(pool.pop()))
+        batch.prepare(cache, [step[s] for s in seqs], [computed[s] for s in seqs],
+                      [tables[s] for s in seqs])
+        t = sum(step.values())
+        assert batch.num_tokens() == t
+        assert batch.is_decode() == all(step[s] == 1 and computed[s] > 0 for s in seqs)
+        positions = np.concatenate([np.arange(computed[s], computed[s] + step[s])
+                                    for s in seqs]).astype(np.int64)
+        slots = np.concatenate([[tables[s][p // 16] * 16 + p % 16
+                                 for p in range(computed[s], computed[s] + step[s])]
+                                for s in seqs]).astype(np.int64)
+        mbs = max(len(tables[s]) for s in seqs)
+        bt = np.zeros((len(seqs), mbs), np.int32)
+        for i, s in enumerate(seqs):
+            bt[i, :len(tables[s])] = tables[s]
+        q_start = np.concatenate([[0], np.cumsum([step[s] for s in seqs])]).astype(np.int32)
+        past = np.array([computed[s] for s in seqs], np.int32)
+        for layer in range(layers):
+            qkv = rng.standard_normal((t, hq + 2 * hkv, d), dtype=np.float32)
+            if dtype == "bf16":
+                qkv = oracle.f32_to_bf16(qkv)
+            g = to_dev(qkv)
+            q = g[:, :hq].contiguous()
+            out = batch.attention(cache, layer, q, g[:, hq:hq + hkv], g[:, hq + hkv:],
+                                  to_dev(inv) if rope else None)
+            qr, kr = qkv[:, :hq], qkv[:, hq:hq + hkv]
+            if rope:
+                qr, kr = oracle.rope(qr, positions, inv), oracle.rope(kr, positions, inv)
+            oracle.reshape_and_cache(kr, qkv[:, hq + hkv:], ref_k[layer], ref_v[layer], slots)
+            want = oracle.paged_attention(np.ascontiguousarray(qr), ref_k[layer], ref_v[layer],
+                                          bt, q_start, past)
+            tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
+            got = to_np(out.float()) if dtype == "bf16" else to_np(out)
+            if dtype == "bf16":
+                want = oracle.bf16_to_f32(want)
+            assert_close(got, want, *tol, f"step {STEPS.index(step)} layer {layer}")
+            if not rope:
+                # the cache holds exactly what the oracle wrote
+                assert np.array_equal(to_np(cache.key_cache(layer)), ref_k[layer])
+                assert np.array_equal(oracle.v_to_ref(to_np(cache.value_cache(layer))),
+                                      ref_v[layer])
+        for s in seqs:
+            computed[s] += step[s]
+
+
+def test_prepare_rejects_bad_tables(pa):
+    cache = pa.PagedKvCache(1, 2, 64, 8, torch.bfloat16, DEV)
+    batch = pa.StepBatch()
+    with pytest.raises(pa.PaError, match="out of bounds"):
+        batch.prepare(cache, [3], [0], [[8]])
+    with pytest.raises(pa.PaError, match="table holds"):
+        batch.prepare(cache, [20], [0], [[1]])
+    batch.prepare(cache, [17], [0], [[1, 2]])
+    q = torch.zeros(17, 4, 64, dtype=torch.bfloat16, device=DEV)
+    kv = torch.zeros(17, 2, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(pa.PaError, match="layer_idx"):
+        batch.attention(cache, 1, q, kv, kv)
+    with pytest.raises(pa.PaError, match="multiple"):
+        batch.attention(cache, 0, torch.zeros(17, 3, 64, dtype=torch.bfloat16, device=DEV),
+                        kv, kv)

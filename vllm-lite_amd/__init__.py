@@ -21,12 +21,13 @@ from .ops import (
     rope_reshape_and_cache,
     slot_mapping,
 )
-from .kv_cache import PagedKvCache
+from .kv_cache import PagedKvCache, StepBatch
 
 __all__ = [
     "BLOCK_SIZE",
     "PaError",
     "PagedKvCache",
+    "StepBatch",
     "block_hash",
     "decode",
     "decode_workspace_size",

@@ -29,12 +29,22 @@ SIGNATURES = {
     "pa_kv_cache_num_layers": (_i32, [_p]),
     "pa_kv_cache_num_blocks": (_i32, [_p]),
     "pa_kv_cache_block_size": (_i32, [_p]),
+    "pa_kv_cache_num_heads": (_i32, [_p]),
+    "pa_kv_cache_head_dim": (_i32, [_p]),
+    "pa_kv_cache_dtype": (_i32, [_p]),
     "pa_kv_cache_key_ptr": (_p, [_p, _i32]),
     "pa_kv_cache_value_ptr": (_p, [_p, _i32]),
     "pa_kv_cache_write_kv": (_i32, [_p, _i32, _i64, _i64, _p, _p, _p]),
     "pa_kv_cache_write_kv_batch": (_i32, [_p, _i32, _i64, _i64, _p, _p, _i32, _p]),
     "pa_kv_cache_write_prefill_kv": (_i32, [_p, _i32, _p, _i32, _p, _i32, _i32, _p, _p, _p]),
     "pa_kv_cache_read_kv": (_i32, [_p, _i32, _p, _i32, _i32, _p, _p, C.POINTER(_i32), _p]),
+    "pa_batch_create": (_i32, [C.POINTER(_p)]),
+    "pa_batch_destroy": (None, [_p]),
+    "pa_batch_prepare": (_i32, [_p, _i32, _p, _p, _p, _p, _i32, _p]),
+    "pa_batch_num_tokens": (_i32, [_p]),
+    "pa_batch_is_decode": (_i32, [_p]),
+    "pa_batch_attention": (_i32, [_p, _p, _i32, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _f32,
+                                  _p, _p]),
 }
 
 _lib = None

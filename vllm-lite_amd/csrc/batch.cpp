@@ -1,0 +1,223 @@
+// Batched step orchestration (pa_batch_* in pa_kv_cache.h).
+//
+// The reference's CausalLm::forward_logits loops over sequences and, per
+// layer, over RopeGqaAttention::forward_{prefill, prefill_continue, decode}
+// (crates/model/src/causal_lm/model/mod.rs:143-164,
+//  crates/model/src/components/attention/rope_gqa.rs:261-429), which write
+// each token with write_kv and attend with dense candle matmuls.  Here the
+// step's index arrays (positions, slots, block tables, query offsets) are
+// built once on the host, uploaded once, and every layer runs one write
+// launch and one attention launch for the whole batch.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/pa_kv_cache.h"
+#include "pa_common.hpp"
+
+struct pa_kv_cache;  // layout shared with kv_cache.cpp through the accessors
+
+namespace {
+
+// Device buffer that only grows.
+struct DevBuf {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  int32_t ensure(size_t need) {
+    if (need <= bytes) return PA_OK;
+    if (ptr) (void)hipFree(ptr);
+    ptr = nullptr;
+    bytes = 0;
+    if (hipMalloc(&ptr, need) != hipSuccess) {
+      pa::set_error("pa_batch: device allocation of %zu bytes failed", need);
+      return PA_ERR_HIP;
+    }
+    bytes = need;
+    return PA_OK;
+  }
+  ~DevBuf() {
+    if (ptr) (void)hipFree(ptr);
+  }
+};
+
+}  // namespace
+
+struct pa_batch {
+  int num_seqs = 0, num_tokens = 0, max_blocks = 0, max_q = 0, max_ctx = 0, num_blocks = 0;
+  bool decode = false;
+  // device arrays
+  DevBuf positions, slots, tables, cu_q, past, ctx_lens, workspace;
+  // pinned staging
+  void* stage = nullptr;
+  size_t stage_bytes = 0;
+  ~pa_batch() {
+    if (stage) (void)hipHostFree(stage);
+  }
+};
+
+extern "C" int32_t pa_batch_create(pa_batch** out) {
+  pa::clear_error();
+  PA_REQUIRE(out, PA_ERR_INVALID_ARG, "pa_batch_create: null out");
+  *out = new pa_batch();
+  return PA_OK;
+}
+
+extern "C" void pa_batch_destroy(pa_batch* b) { delete b; }
+
+extern "C" int32_t pa_batch_num_tokens(const pa_batch* b) { return b ? b->num_tokens : 0; }
+extern "C" int32_t pa_batch_is_decode(const pa_batch* b) { return b && b->decode ? 1 : 0; }
+
+extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t* num_tokens,
+                                    const int32_t* num_computed, const int64_t* block_ids,
+                                    const int32_t* block_counts, int32_t num_blocks,
+                                    pa_stream_t stream) {
+  pa::clear_error();
+  PA_REQUIRE(b && num_seqs >= 0 && num_blocks > 0, PA_ERR_INVALID_ARG,
+             "pa_batch_prepare: bad arguments");
+  PA_REQUIRE(num_seqs == 0 || (num_tokens && num_computed && block_counts), PA_ERR_INVALID_ARG,
+             "pa_batch_prepare: null per-sequence array");
+  int64_t total_ids = 0, total_tokens = 0;
+  int max_blocks = 1, max_q = 0, max_ctx = 0;
+  bool decode = num_seqs > 0;
+  for (int s = 0; s < num_seqs; ++s) {
+    PA_REQUIRE(num_tokens[s] >= 0 && num_computed[s] >= 0 && block_counts[s] >= 0,
+               PA_ERR_INVALID_ARG, "pa_batch_prepare: negative count for sequence %d", s);
+    const int64_t ctx = (int64_t)num_computed[s] + num_tokens[s];
+    PA_REQUIRE(ctx <= (int64_t)block_counts[s] * pa::kBlock, PA_ERR_OUT_OF_BOUNDS,
+               "pa_batch_prepare: sequence %d needs %lld tokens, its table holds %d blocks", s,
+               (long long)ctx, block_counts[s]);
+    total_ids += block_counts[s];
+    total_tokens += num_tokens[s];
+    max_blocks = std::max(max_blocks, block_counts[s]);
+    max_q = std::max(max_q, num_tokens[s]);
+    max_ctx = std::max<int>(max_ctx, (int)ctx);
+    decode = decode && num_tokens[s] == 1 && num_computed[s] > 0;
+  }
+  PA_REQUIRE(total_ids == 0 || block_ids, PA_ERR_INVALID_ARG, "pa_batch_prepare: null block_ids");
+  PA_REQUIRE(total_tokens < (1ll << 31), PA_ERR_INVALID_ARG, "pa_batch_prepare: too many tokens");
+  for (int64_t i = 0; i < total_ids; ++i)
+    PA_REQUIRE(block_ids[i] >= 0 && block_ids[i] < num_blocks, PA_ERR_OUT_OF_BOUNDS,
+               "block_id %lld out of bounds for %d blocks", (long long)block_ids[i], num_blocks);
+
+  // Host images of the index arrays, packed into one staging buffer.
+  const int T = (int)total_tokens;
+  std::vector<int64_t> pos(T), slot(T);
+  std::vector<int32_t> table((size_t)num_seqs * max_blocks, 0), cu(num_seqs + 1, 0),
+      past(num_seqs), ctxl(num_seqs);
+  int64_t id_off = 0;
+  int t = 0;
+  for (int s = 0; s < num_seqs; ++s) {
+    for (int i = 0; i < block_counts[s]; ++i)
+      table[(size_t)s * max_blocks + i] = (int32_t)block_ids[id_off + i];
+    for (int i = 0; i < num_tokens[s]; ++i, ++t) {
+      const int64_t p = (int64_t)num_computed[s] + i;
+      pos[t] = p;
+      slot[t] = block_ids[id_off + p / pa::kBlock] * pa::kBlock + p % pa::kBlock;
+    }
+    id_off += block_counts[s];
+    cu[s + 1] = cu[s] + num_tokens[s];
+    past[s] = num_computed[s];
+    ctxl[s] = num_computed[s] + num_tokens[s];
+  }
+  const size_t b_pos = pos.size() * 8, b_slot = slot.size() * 8, b_tab = table.size() * 4,
+               b_cu = cu.size() * 4, b_past = past.size() * 4, b_ctx = ctxl.size() * 4;
+  const size_t total = b_pos + b_slot + b_tab + b_cu + b_past + b_ctx;
+  if (total > b->stage_bytes) {
+    if (b->stage) (void)hipHostFree(b->stage);
+    b->stage = nullptr;
+    b->stage_bytes = 0;
+    if (hipHostMalloc(&b->stage, total, hipHostMallocDefault) != hipSuccess) {
+      pa::set_error("pa_batch_prepare: pinned staging of %zu bytes failed", total);
+      return PA_ERR_HIP;
+    }
+    b->stage_bytes = total;
+  }
+  int32_t rc = PA_OK;
+  if ((rc = b->positions.ensure(std::max<size_t>(b_pos, 8))) ||
+      (rc = b->slots.ensure(std::max<size_t>(b_slot, 8))) ||
+      (rc = b->tables.ensure(std::max<size_t>(b_tab, 4))) || (rc = b->cu_q.ensure(b_cu)) ||
+      (rc = b->past.ensure(std::max<size_t>(b_past, 4))) ||
+      (rc = b->ctx_lens.ensure(std::max<size_t>(b_ctx, 4))))
+    return rc;
+  char* st = (char*)b->stage;
+  hipStream_t s = (hipStream_t)stream;
+  struct Part {
+    const void* src;
+    size_t bytes;
+    void* dst;
+  } parts[] = {{pos.data(), b_pos, b->positions.ptr},   {slot.data(), b_slot, b->slots.ptr},
+               {table.data(), b_tab, b->tables.ptr},   {cu.data(), b_cu, b->cu_q.ptr},
+               {past.data(), b_past, b->past.ptr},     {ctxl.data(), b_ctx, b->ctx_lens.ptr}};
+  size_t off = 0;
+  for (const Part& p : parts) {
+    if (p.bytes == 0) continue;
+    std::memcpy(st + off, p.src, p.bytes);
+    if (hipMemcpyAsync(p.dst, st + off, p.bytes, hipMemcpyHostToDevice, s) != hipSuccess) {
+      pa::set_error("pa_batch_prepare: upload failed");
+      return PA_ERR_HIP;
+    }
+    off += p.bytes;
+  }
+  if (hipStreamSynchronize(s) != hipSuccess) {
+    pa::set_error("pa_batch_prepare: stream synchronisation failed");
+    return PA_ERR_HIP;
+  }
+  b->num_seqs = num_seqs;
+  b->num_tokens = T;
+  b->max_blocks = max_blocks;
+  b->max_q = max_q;
+  b->max_ctx = max_ctx;
+  b->num_blocks = num_blocks;
+  b->decode = decode;
+  return PA_OK;
+}
+
+extern "C" int32_t pa_batch_attention(pa_batch* b, pa_kv_cache* cache, int32_t layer,
+                                      int32_t num_heads, void* q, int64_t q_stride,
+                                      const void* key, int64_t key_stride, const void* value,
+                                      int64_t value_stride, const float* inv_freq, float scale,
+                                      void* out, pa_stream_t stream) {
+  pa::clear_error();
+  PA_REQUIRE(b && cache, PA_ERR_INVALID_ARG, "pa_batch_attention: null batch or cache");
+  void* kc = pa_kv_cache_key_ptr(cache, layer);
+  void* vc = pa_kv_cache_value_ptr(cache, layer);
+  PA_REQUIRE(kc && vc, PA_ERR_OUT_OF_BOUNDS, "layer_idx %d out of bounds for %d layers", layer,
+             pa_kv_cache_num_layers(cache));
+  PA_REQUIRE(pa_kv_cache_num_blocks(cache) == b->num_blocks, PA_ERR_INVALID_ARG,
+             "pa_batch_attention: batch prepared for %d blocks, cache has %d", b->num_blocks,
+             pa_kv_cache_num_blocks(cache));
+  if (b->num_tokens == 0) return PA_OK;
+  const int hkv = pa_kv_cache_num_heads(cache), d = pa_kv_cache_head_dim(cache);
+  const int dtype = pa_kv_cache_dtype(cache);
+  PA_REQUIRE(num_heads > 0 && num_heads % hkv == 0, PA_ERR_INVALID_ARG,
+             "pa_batch_attention: num_heads %d not a multiple of num_kv_heads %d", num_heads, hkv);
+  PA_REQUIRE(q && key && value && out, PA_ERR_INVALID_ARG, "pa_batch_attention: null tensor");
+  const int64_t* slots = (const int64_t*)b->slots.ptr;
+  int32_t rc;
+  if (inv_freq) {
+    rc = pa_rope_reshape_and_cache(q, q_stride, key, key_stride, value, value_stride, kc, vc,
+                                   slots, (const int64_t*)b->positions.ptr, inv_freq,
+                                   b->num_tokens, num_heads, hkv, d, b->num_blocks, dtype,
+                                   stream);
+  } else {
+    rc = pa_reshape_and_cache(key, value, kc, vc, slots, b->num_tokens, hkv, d, b->num_blocks,
+                              key_stride, value_stride, dtype, stream);
+  }
+  if (rc != PA_OK) return rc;
+  PA_REQUIRE(q_stride == 0 || q_stride == (int64_t)num_heads * d, PA_ERR_UNSUPPORTED,
+             "pa_batch_attention: attention needs contiguous q rows");
+  if (b->decode) {
+    const size_t need = pa_decode_workspace_size(b->num_seqs, num_heads, d, b->max_ctx);
+    if ((rc = b->workspace.ensure(std::max<size_t>(need, 256)))) return rc;
+    return pa_decode(out, q, kc, vc, (const int32_t*)b->tables.ptr, b->max_blocks,
+                     (const int32_t*)b->ctx_lens.ptr, b->max_ctx, b->num_seqs, num_heads, hkv, d,
+                     b->num_blocks, scale, b->workspace.ptr, b->workspace.bytes, dtype, stream);
+  }
+  return pa_prefill(out, q, kc, vc, (const int32_t*)b->tables.ptr, b->max_blocks,
+                    (const int32_t*)b->cu_q.ptr, (const int32_t*)b->past.ptr, b->num_seqs,
+                    b->num_tokens, b->max_q, num_heads, hkv, d, b->num_blocks, scale, dtype,
+                    stream);
+}

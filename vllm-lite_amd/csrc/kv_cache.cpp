@@ -128,6 +128,9 @@ extern "C" void pa_kv_cache_destroy(pa_kv_cache* c) {
 extern "C" int32_t pa_kv_cache_num_layers(const pa_kv_cache* c) { return c ? c->num_layers : 0; }
 extern "C" int32_t pa_kv_cache_num_blocks(const pa_kv_cache* c) { return c ? c->num_blocks : 0; }
 extern "C" int32_t pa_kv_cache_block_size(const pa_kv_cache*) { return pa::kBlock; }
+extern "C" int32_t pa_kv_cache_num_heads(const pa_kv_cache* c) { return c ? c->num_heads : 0; }
+extern "C" int32_t pa_kv_cache_head_dim(const pa_kv_cache* c) { return c ? c->head_dim : 0; }
+extern "C" int32_t pa_kv_cache_dtype(const pa_kv_cache* c) { return c ? c->dtype : -1; }
 
 extern "C" void* pa_kv_cache_key_ptr(pa_kv_cache* c, int32_t layer) {
   return (c && layer >= 0 && layer < c->num_layers) ? c->key[layer] : nullptr;

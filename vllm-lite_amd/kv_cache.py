@@ -145,3 +145,79 @@ class PagedKvCache:
             C.c_void_p(out_k.data_ptr()) if cover else None,
             C.c_void_p(out_v.data_ptr()) if cover else None, C.byref(n), self._stream()))
         return out_k[: n.value], out_v[: n.value]
+
+
+class StepBatch:
+    """One engine step's batch for every layer (pa_batch_*).
+
+    Built from the scheduler's per-sequence view of a step (the Batch of
+    crates/traits/src/types.rs:84-117): tokens fed this step, tokens already
+    cached, and each sequence's block ids.  attention() then runs one
+    layer's KV write (with RoPE when inv_freq is given) and attention for
+    all sequences, in place of the reference's per-sequence loop
+    (crates/model/src/causal_lm/model/mod.rs:143-164)."""
+
+    def __init__(self):
+        self._lib = _lib.load()
+        h = C.c_void_p()
+        _check("pa_batch_create", self._lib.pa_batch_create(C.byref(h)))
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            self._lib.pa_batch_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prepare(self, cache, num_tokens, num_computed, block_ids):
+        """num_tokens / num_computed: per-sequence ints; block_ids: list of
+        per-sequence lists."""
+        n = len(num_tokens)
+        if len(num_computed) != n or len(block_ids) != n:
+            raise ValueError("per-sequence lists must have equal length")
+        nt = (C.c_int32 * max(n, 1))(*[int(x) for x in num_tokens])
+        nc = (C.c_int32 * max(n, 1))(*[int(x) for x in num_computed])
+        cnt = (C.c_int32 * max(n, 1))(*[len(b) for b in block_ids])
+        flat = [int(x) for b in block_ids for x in b]
+        ids = (C.c_int64 * max(len(flat), 1))(*flat)
+        _check("pa_batch_prepare", self._lib.pa_batch_prepare(
+            self._h, n, nt, nc, ids, cnt, cache.num_blocks(), cache._stream()))
+
+    def num_tokens(self):
+        return self._lib.pa_batch_num_tokens(self._h)
+
+    def is_decode(self):
+        return bool(self._lib.pa_batch_is_decode(self._h))
+
+    def attention(self, cache, layer, q, key, value, inv_freq=None, scale=None):
+        """q [T, Hq, D] (rotated in place with inv_freq), key / value
+        [T, Hkv, D] (rows may be strided views of a fused projection) ->
+        out [T, Hq, D]."""
+        t, hq, d = q.shape
+        if t != self.num_tokens():
+            raise ValueError(f"batch has {self.num_tokens()} tokens, q has {t}")
+        if key.shape != (t, cache.num_heads, d) or value.shape != key.shape:
+            raise ValueError("key / value must be [T, Hkv, D]")
+        for x in (q, key, value):
+            if x.dtype != cache.dtype or x.device != cache.device or x.stride(2) != 1 or \
+                    x.stride(1) != d:
+                raise ValueError("q / key / value rows must be [H, D] in the cache dtype")
+        if q.stride(0) != hq * d:
+            raise ValueError("q must be contiguous")
+        if inv_freq is not None and (inv_freq.dtype != torch.float32 or
+                                     inv_freq.shape != (d // 2,)):
+            raise ValueError("inv_freq must be float32 [D/2]")
+        if scale is None:
+            scale = 1.0 / d ** 0.5
+        out = torch.empty_like(q)
+        _check("pa_batch_attention", self._lib.pa_batch_attention(
+            self._h, cache._h, layer, hq, C.c_void_p(q.data_ptr()), q.stride(0),
+            C.c_void_p(key.data_ptr()), key.stride(0), C.c_void_p(value.data_ptr()),
+            value.stride(0), C.c_void_p(inv_freq.data_ptr()) if inv_freq is not None else None,
+            float(scale), C.c_void_p(out.data_ptr()), cache._stream()))
+        return out
