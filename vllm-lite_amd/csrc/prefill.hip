@@ -319,13 +319,16 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     const int row = r0 + 16 * nt + c;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      if (rows_active && row < qlen)
-        qv[nt][s] = *reinterpret_cast<const bf16x8*>(
+      if (rows_active && row < qlen) {
+        const bf16x8 raw = *reinterpret_cast<const bf16x8*>(
             q + ((int64_t)(q_begin + row) * Hq + head) * D + 32 * s + 8 * j);
-      else
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qv[nt][s][i] = (__bf16)((float)raw[i] * scale_log2);
+      } else {
         qv[nt][s] = bf16x8{};
+      }
     }
-    m[nt] = kNegBig;
+    m[nt] = 0.f;
     lacc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -486,10 +489,22 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // block the P·V products of this step and the Sᵀ products of the next.
   auto step = [&](int n, f32x4 (&S)[NT][2], f32x4 (&Snext)[NT][2]) {
     const int kt = n >> 1, st = n & 1;
-    const bool act = n < wave_steps;
+    const bool act = true; (void)wave_steps;
     // K fragments of the next step: when it is in this tile they are read
     // now, so the softmax prep below covers their LDS latency.
     bf16x8 ka[2][KS];
+    // This step's Vᵀ fragments (dims 16 dt + c, keys 8j .. 8j+7 = one
+    // 16-byte half of the 32-byte row of block 2 st + j / 2), read first so
+    // the softmax covers their latency.
+    bf16x8 va[DT];
+    if (act) {
+      const uint8_t* vrow = &smem[buf][1][0] + (2 * st + (j >> 1)) * (D * 32) + c * 32;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = 16 * dt + c;
+        va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 + (((j & 1) ^ vswz(d)) * 16));
+      }
+    }
     if (act && st == 0) qk_load(buf, 1, ka);
     // Block ids of the tile two ahead, loaded a step before they are needed.
     if (st == 0 && kt + 2 < n_kt) ids_next2 = fetch_ids(kt + 2);
@@ -508,29 +523,39 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
           }
         }
       }
+      // S holds log2-domain scores already offset by the row's running
+      // max m (the Sᵀ accumulators start at -m).
       float lm[NT];
       bool need = false;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        lm[nt] = fmaxf(fmaxf(fmaxf(S[nt][0][0], S[nt][0][1]), fmaxf(S[nt][0][2], S[nt][0][3])),
-                       fmaxf(fmaxf(S[nt][1][0], S[nt][1][1]), fmaxf(S[nt][1][2], S[nt][1][3])));
-        need |= __builtin_fmaf(lm[nt], scale_log2, -m[nt]) > 8.0f;
+        const float t0 = fmaxf(fmaxf(S[nt][0][0], S[nt][0][1]), S[nt][0][2]);
+        const float t1 = fmaxf(fmaxf(S[nt][0][3], S[nt][1][0]), S[nt][1][1]);
+        lm[nt] = fmaxf(fmaxf(t0, t1), fmaxf(S[nt][1][2], S[nt][1][3]));
+        need |= lm[nt] > 8.0f;
       }
       // Rows keep a stale max until one of their scores exceeds it by 2^8;
       // only then is the exact max formed across the four lanes of the row
-      // and the accumulator rescaled.
-      if (__builtin_amdgcn_ballot_w64(need)) {
+      // and the accumulator rescaled.  The first step always sets the max
+      // (m starts at 0, which says nothing about the row's scores).
+      const bool first = n == 0;
+      if (first || __builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           float bm = lm[nt];
           bm = fmaxf(bm, shfl_xor_f(bm, 16));
           bm = fmaxf(bm, shfl_xor_f(bm, 32));
-          const float mn = fmaxf(m[nt], bm * scale_log2);
-          const float a = fast_exp2(m[nt] - mn);
-          m[nt] = mn;
-          lacc[nt] *= a;
+          // a row with every key of the first step masked keeps m = 0
+          const float delta = first ? (bm > -INFINITY ? bm : 0.f) : fmaxf(bm, 0.f);
+          m[nt] += delta;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) o[nt][dt] *= a;
+          for (int i = 0; i < 8; ++i) S[nt][i >> 2][i & 3] -= delta;
+          if (!first) {
+            const float a = fast_exp2(-delta);
+            lacc[nt] *= a;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[nt][dt] *= a;
+          }
         }
       }
     }
@@ -541,7 +566,9 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     if (st == 1 && kt + 1 < n_kt) {
       next_buf = buf == NBUF - 1 ? 0 : buf + 1;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): only tile kt + 1 is in flight
-      __syncthreads();
+      // No LDS fence: this wavefront's outstanding LDS reads are of tile kt,
+      // which neither the landed tile nor the next copy touches.
+      __builtin_amdgcn_s_barrier();
       if (kt + 2 < n_kt) issue_tile(ids_next2, next_buf == NBUF - 1 ? 0 : next_buf + 1);
     }
 
@@ -549,13 +576,6 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       // Operands first: this step's Vᵀ fragments and the next step's K
       // fragments (dims 16 dt + c, keys 8j .. 8j+7 = one 16-byte half of
       // the 32-byte row of block 2 st + j / 2).
-      const uint8_t* vrow = &smem[buf][1][0] + (2 * st + (j >> 1)) * (D * 32) + c * 32;
-      bf16x8 va[DT];
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int d = 16 * dt + c;
-        va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 + (((j & 1) ^ vswz(d)) * 16));
-      }
       // The next step's Sᵀ is computed even past this wavefront's last
       // step (it is then unused): keeping it unconditional keeps this one
       // basic block.  Its MFMAs are interleaved by hand with this step's
@@ -571,14 +591,15 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       for (int g = 0; g < NQK; ++g) {
         const int s_ = g / (2 * NT), q_ = g % (2 * NT), nt_ = q_ / 2, kk = q_ % 2;
         Snext[nt_][kk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            ka[kk][s_], qv[nt_][s_], s_ == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : Snext[nt_][kk], 0,
-            0, 0);
+            ka[kk][s_], qv[nt_][s_], s_ == 0 ? f32x4{-m[nt_], -m[nt_], -m[nt_], -m[nt_]}
+                                             : Snext[nt_][kk],
+            0, 0, 0);
 #pragma unroll
         for (int e = 0; e < EPM; ++e) {
           const int x = g * EPM + e;
           if (x < NEXP) {
             const int nt = x / 8, i = x % 8;
-            pv[nt][i] = fast_exp2(__builtin_fmaf(S[nt][i >> 2][i & 3], scale_log2, -m[nt]));
+            pv[nt][i] = fast_exp2(S[nt][i >> 2][i & 3]);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -586,7 +607,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
 #pragma unroll
       for (int x = NQK * EPM; x < NEXP; ++x) {
         const int nt = x / 8, i = x % 8;
-        pv[nt][i] = fast_exp2(__builtin_fmaf(S[nt][i >> 2][i & 3], scale_log2, -m[nt]));
+        pv[nt][i] = fast_exp2(S[nt][i >> 2][i & 3]);
       }
       bf16x8 pb[NT];
 #pragma unroll
