@@ -506,6 +506,22 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       }
     }
     if (act && st == 0) qk_load(buf, 1, ka);
+    // Tile boundary, at the start of a tile's second step: the next tile
+    // has landed (all waves), the buffer two tiles ahead is free again (every
+    // wavefront has finished the tile before this one), and the next tile's
+    // first K fragments are read now so this step's softmax covers them.
+    int next_buf = buf;
+    if (st == 1) {
+      if (kt + 1 < n_kt) {
+        next_buf = buf == NBUF - 1 ? 0 : buf + 1;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): only tile kt + 1 is in flight
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + 2 < n_kt) issue_tile(ids_next2, next_buf == NBUF - 1 ? 0 : next_buf + 1);
+      }
+      qk_load(next_buf, 0, ka);
+    }
     // Block ids of the tile two ahead, loaded a step before they are needed.
     if (st == 0 && kt + 2 < n_kt) ids_next2 = fetch_ids(kt + 2);
     if (act) {
@@ -560,18 +576,6 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       }
     }
 
-    // Tile boundary: the next tile has landed (all waves), and the buffer
-    // two tiles ahead is free again.
-    int next_buf = buf;
-    if (st == 1 && kt + 1 < n_kt) {
-      next_buf = buf == NBUF - 1 ? 0 : buf + 1;
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): only tile kt + 1 is in flight
-      // No LDS fence: this wavefront's outstanding LDS reads are of tile kt,
-      // which neither the landed tile nor the next copy touches.
-      __builtin_amdgcn_s_barrier();
-      if (kt + 2 < n_kt) issue_tile(ids_next2, next_buf == NBUF - 1 ? 0 : next_buf + 1);
-    }
-
     if (act) {
       // Operands first: this step's Vᵀ fragments and the next step's K
       // fragments (dims 16 dt + c, keys 8j .. 8j+7 = one 16-byte half of
@@ -582,7 +586,6 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       // exponentials, one MFMA then EPM exponentials, so the matrix core
       // and the VALU of this wavefront work at the same time.  Consecutive
       // MFMAs go to independent accumulators (s outer, (nt, kk) inner).
-      if (st == 1) qk_load(next_buf, 0, ka);
       constexpr int NQK = 2 * KS * NT;  // next-step Sᵀ MFMAs
       constexpr int NEXP = 8 * NT;      // exponentials per lane
       constexpr int EPM = NEXP / NQK > 0 ? NEXP / NQK : 1;
@@ -727,6 +730,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
 }  // namespace pa
 
 using namespace pa;
+
 
 extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
                               const int32_t* block_tables, int32_t max_blocks_per_seq,
