@@ -64,11 +64,12 @@ class Workload:
     def __init__(self, pa, name):
         self.pa = pa
         self.name = name
-        g = torch.Generator().manual_seed({"decode": 1, "prefill": 2, "splitk": 3,
-                                           "qwen": 0}[name])
+        g = torch.Generator().manual_seed({"decode": 1, "decode-fp8": 1, "prefill": 2,
+                                           "splitk": 3, "qwen": 0}[name])
         dg = torch.Generator(device=DEV).manual_seed(1234)
         self.kind = "decode"
-        if name == "decode":
+        self.fp8 = name == "decode-fp8"
+        if name in ("decode", "decode-fp8"):
             B, hq, hkv, d, ctx = 64, 32, 8, 128, 4096
             self.dtype = torch.bfloat16
             nblk = ctx // 16
@@ -78,6 +79,9 @@ class Workload:
             kv_scale = 0.5
             self.workload = ("config 2: Llama-3-8B decode bf16, B 64, 32/8 heads x 128, "
                              "ctx 4096, block 16, random block tables over 16384 blocks")
+            if self.fp8:
+                self.workload = ("config 2 shape over an FP8-E4M3 KV cache (reference codes), "
+                                 "q/out bf16, B 64, 32/8 heads x 128, ctx 4096, 16384 blocks")
         elif name == "splitk":
             B, hq, hkv, d = 16, 32, 8, 128
             self.dtype = torch.bfloat16
@@ -146,10 +150,22 @@ class Workload:
         self.scale = 1.0 / math.sqrt(d)
         self.bt = bt.to(DEV)
         self.pool = pool
-        self.kc = (torch.randn(pool, hkv, 16, d, generator=dg, device=DEV) * kv_scale).to(
-            self.dtype)
-        self.vc = (torch.randn(pool, hkv, d, 16, generator=dg, device=DEV) * kv_scale).to(
-            self.dtype)
+        if self.fp8:
+            # quantise N(0, 0.5) K/V into the pool with the library's encoder
+            self.kc, self.vc = pa.ops.new_cache(pool, hkv, d, torch.uint8, DEV)
+            chunk = 16384
+            for t0 in range(0, pool * 16, chunk):
+                n = min(chunk, pool * 16 - t0)
+                kk = (torch.randn(n, hkv, d, generator=dg, device=DEV) * kv_scale).to(self.dtype)
+                vv = (torch.randn(n, hkv, d, generator=dg, device=DEV) * kv_scale).to(self.dtype)
+                sl = torch.arange(t0, t0 + n, dtype=torch.int64, device=DEV)
+                pa.reshape_and_cache_fp8(kk, vv, self.kc, self.vc, sl)
+            del kk, vv, sl
+        else:
+            self.kc = (torch.randn(pool, hkv, 16, d, generator=dg, device=DEV) * kv_scale).to(
+                self.dtype)
+            self.vc = (torch.randn(pool, hkv, d, 16, generator=dg, device=DEV) * kv_scale).to(
+                self.dtype)
         self.ctx_dev = self.ctx.to(DEV) if self.kind == "decode" else None
         es = torch.empty(0, dtype=self.dtype).element_size()
         if self.kind == "decode":
@@ -167,18 +183,22 @@ class Workload:
             tokens = int(self.ctx.sum())
             # algorithmic bytes per pa_decode launch: K and V of every context
             # token at Hkv heads, q in, out, block tables, context lengths.
-            self.kv_bytes = 2 * tokens * hkv * d * es
+            kv_es = 1 if self.fp8 else es
+            self.kv_bytes = 2 * tokens * hkv * d * kv_es
             self.alg_bytes = (self.kv_bytes + 2 * B * hq * d * es +
                               int(((self.ctx + 15) // 16).sum()) * 4 + B * 4)
             uniq = len(set(bt[:, :].flatten().tolist()))
-            self.unique_kv_bytes = 2 * min(uniq * 16, tokens) * hkv * d * es
+            self.unique_kv_bytes = 2 * min(uniq * 16, tokens) * hkv * d * kv_es
         else:
             self.out = torch.empty_like(self.q)
             tokens_all = sum(p + 2048 for p in [0, 512, 1024, 2048])
             self.alg_bytes = (2 * tokens_all * hkv * d * es + 2 * self.q.numel() * es)
 
     def write_step(self):
-        self.pa.reshape_and_cache(self.k_new, self.v_new, self.kc, self.vc, self.slots)
+        if self.fp8:
+            self.pa.reshape_and_cache_fp8(self.k_new, self.v_new, self.kc, self.vc, self.slots)
+        else:
+            self.pa.reshape_and_cache(self.k_new, self.v_new, self.kc, self.vc, self.slots)
 
     def attend(self):
         if self.kind == "decode":
@@ -248,13 +268,22 @@ def cpu_baseline(w, budget_s=12.0):
     kc = host(w.kc[idx])
     vc = host(w.vc[idx].transpose(-1, -2))
     q = host(w.q[:nseq])
-    oracle.paged_attention(q[:1], kc, vc, bt_c[:1], [0, 1], ctx[:1] - 1, scale=w.scale,
-                           threads=threads)  # warm
+    if w.fp8:
+        # the reference dequantises FP8 blocks (Fp8Quantizer::dequantize) before
+        # attending in f32; the dequantisation is part of each timed pass
+        q = oracle.bf16_to_f32(q)
+
+        def attend(qq, bts, qs, past):
+            oracle.paged_attention(qq, oracle.fp8_decode(kc), oracle.fp8_decode(vc), bts, qs,
+                                   past, scale=w.scale, threads=threads)
+    else:
+        def attend(qq, bts, qs, past):
+            oracle.paged_attention(qq, kc, vc, bts, qs, past, scale=w.scale, threads=threads)
+    attend(q[:1], bt_c[:1], [0, 1], ctx[:1] - 1)  # warm
     t0 = time.perf_counter()
     reps = 0
     while True:
-        oracle.paged_attention(q, kc, vc, bt_c, np.arange(nseq + 1), ctx - 1, scale=w.scale,
-                               threads=threads)
+        attend(q, bt_c, np.arange(nseq + 1), ctx - 1)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 50:
@@ -262,8 +291,8 @@ def cpu_baseline(w, budget_s=12.0):
     return {"value": round(nseq * reps / el, 2), "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": f"{nseq} sequences of the same workload x {reps} passes "
-                      f"({el:.1f} s): oracle gather + expand_kv + dense f32 softmax "
-                      "attention, OpenMP"}
+                      f"({el:.1f} s): oracle {'FP8 dequantisation + ' if w.fp8 else ''}"
+                      "gather + expand_kv + dense f32 softmax attention, OpenMP"}
 
 
 def copy_calibration(args):
@@ -294,7 +323,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "prefill", "splitk", "qwen", "copy"])
+                    choices=["decode", "decode-fp8", "prefill", "splitk", "qwen", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -332,6 +361,8 @@ def main():
             roof["unique_block_gbs"] = round((w.unique_kv_bytes) / t_attn / 1e9, 1)
         if w.dtype == torch.float32:
             roof["kernel"] = "pa_decode (decode_generic_kernel + decode_reduce_kernel)"
+        if w.fp8:
+            roof["kernel"] = "pa_decode (decode_fp8_kernel + decode_reduce_kernel)"
     else:
         value = w.flops / t_attn / 1e12
         unit = "TFLOP/s"
@@ -346,7 +377,8 @@ def main():
         "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16" if w.dtype == torch.bfloat16 else "f32",
+        "dtype": ("fp8-e4m3 KV, bf16 q/out" if w.fp8 else
+                  "bf16" if w.dtype == torch.bfloat16 else "f32"),
         "data": "synthetic (seeded N(0,1) Q/K/V, random block tables)",
         "config": {"workload": w.workload, "global_batch": w.B,
                    "seq_len": int(w.ctx.max()) if w.kind == "decode" else 2048,

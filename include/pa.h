@@ -16,7 +16,11 @@
  *    throws or unwinds; pa_last_error() gives a message for the calling
  *    thread's most recent failure.
  *  - dtype: PA_DTYPE_F32 or PA_DTYPE_BF16, shared by q, k, v, the caches and
- *    out.  Arithmetic accumulates in f32.
+ *    out.  Arithmetic accumulates in f32.  PA_DTYPE_FP8_E4M3 selects one-byte
+ *    caches in the reference's FP8 convention
+ *    (crates/model/src/components/kv_cache_fp8.rs:143-212); with it q and out
+ *    are bf16, K / V are written by pa_reshape_and_cache_fp8 and pa_read_kv
+ *    returns f32.
  *  - Block size is fixed at 16 tokens (crates/traits/src/types.rs:13).
  *
  * Cache layout (one layer, one of K / V; num_blocks = NB, kv heads = Hkv):
@@ -44,7 +48,7 @@ typedef struct ihipStream_t* pa_stream_t; /* same type as hipStream_t */
 
 #define PA_BLOCK_SIZE 16
 
-typedef enum pa_dtype { PA_DTYPE_F32 = 0, PA_DTYPE_BF16 = 1 } pa_dtype;
+typedef enum pa_dtype { PA_DTYPE_F32 = 0, PA_DTYPE_BF16 = 1, PA_DTYPE_FP8_E4M3 = 2 } pa_dtype;
 
 typedef enum pa_status {
   PA_OK = 0,
@@ -80,6 +84,18 @@ int32_t pa_reshape_and_cache(const void* key, const void* value, void* k_cache, 
                              int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                              int64_t key_stride, int64_t value_stride, int32_t dtype,
                              pa_stream_t stream);
+
+/* pa_reshape_and_cache into FP8 caches (PA_DTYPE_FP8_E4M3, one byte per
+ * element, same block layouts): every element is quantised with the
+ * reference's encoder, Fp8Quantizer::quantize / float32_to_fp8_e4m3
+ * (crates/model/src/components/kv_cache_fp8.rs:59-68, :143-186), bit for
+ * bit.  key / value are src_dtype (PA_DTYPE_F32 or PA_DTYPE_BF16) with
+ * token strides in elements (0 = contiguous). */
+int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, uint8_t* k_cache,
+                                 uint8_t* v_cache, const int64_t* slot_mapping, int32_t num_tokens,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                                 int64_t key_stride, int64_t value_stride, int32_t src_dtype,
+                                 pa_stream_t stream);
 
 /* Build slot_mapping on the device from per-sequence block tables:
  *   slot_mapping[t] = block_tables[s, positions[t] / 16] * 16 + positions[t] % 16
@@ -144,7 +160,9 @@ int32_t pa_rope_inv_freq(int32_t head_dim, float theta, int32_t rope_type, float
  * out_k / out_v [seq_len, Hkv, D] (reference layout, bit-exact copies).
  *   block_ids [n_ids] int32; block b holds tokens [16b, 16b + 16).
  * Requires n_ids * 16 >= seq_len.  Entries outside [0, num_blocks) produce
- * zero rows.
+ * zero rows.  With PA_DTYPE_FP8_E4M3 caches the outputs are f32, each
+ * element the reference's dequantised value (Fp8Quantizer::dequantize,
+ * kv_cache_fp8.rs:70-88, :188-212: f16-exact, NaN / +-inf codes kept).
  * Replaces PagedKvCache::read_kv
  * (crates/model/src/paged_tensor/tensor_store/buffer.rs:273-339). */
 int32_t pa_read_kv(const void* k_cache, const void* v_cache, const int32_t* block_ids,

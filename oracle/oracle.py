@@ -52,6 +52,14 @@ def load():
         lib.oracle_rope_inv_freq.restype = None
         lib.oracle_rope.argtypes = [p, i32, i32, i32, p, p, i32]
         lib.oracle_rope.restype = None
+        lib.oracle_fp8_encode.argtypes = [f32]
+        lib.oracle_fp8_encode.restype = C.c_uint8
+        lib.oracle_fp8_decode.argtypes = [C.c_uint8]
+        lib.oracle_fp8_decode.restype = f32
+        lib.oracle_fp8_encode_n.argtypes = [p, p, i64]
+        lib.oracle_fp8_encode_n.restype = None
+        lib.oracle_fp8_decode_n.argtypes = [p, p, i64]
+        lib.oracle_fp8_decode_n.restype = None
         lib.oracle_f32_to_bf16.argtypes = [f32]
         lib.oracle_f32_to_bf16.restype = C.c_uint16
         _lib = lib
@@ -256,3 +264,19 @@ def rope(x, positions, inv_freq):
     inv = np.ascontiguousarray(inv_freq, dtype=np.float32)
     load().oracle_rope(_p(x), t, h, d, _p(pos), _p(inv), _code(x))
     return x
+
+
+def fp8_encode(x):
+    """Reference FP8-E4M3 codes (uint8) of f32 values (any shape)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint8)
+    load().oracle_fp8_encode_n(_p(x), _p(out), x.size)
+    return out
+
+
+def fp8_decode(b):
+    """f32 values of reference FP8-E4M3 codes (any shape)."""
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(b.shape, np.float32)
+    load().oracle_fp8_decode_n(_p(b), _p(out), b.size)
+    return out

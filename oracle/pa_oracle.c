@@ -33,6 +33,13 @@
  *          the saturating float->u64 cast cases.
  *   oracle_quant_write_kv / oracle_quant_read_kv -> closed-form int8 grid
  *          checks (scale = max|x| / 127, values on the integer grid).
+ *   oracle_rope_inv_freq / oracle_rope -> closed forms (identity at
+ *          position 0, cos/sin at position 1, rotation direction, per-type
+ *          frequency tables).
+ *   oracle_fp8_encode / oracle_fp8_decode -> the reference's own test values,
+ *          torch's independent float8_e4m3fn conversions wherever that
+ *          format and the reference's coincide, exhaustive round trips and a
+ *          brute-force nearest-value search.
  */
 #include <math.h>
 #include <stdint.h>
@@ -575,4 +582,62 @@ void oracle_rope(void* x, int T, int H, int D, const int64_t* positions, const f
         store_el(x, base + half + i, x2 * c + x1 * s, dtype);
       }
     }
+}
+
+/* ---------------------------------------------------------------------- */
+/* FP8 E4M3 KV codec, the reference's convention                           */
+/* ---------------------------------------------------------------------- */
+
+/* crates/model/src/components/kv_cache_fp8.rs:143-186
+ * (Fp8Quantizer::float32_to_fp8_e4m3): sign bit 7, 4-bit exponent with
+ * bias 7, 3-bit mantissa; normals only.  NaN -> 0x80, +-inf -> 0x7C / 0xFC;
+ * |v| < 2^-6 (biased exponent <= 0 before rounding) -> +0; biased exponent
+ * > 14 (before or after rounding) saturates to 0x7B / 0xFB; the [1, 2)
+ * significand is rounded to 3 fraction bits half-up (fma(f, 8, 0.5)
+ * truncated), a carry to 2.0 bumping the exponent. */
+uint8_t oracle_fp8_encode(float v) {
+  if (isnan(v)) return 0x80;
+  if (isinf(v)) return v > 0 ? 0x7C : 0xFC;
+  const uint8_t sign = signbit(v) ? 1 : 0;
+  const float a = fabsf(v);
+  if (a == 0.0f) return 0;
+  int e2;
+  const float half = frexpf(a, &e2); /* a = half * 2^e2, half in [0.5, 1) */
+  const float f = half * 2.0f;       /* [1, 2) */
+  int be = (e2 - 1) + 7;
+  if (be <= 0) return 0;
+  const uint8_t sat = sign ? 0xFB : 0x7B;
+  if (be > 14) return sat;
+  const unsigned im = (unsigned)fmaf(f, 8.0f, 0.5f); /* 8 .. 16 */
+  unsigned frac;
+  if (im >= 16) {
+    be += 1;
+    frac = 0;
+  } else {
+    frac = im - 8;
+  }
+  if (be > 14) return sat;
+  return (uint8_t)((sign << 7) | ((unsigned)be << 3) | frac);
+}
+
+/* crates/model/src/components/kv_cache_fp8.rs:188-212
+ * (fp8_e4m3_to_float16), as the f32 value of that f16: 0x80 -> NaN,
+ * 0x7C / 0xFC -> +-inf, exponent and mantissa 0 -> +-0, otherwise
+ * (-1)^s * 2^(e - 7) * (1 + m / 8) for every exponent field 0 .. 15. */
+float oracle_fp8_decode(uint8_t b) {
+  if (b == 0x80) return NAN;
+  if (b == 0x7C) return INFINITY;
+  if (b == 0xFC) return -INFINITY;
+  const int sign = b >> 7, e = (b >> 3) & 15, m = b & 7;
+  if (e == 0 && m == 0) return sign ? -0.0f : 0.0f;
+  const float v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+  return sign ? -v : v;
+}
+
+void oracle_fp8_encode_n(const float* x, uint8_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_fp8_encode(x[i]);
+}
+
+void oracle_fp8_decode_n(const uint8_t* x, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_fp8_decode(x[i]);
 }

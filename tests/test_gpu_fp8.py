@@ -1,0 +1,152 @@
+"""GPU parity of the FP8-E4M3 KV path (the reference's codes,
+crates/model/src/components/kv_cache_fp8.rs): the quantising cache write is
+bit-exact against the oracle encoder, read_kv against the oracle decoder, and
+decode / prefill over FP8 caches match the oracle's attention over the
+dequantised caches within the bf16 tolerance."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import BF16_ATOL, BF16_RTOL, assert_close, make_decode_case
+from test_gpu_cache_ops import DEV, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def wide_values(rng, shape):
+    """Magnitudes across and beyond the E4M3 range, exact ties, specials."""
+    n = int(np.prod(shape))
+    x = np.exp(rng.uniform(np.log(1e-5), np.log(2e3), n)).astype(np.float32)
+    x *= rng.choice([-1.0, 1.0], n).astype(np.float32)
+    k = n // 8
+    grid = np.ldexp(1.0 + rng.integers(0, 8, k) / 8.0, rng.integers(-6, 8, k))
+    x[:k] = (grid + np.ldexp(1.0 / 16.0, np.frexp(grid)[1] - 1)).astype(np.float32)  # ties
+    specials = np.array([0.0, -0.0, np.nan, np.inf, -np.inf, 1e-40, 240.0, 247.9, 248.0,
+                         352.0, 1e30, 2.0 ** -6, 2.0 ** -6 * 0.99], np.float32)
+    x[k:k + specials.size] = specials
+    return x.reshape(shape)
+
+
+def ref_scatter(codes, slots, nb):
+    """Reference-layout scatter of per-token codes [T, H, D] (uint8)."""
+    t, h, d = codes.shape
+    cache = np.zeros((nb, h, 16, d), np.uint8)
+    for i, s in enumerate(slots):
+        if 0 <= s < nb * 16:
+            cache[s // 16, :, s % 16, :] = codes[i]
+    return cache
+
+
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+@pytest.mark.parametrize("h,d", [(8, 128), (2, 64), (3, 40)])
+def test_reshape_and_cache_fp8_bit_exact(pa, oracle, src, h, d):
+    rng = np.random.default_rng(h * d)
+    t, nb = 77, 12
+    k = wide_values(rng, (t, h, d))
+    v = wide_values(rng, (t, h, d))
+    if src == "bf16":
+        kb, vb = oracle.f32_to_bf16(k), oracle.f32_to_bf16(v)
+        k, v = oracle.bf16_to_f32(kb), oracle.bf16_to_f32(vb)  # the values the GPU sees
+        dk, dv = to_dev(kb), to_dev(vb)
+    else:
+        dk, dv = to_dev(k), to_dev(v)
+    slots = rng.permutation(nb * 16)[:t].astype(np.int64)
+    slots[3] = -1
+    slots[9] = nb * 16
+    kc, vc = pa.ops.new_cache(nb, h, d, torch.uint8, DEV)
+    pa.reshape_and_cache_fp8(dk, dv, kc, vc, to_dev(slots))
+    kref = ref_scatter(oracle.fp8_encode(k), slots, nb)
+    vref = ref_scatter(oracle.fp8_encode(v), slots, nb)
+    assert np.array_equal(to_np(kc), kref)
+    assert np.array_equal(oracle.v_to_ref(to_np(vc)), vref)
+
+
+def test_read_kv_fp8_every_code(pa, oracle):
+    rng = np.random.default_rng(5)
+    nb, h, d = 9, 2, 64
+    kref = rng.integers(0, 256, (nb, h, 16, d)).astype(np.uint8)
+    vref = rng.integers(0, 256, (nb, h, 16, d)).astype(np.uint8)
+    kref.reshape(-1)[:256] = np.arange(256)
+    ids = np.array([4, 0, 7, 2, 8], np.int32)
+    seq_len = 70
+    k, v = pa.read_kv(to_dev(kref), to_dev(oracle.v_from_ref(vref)), to_dev(ids), seq_len)
+    want_k = oracle.fp8_decode(kref[ids].transpose(0, 2, 1, 3).reshape(-1, h, d)[:seq_len])
+    want_v = oracle.fp8_decode(vref[ids].transpose(0, 2, 1, 3).reshape(-1, h, d)[:seq_len])
+    got_k, got_v = to_np(k), to_np(v)
+    # bit-exact, NaN codes included
+    assert np.array_equal(got_k.view(np.uint32), want_k.view(np.uint32))
+    assert np.array_equal(got_v.view(np.uint32), want_v.view(np.uint32))
+
+
+def fp8_decode_case(oracle, rng, B, hq, hkv, d, ctx, shared=0):
+    case = make_decode_case(rng, B, hq, hkv, d, ctx, dtype="bf16", shared_prefix_blocks=shared)
+    kf = oracle.bf16_to_f32(case["k_cache"])
+    vf = oracle.bf16_to_f32(case["v_cache_ref"])
+    kc, vc = oracle.fp8_encode(kf), oracle.fp8_encode(vf)
+    return case, kc, vc
+
+
+def run_fp8_decode(pa, oracle, case, kc, vc):
+    q, bt, ctx = case["q"], case["block_tables"], case["ctx"]
+    out = pa.decode(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt),
+                    to_dev(ctx), int(ctx.max()))
+    got = oracle.bf16_to_f32(to_np(out))
+    b = q.shape[0]
+    qs = np.arange(b + 1, dtype=np.int32)
+    past = (ctx - 1).astype(np.int32)
+    ref = oracle.paged_attention(oracle.bf16_to_f32(q), oracle.fp8_decode(kc),
+                                 oracle.fp8_decode(vc), np.where(bt < 0, 0, bt), qs, past)
+    return got, ref
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (8, 1, 256), (16, 16, 128),
+                                      (28, 4, 64), (64, 4, 128), (12, 4, 96)])
+def test_decode_fp8(pa, oracle, hq, hkv, d):
+    # (64, 4): group 16; (12, 4, 96): the generic kernel
+    rng = np.random.default_rng(hq * d)
+    ctx = [1, 15, 16, 17, 33, 255, 256, 257, 700, 1500]
+    case, kc, vc = fp8_decode_case(oracle, rng, len(ctx), hq, hkv, d, ctx)
+    got, ref = run_fp8_decode(pa, oracle, case, kc, vc)
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, f"fp8 decode {hq}/{hkv}x{d}")
+
+
+def test_decode_fp8_long_split_and_stale_codes(pa, oracle):
+    rng = np.random.default_rng(9)
+    ctx = [5000, 12003, 200]
+    case, kc, vc = fp8_decode_case(oracle, rng, len(ctx), 32, 8, 128, ctx, shared=8)
+    # codes past each context (in its last block) are 0x7F, NaN to the
+    # hardware conversion; they must be masked, not multiplied by 0
+    bt = case["block_tables"]
+    for b, c in enumerate(ctx):
+        last = bt[b, (c - 1) // 16]
+        if c % 16 and (c - 1) // 16 >= 8:  # not a shared prefix block
+            kc[last, :, c % 16:, :] = 0x7F
+            vc[last, :, c % 16:, :] = 0x7F
+    got, ref = run_fp8_decode(pa, oracle, case, kc, vc)
+    assert np.isfinite(got).all()
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, "fp8 decode long")
+
+
+def test_prefill_fp8(pa, oracle):
+    rng = np.random.default_rng(11)
+    hq, hkv, d = 8, 2, 128
+    pasts, chunks = [0, 37, 100], [20, 45, 3]
+    nblk = [(p + c + 15) // 16 for p, c in zip(pasts, chunks)]
+    nb = sum(nblk) + 3
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = np.zeros((3, max(nblk)), np.int32)
+    o = 0
+    for b in range(3):
+        bt[b, :nblk[b]] = perm[o:o + nblk[b]]
+        o += nblk[b]
+    kc = oracle.fp8_encode(rng.standard_normal((nb, hkv, 16, d), dtype=np.float32))
+    vc = oracle.fp8_encode(rng.standard_normal((nb, hkv, 16, d), dtype=np.float32))
+    q = oracle.f32_to_bf16(rng.standard_normal((sum(chunks), hq, d), dtype=np.float32))
+    cu = np.concatenate([[0], np.cumsum(chunks)]).astype(np.int32)
+    past = np.asarray(pasts, np.int32)
+    out = pa.prefill(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt),
+                     to_dev(cu), to_dev(past), max(chunks))
+    got = oracle.bf16_to_f32(to_np(out))
+    ref = oracle.paged_attention(oracle.bf16_to_f32(q), oracle.fp8_decode(kc),
+                                 oracle.fp8_decode(vc), bt, cu, past)
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, "fp8 prefill")

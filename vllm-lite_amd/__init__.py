@@ -17,6 +17,7 @@ from .ops import (
     prefill,
     read_kv,
     reshape_and_cache,
+    reshape_and_cache_fp8,
     rope_inv_freq,
     rope_reshape_and_cache,
     slot_mapping,
@@ -34,6 +35,7 @@ __all__ = [
     "prefill",
     "read_kv",
     "reshape_and_cache",
+    "reshape_and_cache_fp8",
     "rope_inv_freq",
     "rope_reshape_and_cache",
     "slot_mapping",

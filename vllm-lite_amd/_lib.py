@@ -13,6 +13,8 @@ SIGNATURES = {
     "pa_version": (C.c_char_p, []),
     "pa_reshape_and_cache": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64,
                                     _i32, _p]),
+    "pa_reshape_and_cache_fp8": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i64, _i64,
+                                         _i32, _p]),
     "pa_slot_mapping": (_i32, [_p, _i32, _p, _p, _i32, _i32, _p, _p]),
     "pa_read_kv": (_i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _i32, _p]),
     "pa_block_hash": (_i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p]),

@@ -62,6 +62,65 @@ __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
   }
 }
 
+// Quantising scatter into FP8 caches: as reshape_and_cache_kernel, each
+// thread encodes VEC consecutive elements of one head (VEC = 8: one 8-byte
+// K store; the V bytes go to VEC rows of the token-minor block).
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void reshape_and_cache_fp8_kernel(
+    const T* __restrict__ key, const T* __restrict__ value, uint8_t* __restrict__ k_cache,
+    uint8_t* __restrict__ v_cache, const int64_t* __restrict__ slots, int H, int D,
+    int64_t num_slots, int64_t key_stride, int64_t value_stride) {
+  const int t = blockIdx.x;
+  const int64_t slot = slots[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t blk = slot / kBlock;
+  const int off = (int)(slot % kBlock);
+  const int per_head = D / VEC;
+  for (int i = threadIdx.x; i < H * per_head; i += blockDim.x) {
+    const int h = i / per_head;
+    const int d0 = (i % per_head) * VEC;
+    const T* ks = key + t * key_stride + (int64_t)h * D + d0;
+    const T* vs = value + t * value_stride + (int64_t)h * D + d0;
+    uint8_t* kd = k_cache + ((blk * H + h) * kBlock + off) * (int64_t)D + d0;
+    uint8_t* vd = v_cache + ((blk * H + h) * (int64_t)D + d0) * kBlock + off;
+    uint8_t kb[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      kb[e] = fp8_encode(Elem<T>::load(ks + e));
+      vd[e * kBlock] = fp8_encode(Elem<T>::load(vs + e));
+    }
+    if constexpr (VEC == 8) {
+      *reinterpret_cast<uint2*>(kd) = *reinterpret_cast<const uint2*>(kb);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) kd[e] = kb[e];
+    }
+  }
+}
+
+// Dequantising gather from FP8 caches (f32 out).
+__global__ __launch_bounds__(256) void read_kv_fp8_kernel(const uint8_t* __restrict__ k_cache,
+                                                          const uint8_t* __restrict__ v_cache,
+                                                          const int32_t* __restrict__ block_ids,
+                                                          int H, int D, int num_blocks,
+                                                          float* __restrict__ out_k,
+                                                          float* __restrict__ out_v) {
+  const int t = blockIdx.x;
+  const int32_t blk = block_ids[t / kBlock];
+  const bool ok = blk >= 0 && blk < num_blocks;
+  const int off = t % kBlock;
+  for (int i = threadIdx.x; i < H * D; i += blockDim.x) {
+    const int h = i / D, d = i % D;
+    float kx = 0.f, vx = 0.f;
+    if (ok) {
+      kx = fp8_decode(k_cache[(((int64_t)blk * H + h) * kBlock + off) * D + d]);
+      vx = fp8_decode(v_cache[(((int64_t)blk * H + h) * D + d) * kBlock + off]);
+    }
+    out_k[(int64_t)t * H * D + i] = kx;
+    out_v[(int64_t)t * H * D + i] = vx;
+  }
+}
+
 // slot_mapping[t] = block_tables[s][pos / 16] * 16 + pos % 16.
 __global__ void slot_mapping_kernel(const int32_t* __restrict__ block_tables, int mbs,
                                     const int64_t* __restrict__ positions,
@@ -213,6 +272,49 @@ extern "C" int32_t pa_reshape_and_cache(const void* key, const void* value, void
   return check_launch("pa_reshape_and_cache");
 }
 
+extern "C" int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, uint8_t* k_cache,
+                                            uint8_t* v_cache, const int64_t* slot_mapping,
+                                            int32_t num_tokens, int32_t num_kv_heads,
+                                            int32_t head_dim, int32_t num_blocks,
+                                            int64_t key_stride, int64_t value_stride,
+                                            int32_t src_dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype_ok(src_dtype), PA_ERR_INVALID_ARG,
+             "pa_reshape_and_cache_fp8: source dtype %d is not f32 or bf16", src_dtype);
+  PA_REQUIRE(num_tokens >= 0 && num_kv_heads > 0 && head_dim > 0 && num_blocks > 0,
+             PA_ERR_INVALID_ARG, "pa_reshape_and_cache_fp8: bad sizes T=%d H=%d D=%d NB=%d",
+             num_tokens, num_kv_heads, head_dim, num_blocks);
+  if (num_tokens == 0) return PA_OK;
+  PA_REQUIRE(key && value && k_cache && v_cache && slot_mapping, PA_ERR_INVALID_ARG,
+             "pa_reshape_and_cache_fp8: null pointer");
+  const int64_t row = (int64_t)num_kv_heads * head_dim;
+  if (key_stride == 0) key_stride = row;
+  if (value_stride == 0) value_stride = row;
+  PA_REQUIRE(key_stride >= row && value_stride >= row, PA_ERR_INVALID_ARG,
+             "pa_reshape_and_cache_fp8: token stride smaller than Hkv*D");
+  const int64_t num_slots = (int64_t)num_blocks * kBlock;
+  const bool vec = head_dim % 8 == 0 && ((uintptr_t)k_cache % 8) == 0;
+  const dim3 grid(num_tokens), block(256);
+  hipStream_t s = (hipStream_t)stream;
+#define PA_LAUNCH_Q(T, V)                                                                    \
+  reshape_and_cache_fp8_kernel<T, V><<<grid, block, 0, s>>>(                                 \
+      (const T*)key, (const T*)value, k_cache, v_cache, slot_mapping, num_kv_heads, head_dim, \
+      num_slots, key_stride, value_stride)
+  if (src_dtype == PA_DTYPE_BF16) {
+    if (vec)
+      PA_LAUNCH_Q(uint16_t, 8);
+    else
+      PA_LAUNCH_Q(uint16_t, 1);
+  } else {
+    if (vec)
+      PA_LAUNCH_Q(float, 8);
+    else
+      PA_LAUNCH_Q(float, 1);
+  }
+#undef PA_LAUNCH_Q
+  return check_launch("pa_reshape_and_cache_fp8");
+}
+
 extern "C" int32_t pa_slot_mapping(const int32_t* block_tables, int32_t max_blocks_per_seq,
                                    const int64_t* positions, const int32_t* cu_seq_tokens,
                                    int32_t num_seqs, int32_t num_tokens, int64_t* slot_mapping,
@@ -233,7 +335,8 @@ extern "C" int32_t pa_read_kv(const void* k_cache, const void* v_cache, const in
                               int32_t head_dim, int32_t num_blocks, void* out_k, void* out_v,
                               int32_t dtype, pa_stream_t stream) {
   clear_error();
-  PA_REQUIRE(dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_read_kv: unknown dtype %d", dtype);
+  PA_REQUIRE(dtype_ok(dtype) || dtype == PA_DTYPE_FP8_E4M3, PA_ERR_INVALID_ARG,
+             "pa_read_kv: unknown dtype %d", dtype);
   PA_REQUIRE(seq_len >= 0 && n_ids >= 0 && num_kv_heads > 0 && head_dim > 0 && num_blocks > 0,
              PA_ERR_INVALID_ARG, "pa_read_kv: bad sizes");
   if (seq_len == 0 || n_ids == 0) return PA_OK;
@@ -242,7 +345,11 @@ extern "C" int32_t pa_read_kv(const void* k_cache, const void* v_cache, const in
   PA_REQUIRE(k_cache && v_cache && block_ids && out_k && out_v, PA_ERR_INVALID_ARG,
              "pa_read_kv: null pointer");
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == PA_DTYPE_BF16)
+  if (dtype == PA_DTYPE_FP8_E4M3)
+    read_kv_fp8_kernel<<<seq_len, 256, 0, s>>>(
+        (const uint8_t*)k_cache, (const uint8_t*)v_cache, block_ids, num_kv_heads, head_dim,
+        num_blocks, (float*)out_k, (float*)out_v);
+  else if (dtype == PA_DTYPE_BF16)
     read_kv_kernel<uint16_t><<<seq_len, 256, 0, s>>>(
         (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_ids, num_kv_heads, head_dim,
         num_blocks, (uint16_t*)out_k, (uint16_t*)out_v);

@@ -216,12 +216,195 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// MFMA decode over FP8 caches (the reference's E4M3 codes, one byte per
+// element), q / out bf16.  Same work split, online softmax and epilogue as
+// decode_mfma_kernel; the operands are converted to bf16 in registers with
+// v_cvt_scalef32_pk_bf16_fp8 (scale 1).  That conversion reads OCP E4M3,
+// which gives the reference's value for every code its encoder produces from
+// finite input; only the NaN / inf codes (0x80, 0x7C, 0xFC) read as -0 and
+// +-384 here.
+//
+// The lane layout is chosen so that every load is contiguous:
+//  * QK step s: lane (c, j) supplies K rows of tokens
+//      tk0 = 8 ((c >> 2) & 1) + (c & 3)  and  tk0 + 4   of block c >> 3
+//    (first / second MFMA), dims D/4 j + 8 s .. + 7 (the lane's D/4 bytes of
+//    each row are contiguous; Q is loaded in the same dim order).  The
+//    scores then land so that lane (c, j) holds the 8 consecutive tokens
+//    8 (j & 1) .. + 7 of block j >> 1.
+//  * P·V: reduction slot 8 j + i is token 8 (j & 1) + i of block j >> 1, so
+//    the Vᵀ operand of dims 16 dt + c is one 8-byte load from the
+//    token-minor block.
+__device__ inline bf16x8 fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void decode_fp8_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
+    const uint8_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
+    float scale_log2, int num_parts, int part_len, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml) {
+  constexpr int KS = D / 32;  // QK reduction steps
+  constexpr int DT = D / 16;  // PV output tiles
+  constexpr int DL = D / 4;   // dims (bytes) of a K row per lane group
+  const int lane = threadIdx.x;
+  const int c = lane & 15, j = lane >> 4;
+  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int ctx = min(context_lens[seq], mbs * kBlock);
+  const int tok0 = part * part_len;
+  if (tok0 >= ctx) {
+    if (num_parts == 1 && c < G) {
+      uint16_t* orow = out + ((int64_t)seq * Hq + kvh * G + c) * D;
+      for (int d = 4 * j; d < D; d += 16) *reinterpret_cast<uint64_t*>(orow + d) = 0;
+    }
+    return;
+  }
+  const int tok_end = min(ctx, tok0 + part_len);
+  const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;
+
+  const int head = kvh * G + c;
+  bf16x8 qv[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    if (c < G)
+      qv[s] = *reinterpret_cast<const bf16x8*>(q + ((int64_t)seq * Hq + head) * D + DL * j + 8 * s);
+    else
+      qv[s] = bf16x8{};
+  }
+
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = kNegBig, lsum = 0.f;
+
+  const int32_t* btab = block_tables + (int64_t)seq * mbs + tok0 / kBlock;
+  const int64_t head_stride = (int64_t)kBlock * D;  // bytes per (block, head)
+  const bool k_second = (c >> 3) != 0;              // this lane's K rows are in block 1
+  const int tk0 = 8 * ((c >> 2) & 1) + (c & 3);
+  const bool v_second = (j >> 1) != 0;              // this lane's P·V tokens are in block 1
+  const int tv0 = 8 * (j & 1);
+
+  for (int ib = 0; ib < nblk; ib += 2) {
+    int32_t b0 = btab[ib];
+    const bool has1 = ib + 1 < nblk;
+    int32_t b1 = has1 ? btab[ib + 1] : b0;
+    const int rem = tok_end - (tok0 + ib * kBlock);
+    int lim0 = rem < kBlock ? rem : kBlock;
+    int lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
+    if (b0 < 0 || b0 >= num_blocks) { b0 = 0; lim0 = 0; }
+    if (b1 < 0 || b1 >= num_blocks) { b1 = 0; lim1 = 0; }
+
+    const uint8_t* kr =
+        kc + ((int64_t)(k_second ? b1 : b0) * Hkv + kvh) * head_stride + tk0 * D + DL * j;
+    uint2 kw0[KS], kw1[KS];  // 8 bytes per reduction step, token tk0 / tk0 + 4
+#pragma unroll
+    for (int s = 0; s < KS; s += 2) {
+      const uint4 x0 = *reinterpret_cast<const uint4*>(kr + 8 * s);
+      const uint4 x1 = *reinterpret_cast<const uint4*>(kr + 4 * D + 8 * s);
+      kw0[s] = uint2{x0.x, x0.y};
+      kw0[s + 1] = uint2{x0.z, x0.w};
+      kw1[s] = uint2{x1.x, x1.y};
+      kw1[s + 1] = uint2{x1.z, x1.w};
+    }
+    const uint8_t* vr =
+        vc + ((int64_t)(v_second ? b1 : b0) * Hkv + kvh) * head_stride + c * kBlock + tv0;
+    uint64_t vw[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) vw[dt] = *reinterpret_cast<const uint64_t*>(vr + dt * 16 * kBlock);
+
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(kw0[s].x, kw0[s].y), qv[s], s0,
+                                                   0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(kw1[s].x, kw1[s].y), qv[s], s1,
+                                                   0, 0, 0);
+    }
+
+    // x[i] <-> token tv0 + i of this lane's block (s0: i < 4, s1: i >= 4)
+    float x[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = s0[r] * scale_log2;
+      x[4 + r] = s1[r] * scale_log2;
+    }
+    if (lim0 < kBlock || lim1 < kBlock) {  // wave-uniform
+      const int lim = v_second ? lim1 : lim0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (tv0 + i >= lim) x[i] = -INFINITY;
+      // Stale codes past the context may be anything; zero them so the
+      // P·V product only sees zeros there.
+      const int n = min(max(lim - tv0, 0), 8);
+      const uint64_t mk = n >= 8 ? ~0ull : ((1ull << (8 * n)) - 1);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) vw[dt] &= mk;
+    }
+
+    float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                     fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    if (__builtin_amdgcn_ballot_w64(bm > m + 8.0f)) {
+      bm = fmaxf(bm, shfl_xor_f(bm, 16));
+      bm = fmaxf(bm, shfl_xor_f(bm, 32));
+      const float mn = fmaxf(m, bm);
+      const float a = fast_exp2(m - mn);
+      m = mn;
+      lsum *= a;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= a;
+    }
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = fast_exp2(x[i] - m);
+      lsum += p[i];
+    }
+    bf16x8 pb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pb[i] = (__bf16)p[i];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          fp8x8_to_bf16((uint32_t)vw[dt], (uint32_t)(vw[dt] >> 32)), pb, o[dt], 0, 0, 0);
+  }
+
+  lsum += shfl_xor_f(lsum, 16);
+  lsum += shfl_xor_f(lsum, 32);
+  if (c >= G) return;
+  if (num_parts == 1) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    uint16_t* orow = out + ((int64_t)seq * Hq + head) * D + 4 * j;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      uint16_t w[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[r] = f32_to_bf16_bits(o[dt][r] * inv);
+      *reinterpret_cast<uint64_t*>(orow + 16 * dt) = *reinterpret_cast<const uint64_t*>(w);
+    }
+  } else {
+    const int64_t row = ((int64_t)seq * Hq + head) * num_parts + part;
+    float* orow = ws_o + row * D + 4 * j;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(orow + 16 * dt) = o[dt];
+    if (j == 0) {
+      ws_ml[2 * row] = m;
+      ws_ml[2 * row + 1] = lsum;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Generic decode kernel: one workgroup of 256 threads per (partition, query
 // head, sequence).  Scores go through LDS; f32 accumulation throughout.
-template <typename T>
+template <typename T, typename TC = T>
 __global__ __launch_bounds__(256) void decode_generic_kernel(
-    T* __restrict__ out, const T* __restrict__ q, const T* __restrict__ kc,
-    const T* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    T* __restrict__ out, const T* __restrict__ q, const TC* __restrict__ kc,
+    const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int D, int num_blocks,
     float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   __shared__ float qs[512];
@@ -255,9 +438,9 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
     const int32_t b = bs[t / kBlock];
     float s = -INFINITY;
     if (b >= 0) {
-      const T* kr = kc + (((int64_t)b * Hkv + kvh) * kBlock + t % kBlock) * D;
+      const TC* kr = kc + (((int64_t)b * Hkv + kvh) * kBlock + t % kBlock) * D;
       float acc = 0.f;
-      for (int d = 0; d < D; ++d) acc += qs[d] * Elem<T>::load(kr + d);
+      for (int d = 0; d < D; ++d) acc += qs[d] * Elem<TC>::load(kr + d);
       s = acc * scale_log2;
     }
     ps[t] = s;
@@ -289,7 +472,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
     for (int t = 0; t < n; ++t) {
       const int32_t b = bs[t / kBlock];
       if (b < 0) continue;
-      acc += ps[t] * Elem<T>::load(vc + (((int64_t)b * Hkv + kvh) * D + d) * kBlock + t % kBlock);
+      acc += ps[t] * Elem<TC>::load(vc + (((int64_t)b * Hkv + kvh) * D + d) * kBlock + t % kBlock);
     }
     if (num_parts == 1) {
       Elem<T>::store(out + ((int64_t)seq * Hq + h) * D + d, l > 0.f ? acc / l : 0.f);
@@ -390,7 +573,8 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
                              int32_t head_dim, int32_t num_blocks, float scale, void* workspace,
                              size_t workspace_bytes, int32_t dtype, pa_stream_t stream) {
   clear_error();
-  PA_REQUIRE(dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_decode: unknown dtype %d", dtype);
+  PA_REQUIRE(dtype_ok(dtype) || dtype == PA_DTYPE_FP8_E4M3, PA_ERR_INVALID_ARG,
+             "pa_decode: unknown dtype %d", dtype);
   PA_REQUIRE(num_seqs >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
                  num_blocks > 0 && max_blocks_per_seq > 0 && max_context_len >= 0,
              PA_ERR_INVALID_ARG, "pa_decode: bad sizes");
@@ -404,7 +588,8 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
   PA_REQUIRE(out && q && k_cache && v_cache && block_tables && context_lens, PA_ERR_INVALID_ARG,
              "pa_decode: null pointer");
   const int G = num_heads / num_kv_heads;
-  const bool mfma = dtype == PA_DTYPE_BF16 && G <= 16 &&
+  const bool fp8 = dtype == PA_DTYPE_FP8_E4M3;
+  const bool mfma = (dtype == PA_DTYPE_BF16 || fp8) && G <= 16 &&
                     (head_dim == 64 || head_dim == 128 || head_dim == 256);
   const int part_len = mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len) : kPart;
   const int np = num_partitions(max_context_len, part_len);
@@ -425,22 +610,34 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
     const dim3 grid(np, num_kv_heads, num_seqs);
     auto* o = (uint16_t*)out;
     auto* qq = (const uint16_t*)q;
-    auto* kc = (const uint16_t*)k_cache;
-    auto* vc = (const uint16_t*)v_cache;
-#define PA_LAUNCH_MFMA(DD)                                                                      \
-  decode_mfma_kernel<DD><<<grid, 64, 0, s>>>(o, qq, kc, vc, block_tables, max_blocks_per_seq,   \
-                                             context_lens, num_heads, num_kv_heads, G,          \
-                                             num_blocks, scale_log2, np, part_len, ws_o, ws_ml)
-    if (head_dim == 64)
-      PA_LAUNCH_MFMA(64);
-    else if (head_dim == 128)
-      PA_LAUNCH_MFMA(128);
-    else
-      PA_LAUNCH_MFMA(256);
+#define PA_LAUNCH_MFMA(KERNEL, TC, DD)                                                          \
+  KERNEL<DD><<<grid, 64, 0, s>>>(o, qq, (const TC*)k_cache, (const TC*)v_cache, block_tables,  \
+                                 max_blocks_per_seq, context_lens, num_heads, num_kv_heads, G, \
+                                 num_blocks, scale_log2, np, part_len, ws_o, ws_ml)
+    if (fp8) {
+      if (head_dim == 64)
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 64);
+      else if (head_dim == 128)
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 128);
+      else
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 256);
+    } else {
+      if (head_dim == 64)
+        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 64);
+      else if (head_dim == 128)
+        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 128);
+      else
+        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 256);
+    }
 #undef PA_LAUNCH_MFMA
   } else {
     const dim3 grid(np, num_heads, num_seqs);
-    if (dtype == PA_DTYPE_BF16)
+    if (fp8)
+      decode_generic_kernel<uint16_t, Fp8><<<grid, 256, 0, s>>>(
+          (uint16_t*)out, (const uint16_t*)q, (const Fp8*)k_cache, (const Fp8*)v_cache,
+          block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
+          num_blocks, scale_log2, np, ws_o, ws_ml);
+    else if (dtype == PA_DTYPE_BF16)
       decode_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
@@ -454,7 +651,7 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
   int32_t rc = check_launch("pa_decode");
   if (rc != PA_OK || np == 1) return rc;
   const dim3 rgrid(num_seqs * num_heads);
-  if (dtype == PA_DTYPE_BF16)
+  if (dtype == PA_DTYPE_BF16 || fp8)
     decode_reduce_kernel<uint16_t><<<rgrid, 256, 0, s>>>((uint16_t*)out, ws_o, ws_ml,
                                                          context_lens, num_heads, head_dim, np,
                                                          max_blocks_per_seq, part_len);

@@ -45,11 +45,57 @@ struct Elem<uint16_t> {
   __device__ static inline void store(uint16_t* p, float x) { *p = f32_to_bf16_bits(x); }
 };
 
+// FP8 E4M3 in the reference's convention
+// (crates/model/src/components/kv_cache_fp8.rs:143-212): bias 7, normals
+// only, NaN -> 0x80, +-inf -> 0x7C / 0xFC, |v| < 2^-6 -> +0, the significand
+// rounded to 3 bits half-up, a biased exponent above 14 (before or after
+// rounding) saturating to 0x7B / 0xFB (+-352).  Integer arithmetic only, so
+// host and device agree bit for bit.
+__host__ __device__ inline uint8_t fp8_encode(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const uint32_t sign = u >> 31, a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return 0x80;
+  if (a == 0x7f800000u) return sign ? 0xFC : 0x7C;
+  int be = (int)(a >> 23) - 127 + 7;  // f32 subnormals land far below 1
+  if (a == 0 || be <= 0) return 0;
+  const uint8_t sat = sign ? 0xFB : 0x7B;
+  if (be > 14) return sat;
+  // floor(f * 8 + 0.5) - 8 for the significand f = 1 + mant / 2^23
+  uint32_t r = ((a & 0x7fffffu) + (1u << 19)) >> 20;
+  if (r >= 8) {
+    ++be;
+    r = 0;
+  }
+  if (be > 14) return sat;
+  return (uint8_t)((sign << 7) | ((uint32_t)be << 3) | r);
+}
+// The f32 value of the reference's f16 decode: 0x80 -> NaN, 0x7C / 0xFC ->
+// +-inf, exponent and mantissa 0 -> +-0, else (-1)^s 2^(e-7) (1 + m/8).
+__host__ __device__ inline float fp8_decode(uint32_t b) {
+  if (b == 0x80) return __builtin_nanf("");
+  if (b == 0x7C) return __builtin_inff();
+  if (b == 0xFC) return -__builtin_inff();
+  const uint32_t sign = (b >> 7) & 1, e = (b >> 3) & 15, m = b & 7;
+  if (e == 0 && m == 0) return __builtin_bit_cast(float, sign << 31);
+  return __builtin_bit_cast(float, (sign << 31) | ((e + 120) << 23) | (m << 20));
+}
+// FP8 cache element (one byte).
+struct Fp8 {
+  uint8_t bits;
+};
+template <>
+struct Elem<Fp8> {
+  __device__ static inline float load(const Fp8* p) { return fp8_decode(p->bits); }
+  __device__ static inline void store(Fp8* p, float x) { p->bits = fp8_encode(x); }
+};
+
 // Thread-local last-error message behind pa_last_error().
 void set_error(const char* fmt, ...);
 void clear_error();
 
-inline size_t dtype_size(int32_t dtype) { return dtype == PA_DTYPE_BF16 ? 2 : 4; }
+inline size_t dtype_size(int32_t dtype) {
+  return dtype == PA_DTYPE_BF16 ? 2 : dtype == PA_DTYPE_FP8_E4M3 ? 1 : 4;
+}
 inline bool dtype_ok(int32_t dtype) { return dtype == PA_DTYPE_F32 || dtype == PA_DTYPE_BF16; }
 
 // Checks the launch that was just enqueued.

@@ -661,10 +661,10 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
 
 // Generic: one wavefront per (query row, head); keys in chunks of 64 with
 // an online softmax; lane d accumulates output dims d, d + 64, ...
-template <typename T>
+template <typename T, typename TC = T>
 __global__ __launch_bounds__(64) void prefill_generic_kernel(
-    T* __restrict__ out, const T* __restrict__ q, const T* __restrict__ kc,
-    const T* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    T* __restrict__ out, const T* __restrict__ q, const TC* __restrict__ kc,
+    const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
     int D, int num_blocks, float scale_log2) {
   __shared__ float qs[512];
@@ -692,9 +692,9 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
     float s = -INFINITY;
     const int32_t b = bids[lane / kBlock];
     if (key <= pos && b >= 0) {
-      const T* kr = kc + (((int64_t)b * Hkv + kvh) * kBlock + key % kBlock) * D;
+      const TC* kr = kc + (((int64_t)b * Hkv + kvh) * kBlock + key % kBlock) * D;
       float a = 0.f;
-      for (int d = 0; d < D; ++d) a += qs[d] * Elem<T>::load(kr + d);
+      for (int d = 0; d < D; ++d) a += qs[d] * Elem<TC>::load(kr + d);
       s = a * scale_log2;
     }
     float bm = s;
@@ -715,8 +715,8 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
       for (int t = 0; t < nk; ++t) {
         const int32_t bt = bids[t / kBlock];
         if (bt < 0) continue;
-        a += ps[t] * Elem<T>::load(vc + (((int64_t)bt * Hkv + kvh) * D + d) * kBlock +
-                                   (k0 + t) % kBlock);
+        a += ps[t] * Elem<TC>::load(vc + (((int64_t)bt * Hkv + kvh) * D + d) * kBlock +
+                                    (k0 + t) % kBlock);
       }
       acc[i] = a;
     }
@@ -739,7 +739,8 @@ extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, con
                               int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                               int32_t num_blocks, float scale, int32_t dtype, pa_stream_t stream) {
   clear_error();
-  PA_REQUIRE(dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_prefill: unknown dtype %d", dtype);
+  PA_REQUIRE(dtype_ok(dtype) || dtype == PA_DTYPE_FP8_E4M3, PA_ERR_INVALID_ARG,
+             "pa_prefill: unknown dtype %d", dtype);
   PA_REQUIRE(num_seqs >= 0 && total_q >= 0 && max_q_len >= 0 && num_heads > 0 &&
                  num_kv_heads > 0 && head_dim > 0 && num_blocks > 0 && max_blocks_per_seq > 0,
              PA_ERR_INVALID_ARG, "pa_prefill: bad sizes");
@@ -793,7 +794,12 @@ extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, con
 #undef PA_LAUNCH_PREFILL
   } else {
     const dim3 grid(max_q_len, num_heads, num_seqs);
-    if (dtype == PA_DTYPE_BF16)
+    if (dtype == PA_DTYPE_FP8_E4M3)
+      prefill_generic_kernel<uint16_t, Fp8><<<grid, 64, 0, s>>>(
+          (uint16_t*)out, (const uint16_t*)q, (const Fp8*)k_cache, (const Fp8*)v_cache,
+          block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
+          head_dim, num_blocks, scale_log2);
+    else if (dtype == PA_DTYPE_BF16)
       prefill_generic_kernel<uint16_t><<<grid, 64, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,

@@ -14,6 +14,8 @@ from . import _lib
 
 BLOCK_SIZE = 16
 _DTYPES = {torch.float32: 0, torch.bfloat16: 1}
+# FP8-E4M3 caches (the reference's codes) are uint8 tensors; q / out are bf16.
+FP8 = 2
 
 
 class PaError(RuntimeError):
@@ -50,7 +52,8 @@ def _dtype_code(t):
 
 
 def new_cache(num_blocks, num_kv_heads, head_dim, dtype, device="cuda"):
-    """Zeroed (k_cache [NB, H, 16, D], v_cache [NB, H, D, 16]) for one layer."""
+    """Zeroed (k_cache [NB, H, 16, D], v_cache [NB, H, D, 16]) for one layer;
+    dtype torch.uint8 makes FP8-E4M3 caches."""
     k = torch.zeros(num_blocks, num_kv_heads, BLOCK_SIZE, head_dim, dtype=dtype, device=device)
     v = torch.zeros(num_blocks, num_kv_heads, head_dim, BLOCK_SIZE, dtype=dtype, device=device)
     return k, v
@@ -82,6 +85,37 @@ def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
         key.stride(0), value.stride(0), _dtype_code(k_cache), _stream(k_cache)))
 
 
+def _cache_code(k_cache, q=None):
+    """dtype code of a (q, cache) pair: uint8 caches are FP8 with bf16 q."""
+    if k_cache.dtype == torch.uint8:
+        if q is not None and q.dtype != torch.bfloat16:
+            raise ValueError("FP8 caches take bf16 q")
+        return FP8
+    if q is not None and q.dtype != k_cache.dtype:
+        raise ValueError("q must be in the cache dtype")
+    return _dtype_code(k_cache)
+
+
+def reshape_and_cache_fp8(key, value, k_cache, v_cache, slot_mapping):
+    """Quantise key/value [T, H, D] (f32 or bf16) into uint8 FP8 caches at
+    slot_mapping [T] (int64), with the reference's E4M3 encoder."""
+    _dev(k_cache, v_cache, slot_mapping)
+    nb, h, d = _cache_dims(k_cache, v_cache)
+    if k_cache.dtype != torch.uint8:
+        raise ValueError("FP8 caches are uint8")
+    t = key.shape[0]
+    if key.shape[1:] != (h, d) or value.shape != key.shape or slot_mapping.shape != (t,):
+        raise ValueError("key/value must be [T, H, D] matching the cache; slot_mapping [T]")
+    if slot_mapping.dtype != torch.int64 or value.dtype != key.dtype:
+        raise ValueError("dtype mismatch")
+    if key.stride(2) != 1 or key.stride(1) != d or value.stride(2) != 1 or value.stride(1) != d:
+        raise ValueError("key/value rows must be contiguous [H, D]")
+    lib = _lib.load()
+    _check("pa_reshape_and_cache_fp8", lib.pa_reshape_and_cache_fp8(
+        _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), t, h, d, nb,
+        key.stride(0), value.stride(0), _dtype_code(key), _stream(k_cache)))
+
+
 def slot_mapping(block_tables, positions, cu_seq_tokens):
     """Device slot mapping from block tables [B, MBS] (int32), positions [T]
     (int64) and cumulative token counts [B + 1] (int32)."""
@@ -96,15 +130,17 @@ def slot_mapping(block_tables, positions, cu_seq_tokens):
 
 
 def read_kv(k_cache, v_cache, block_ids, seq_len):
-    """Gather one sequence's first seq_len tokens -> (k, v) [seq_len, H, D]."""
+    """Gather one sequence's first seq_len tokens -> (k, v) [seq_len, H, D]
+    (f32 dequantised values for FP8 caches)."""
     _dev(k_cache, v_cache, block_ids)
     nb, h, d = _cache_dims(k_cache, v_cache)
-    out_k = torch.empty(seq_len, h, d, dtype=k_cache.dtype, device=k_cache.device)
+    odt = torch.float32 if k_cache.dtype == torch.uint8 else k_cache.dtype
+    out_k = torch.empty(seq_len, h, d, dtype=odt, device=k_cache.device)
     out_v = torch.empty_like(out_k)
     lib = _lib.load()
     _check("pa_read_kv", lib.pa_read_kv(
         _ptr(k_cache), _ptr(v_cache), _ptr(block_ids), block_ids.shape[0], seq_len, h, d, nb,
-        _ptr(out_k), _ptr(out_v), _dtype_code(k_cache), _stream(k_cache)))
+        _ptr(out_k), _ptr(out_v), _cache_code(k_cache), _stream(k_cache)))
     return out_k, out_v
 
 
@@ -134,8 +170,9 @@ def decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len, sca
     _dev(q, k_cache, v_cache, block_tables, context_lens)
     nb, hkv, d = _cache_dims(k_cache, v_cache)
     b, hq, dq = q.shape
-    if dq != d or q.dtype != k_cache.dtype:
-        raise ValueError("q must be [B, Hq, D] in the cache dtype")
+    if dq != d:
+        raise ValueError("q must be [B, Hq, D]")
+    code = _cache_code(k_cache, q)
     if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
         raise ValueError("block_tables / context_lens must be int32")
     if scale is None:
@@ -150,7 +187,7 @@ def decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len, sca
     _check("pa_decode", lib.pa_decode(
         _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
         block_tables.shape[1], _ptr(context_lens), max_context_len, b, hq, hkv, d, nb,
-        float(scale), _ptr(workspace), ws_bytes, _dtype_code(q), _stream(q)))
+        float(scale), _ptr(workspace), ws_bytes, code, _stream(q)))
     return out
 
 
@@ -160,8 +197,9 @@ def prefill(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens, max_q_len, 
     _dev(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens)
     nb, hkv, d = _cache_dims(k_cache, v_cache)
     tq, hq, dq = q.shape
-    if dq != d or q.dtype != k_cache.dtype:
-        raise ValueError("q must be [total_q, Hq, D] in the cache dtype")
+    if dq != d:
+        raise ValueError("q must be [total_q, Hq, D]")
+    code = _cache_code(k_cache, q)
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     if out is None:
@@ -170,7 +208,7 @@ def prefill(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens, max_q_len, 
     _check("pa_prefill", lib.pa_prefill(
         _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
         block_tables.shape[1], _ptr(cu_q_lens), _ptr(past_lens), block_tables.shape[0], tq,
-        max_q_len, hq, hkv, d, nb, float(scale), _dtype_code(q), _stream(q)))
+        max_q_len, hq, hkv, d, nb, float(scale), code, _stream(q)))
     return out
 
 
