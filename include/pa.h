@@ -210,6 +210,19 @@ int32_t pa_decode(void* out, const void* q, const void* k_cache, const void* v_c
                   float scale, void* workspace, size_t workspace_bytes, int32_t dtype,
                   pa_stream_t stream);
 
+/* pa_decode over a quantised PagedKvCache (int8 values in f32 caches with
+ * one scale per block, pa_kv_cache_create_quantized): every K / V element
+ * is read as value * block_scales[block], which is what the reference's
+ * read_kv returns for such a cache (buffer.rs:320-331) before attention.
+ * f32 q / out; block_scales device f32 [num_blocks]. */
+int32_t pa_decode_quantized(void* out, const void* q, const float* k_cache, const float* v_cache,
+                            const float* block_scales, const int32_t* block_tables,
+                            int32_t max_blocks_per_seq, const int32_t* context_lens,
+                            int32_t max_context_len, int32_t num_seqs, int32_t num_heads,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                            float scale, void* workspace, size_t workspace_bytes,
+                            pa_stream_t stream);
+
 /* Chunked causal prefill over the paged cache.
  *   out, q        [total_q, Hq, D]; sequence s owns rows
  *                 cu_q_lens[s] .. cu_q_lens[s+1]-1
@@ -228,6 +241,16 @@ int32_t pa_prefill(void* out, const void* q, const void* k_cache, const void* v_
                    int32_t total_q, int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
                    int32_t head_dim, int32_t num_blocks, float scale, int32_t dtype,
                    pa_stream_t stream);
+
+/* pa_prefill over a quantised PagedKvCache, reading values as in
+ * pa_decode_quantized (f32 q / out). */
+int32_t pa_prefill_quantized(void* out, const void* q, const float* k_cache, const float* v_cache,
+                             const float* block_scales, const int32_t* block_tables,
+                             int32_t max_blocks_per_seq, const int32_t* cu_q_lens,
+                             const int32_t* past_lens, int32_t num_seqs, int32_t total_q,
+                             int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t num_blocks, float scale,
+                             pa_stream_t stream);
 
 #ifdef __cplusplus
 }

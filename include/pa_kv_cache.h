@@ -34,6 +34,19 @@ int32_t pa_kv_cache_create(int32_t num_layers, int32_t num_kv_heads, int32_t hea
                            int32_t num_blocks, int32_t dtype, pa_kv_cache** out);
 void pa_kv_cache_destroy(pa_kv_cache* cache);
 
+/* PagedKvCache::new(..., quantized = true) (tensor_store/mod.rs:50-84): an
+ * f32 cache holding int8 values with one scale per block (all 1.0 at
+ * creation, mod.rs:69).  Every write re-quantises the block it lands in as
+ * write_kv does (buffer.rs:170-231): dequantise with the block's scale,
+ * store the token, scale = max(max|K|, max|V|) / 127 (1 for an all-zero
+ * block), values round(x / scale); tokens are applied in order.  read_kv
+ * returns x * scale + 0.0 per block (buffer.rs:320-331). */
+int32_t pa_kv_cache_create_quantized(int32_t num_layers, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t num_blocks, pa_kv_cache** out);
+int32_t pa_kv_cache_is_quantized(const pa_kv_cache* cache);
+/* Device f32 [num_blocks] block scales of one layer (NULL unless quantised). */
+float* pa_kv_cache_scales_ptr(pa_kv_cache* cache, int32_t layer);
+
 /* Accessors (tensor_store/layout.rs:15-44). */
 int32_t pa_kv_cache_num_layers(const pa_kv_cache* cache);
 int32_t pa_kv_cache_num_blocks(const pa_kv_cache* cache);

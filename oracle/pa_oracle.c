@@ -503,8 +503,9 @@ int oracle_quant_write_kv(float* k_cache, float* v_cache, float* scales, int num
   return ORC_OK;
 }
 
-/* read_kv, quantised branch (buffer.rs:320-331): each block is multiplied by
- * its own scale.  Same walk as oracle_read_kv, f32 only. */
+/* read_kv, quantised branch (buffer.rs:320-331): each block goes through
+ * candle's affine(scale, 0.0), i.e. x * scale + 0.0 in f32 (so a stored -0
+ * reads back as +0).  Same walk as oracle_read_kv, f32 only. */
 int oracle_quant_read_kv(const float* k_cache, const float* v_cache, const float* scales,
                          int num_blocks, int H, int D, const int64_t* block_ids, int n_ids,
                          int seq_len, float* out_k, float* out_v) {
@@ -514,8 +515,8 @@ int oracle_quant_read_kv(const float* k_cache, const float* v_cache, const float
   for (int t = 0; t < n; ++t) {
     float s = scales[block_ids[t / PA_BLOCK]];
     for (size_t i = 0; i < (size_t)H * D; ++i) {
-      out_k[(size_t)t * H * D + i] *= s;
-      out_v[(size_t)t * H * D + i] *= s;
+      out_k[(size_t)t * H * D + i] = out_k[(size_t)t * H * D + i] * s + 0.0f;
+      out_v[(size_t)t * H * D + i] = out_v[(size_t)t * H * D + i] * s + 0.0f;
     }
   }
   return n;

@@ -219,3 +219,17 @@ def test_quant_per_block_scale(oracle):
         assert abs(rk[t, 0, 0] - x) < tol and abs(rv[t, 0, 0] - x) < tol
     # values sit on the int8 grid of their own block's scale
     assert np.all(np.abs(kc) <= 127) and np.all(kc == np.round(kc))
+
+
+def test_quant_read_is_affine_plus_zero(oracle):
+    # buffer.rs:320-331 reads a quantised block through candle's
+    # affine(scale, 0.0): x * scale + 0.0, so a stored -0 (round(-0.3) in the
+    # write) reads back as +0
+    kc = np.zeros((1, 1, 16, 2), np.float32)
+    vc = np.zeros_like(kc)
+    scales = np.ones(1, np.float32)
+    k = np.array([[-0.3, 100.0]], np.float32)  # scale 100/127: -0.3 -> round(-0.38) = -0
+    assert oracle.quant_write_kv(kc, vc, scales, 0, 0, k, k) == 0
+    assert np.signbit(kc[0, 0, 0, 0]) and kc[0, 0, 0, 0] == 0.0
+    n, rk, rv = oracle.quant_read_kv(kc, vc, scales, [0], 1)
+    assert rk[0, 0, 0].view(np.uint32) == 0 and rk[0, 0, 1] == np.float32(127.0) * scales[0]

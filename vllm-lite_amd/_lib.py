@@ -23,6 +23,13 @@ SIGNATURES = {
                          _p, _sz, _i32, _p]),
     "pa_prefill": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                           _i32, _f32, _i32, _p]),
+    "pa_decode_quantized": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32,
+                                   _i32, _i32, _f32, _p, _sz, _p]),
+    "pa_prefill_quantized": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32,
+                                    _i32, _i32, _i32, _f32, _p]),
+    "pa_kv_cache_create_quantized": (_i32, [_i32, _i32, _i32, _i32, C.POINTER(_p)]),
+    "pa_kv_cache_is_quantized": (_i32, [_p]),
+    "pa_kv_cache_scales_ptr": (_p, [_p, _i32]),
     "pa_rope_reshape_and_cache": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i32,
                                          _i32, _i32, _i32, _i32, _i32, _p]),
     "pa_rope_inv_freq": (_i32, [_i32, _f32, _i32, _f32, _i32, _i32, _p, _p, _p]),

@@ -406,7 +406,9 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
     T* __restrict__ out, const T* __restrict__ q, const TC* __restrict__ kc,
     const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int D, int num_blocks,
-    float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+    float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    const float* __restrict__ kv_scales) {
+  // kv_scales: per-block scales of a quantised (int8-in-f32) cache, or null
   __shared__ float qs[512];
   __shared__ float ps[kPart];
   __shared__ int32_t bs[kPart / kBlock];
@@ -439,8 +441,9 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
     float s = -INFINITY;
     if (b >= 0) {
       const TC* kr = kc + (((int64_t)b * Hkv + kvh) * kBlock + t % kBlock) * D;
+      const float ks = kv_scales ? kv_scales[b] : 1.0f;
       float acc = 0.f;
-      for (int d = 0; d < D; ++d) acc += qs[d] * Elem<TC>::load(kr + d);
+      for (int d = 0; d < D; ++d) acc += qs[d] * (Elem<TC>::load(kr + d) * ks);
       s = acc * scale_log2;
     }
     ps[t] = s;
@@ -472,7 +475,8 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
     for (int t = 0; t < n; ++t) {
       const int32_t b = bs[t / kBlock];
       if (b < 0) continue;
-      acc += ps[t] * Elem<TC>::load(vc + (((int64_t)b * Hkv + kvh) * D + d) * kBlock + t % kBlock);
+      const float vs = kv_scales ? kv_scales[b] : 1.0f;
+      acc += ps[t] * (Elem<TC>::load(vc + (((int64_t)b * Hkv + kvh) * D + d) * kBlock + t % kBlock) * vs);
     }
     if (num_parts == 1) {
       Elem<T>::store(out + ((int64_t)seq * Hq + h) * D + d, l > 0.f ? acc / l : 0.f);
@@ -566,12 +570,13 @@ extern "C" size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, 
   return (size_t)num_seqs * num_heads * np * (head_dim + 2) * sizeof(float);
 }
 
-extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, const void* v_cache,
-                             const int32_t* block_tables, int32_t max_blocks_per_seq,
-                             const int32_t* context_lens, int32_t max_context_len,
-                             int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
-                             int32_t head_dim, int32_t num_blocks, float scale, void* workspace,
-                             size_t workspace_bytes, int32_t dtype, pa_stream_t stream) {
+namespace {
+int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v_cache,
+                    const float* kv_scales, const int32_t* block_tables,
+                    int32_t max_blocks_per_seq, const int32_t* context_lens,
+                    int32_t max_context_len, int32_t num_seqs, int32_t num_heads,
+                    int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks, float scale,
+                    void* workspace, size_t workspace_bytes, int32_t dtype, pa_stream_t stream) {
   clear_error();
   PA_REQUIRE(dtype_ok(dtype) || dtype == PA_DTYPE_FP8_E4M3, PA_ERR_INVALID_ARG,
              "pa_decode: unknown dtype %d", dtype);
@@ -589,7 +594,7 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
              "pa_decode: null pointer");
   const int G = num_heads / num_kv_heads;
   const bool fp8 = dtype == PA_DTYPE_FP8_E4M3;
-  const bool mfma = (dtype == PA_DTYPE_BF16 || fp8) && G <= 16 &&
+  const bool mfma = !kv_scales && (dtype == PA_DTYPE_BF16 || fp8) && G <= 16 &&
                     (head_dim == 64 || head_dim == 128 || head_dim == 256);
   const int part_len = mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len) : kPart;
   const int np = num_partitions(max_context_len, part_len);
@@ -636,17 +641,17 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
       decode_generic_kernel<uint16_t, Fp8><<<grid, 256, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const Fp8*)k_cache, (const Fp8*)v_cache,
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
-          num_blocks, scale_log2, np, ws_o, ws_ml);
+          num_blocks, scale_log2, np, ws_o, ws_ml, nullptr);
     else if (dtype == PA_DTYPE_BF16)
       decode_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
-          num_blocks, scale_log2, np, ws_o, ws_ml);
+          num_blocks, scale_log2, np, ws_o, ws_ml, nullptr);
     else
       decode_generic_kernel<float><<<grid, 256, 0, s>>>(
           (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
-          num_blocks, scale_log2, np, ws_o, ws_ml);
+          num_blocks, scale_log2, np, ws_o, ws_ml, kv_scales);
   }
   int32_t rc = check_launch("pa_decode");
   if (rc != PA_OK || np == 1) return rc;
@@ -660,4 +665,34 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
                                                       num_heads, head_dim, np,
                                                       max_blocks_per_seq, part_len);
   return check_launch("pa_decode reduce");
+}
+}  // namespace
+
+extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, const void* v_cache,
+                             const int32_t* block_tables, int32_t max_blocks_per_seq,
+                             const int32_t* context_lens, int32_t max_context_len,
+                             int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t num_blocks, float scale, void* workspace,
+                             size_t workspace_bytes, int32_t dtype, pa_stream_t stream) {
+  return decode_impl(out, q, k_cache, v_cache, nullptr, block_tables, max_blocks_per_seq,
+                     context_lens, max_context_len, num_seqs, num_heads, num_kv_heads, head_dim,
+                     num_blocks, scale, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" int32_t pa_decode_quantized(void* out, const void* q, const float* k_cache,
+                                       const float* v_cache, const float* block_scales,
+                                       const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                       const int32_t* context_lens, int32_t max_context_len,
+                                       int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t num_blocks, float scale,
+                                       void* workspace, size_t workspace_bytes,
+                                       pa_stream_t stream) {
+  if (!block_scales) {
+    clear_error();
+    set_error("pa_decode_quantized: null block_scales");
+    return PA_ERR_INVALID_ARG;
+  }
+  return decode_impl(out, q, k_cache, v_cache, block_scales, block_tables, max_blocks_per_seq,
+                     context_lens, max_context_len, num_seqs, num_heads, num_kv_heads, head_dim,
+                     num_blocks, scale, workspace, workspace_bytes, PA_DTYPE_F32, stream);
 }

@@ -4,18 +4,24 @@
 // reference's write_kv / write_kv_batch / write_prefill_kv / read_kv on top
 // of the stateless kernels: index arithmetic and bounds checks run on the
 // host exactly where the reference checks them, the data movement is one
-// kernel launch per call.
+// kernel launch per call.  A quantised cache (the reference's
+// quantized = true) keeps int8 values in f32 with one scale per block; its
+// writes re-quantise whole blocks (quant.hip).
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <map>
 #include <vector>
 
 #include "../../include/pa_kv_cache.h"
 #include "pa_common.hpp"
+#include "pa_internal.hpp"
 
 struct pa_kv_cache {
   int num_layers = 0, num_heads = 0, head_dim = 0, num_blocks = 0, dtype = 0;
+  bool quantized = false;
   std::vector<void*> key, value;
+  std::vector<float*> scales;  // quantised caches: [num_blocks] per layer
   // Staging for host index arrays: pinned host copy -> device copy.
   void* host_stage = nullptr;
   void* dev_stage = nullptr;
@@ -69,9 +75,45 @@ int32_t finish(hipStream_t stream, int32_t rc) {
   return PA_OK;
 }
 
+// Quantised write of T tokens at host-computed slots: the tokens are grouped
+// by block (keeping their order) and each block is re-quantised once per
+// token, as write_kv does.
+int32_t quant_scatter(pa_kv_cache* c, int layer, const std::vector<int64_t>& slots, const void* k,
+                      const void* v, hipStream_t stream) {
+  std::map<int64_t, std::vector<int32_t>> by_block;  // block -> token indices, in order
+  for (size_t t = 0; t < slots.size(); ++t) by_block[slots[t] / pa::kBlock].push_back((int32_t)t);
+  const int tasks = (int)by_block.size();
+  const int T = (int)slots.size();
+  std::vector<int32_t> host(tasks + (tasks + 1) + 2 * T);
+  int32_t* blk = host.data();
+  int32_t* beg = blk + tasks;
+  int32_t* tok = beg + tasks + 1;
+  int32_t* off = tok + T;
+  int w = 0, i = 0;
+  for (const auto& kv : by_block) {
+    blk[w] = (int32_t)kv.first;
+    beg[w] = i;
+    for (int32_t t : kv.second) {
+      tok[i] = t;
+      off[i] = (int32_t)(slots[t] % pa::kBlock);
+      ++i;
+    }
+    ++w;
+  }
+  beg[tasks] = i;
+  int32_t rc = PA_OK;
+  auto* d = (int32_t*)c->upload(host.data(), host.size() * sizeof(int32_t), stream, &rc);
+  if (rc != PA_OK) return rc;
+  rc = pa::launch_quant_write((float*)c->key[layer], (float*)c->value[layer], c->scales[layer],
+                              (const float*)k, (const float*)v, c->num_heads, c->head_dim, tasks,
+                              d, d + tasks, d + 2 * tasks + 1, d + 2 * tasks + 1 + T, stream);
+  return finish(stream, rc);
+}
+
 // Scatters T tokens at host-computed slots.
 int32_t scatter(pa_kv_cache* c, int layer, const std::vector<int64_t>& slots, const void* k,
                 const void* v, hipStream_t stream) {
+  if (c->quantized) return quant_scatter(c, layer, slots, k, v, stream);
   int32_t rc = PA_OK;
   void* d_slots = c->upload(slots.data(), slots.size() * sizeof(int64_t), stream, &rc);
   if (rc != PA_OK) return rc;
@@ -116,10 +158,36 @@ extern "C" int32_t pa_kv_cache_create(int32_t num_layers, int32_t num_kv_heads, 
   return PA_OK;
 }
 
+extern "C" int32_t pa_kv_cache_create_quantized(int32_t num_layers, int32_t num_kv_heads,
+                                                int32_t head_dim, int32_t num_blocks,
+                                                pa_kv_cache** out) {
+  int32_t rc = pa_kv_cache_create(num_layers, num_kv_heads, head_dim, num_blocks, PA_DTYPE_F32,
+                                  out);
+  if (rc != PA_OK) return rc;
+  pa_kv_cache* c = *out;
+  c->quantized = true;
+  const std::vector<float> ones(num_blocks, 1.0f);  // mod.rs:69
+  for (int l = 0; l < num_layers; ++l) {
+    float* sp = nullptr;
+    if (hipMalloc(&sp, num_blocks * sizeof(float)) != hipSuccess ||
+        hipMemcpy(sp, ones.data(), num_blocks * sizeof(float), hipMemcpyHostToDevice) !=
+            hipSuccess) {
+      if (sp) (void)hipFree(sp);
+      pa_kv_cache_destroy(c);
+      *out = nullptr;
+      pa::set_error("pa_kv_cache_create_quantized: allocating the block scales failed");
+      return PA_ERR_HIP;
+    }
+    c->scales.push_back(sp);
+  }
+  return PA_OK;
+}
+
 extern "C" void pa_kv_cache_destroy(pa_kv_cache* c) {
   if (!c) return;
   for (void* p : c->key) (void)hipFree(p);
   for (void* p : c->value) (void)hipFree(p);
+  for (float* p : c->scales) (void)hipFree(p);
   if (c->host_stage) (void)hipHostFree(c->host_stage);
   if (c->dev_stage) (void)hipFree(c->dev_stage);
   delete c;
@@ -131,6 +199,13 @@ extern "C" int32_t pa_kv_cache_block_size(const pa_kv_cache*) { return pa::kBloc
 extern "C" int32_t pa_kv_cache_num_heads(const pa_kv_cache* c) { return c ? c->num_heads : 0; }
 extern "C" int32_t pa_kv_cache_head_dim(const pa_kv_cache* c) { return c ? c->head_dim : 0; }
 extern "C" int32_t pa_kv_cache_dtype(const pa_kv_cache* c) { return c ? c->dtype : -1; }
+
+extern "C" int32_t pa_kv_cache_is_quantized(const pa_kv_cache* c) {
+  return c && c->quantized ? 1 : 0;
+}
+extern "C" float* pa_kv_cache_scales_ptr(pa_kv_cache* c, int32_t layer) {
+  return (c && c->quantized && layer >= 0 && layer < c->num_layers) ? c->scales[layer] : nullptr;
+}
 
 extern "C" void* pa_kv_cache_key_ptr(pa_kv_cache* c, int32_t layer) {
   return (c && layer >= 0 && layer < c->num_layers) ? c->key[layer] : nullptr;
@@ -237,8 +312,13 @@ extern "C" int32_t pa_kv_cache_read_kv(pa_kv_cache* c, int32_t layer, const int6
   int32_t rc = PA_OK;
   void* d_ids = c->upload(ids.data(), ids.size() * sizeof(int32_t), s, &rc);
   if (rc != PA_OK) return rc;
-  rc = pa_read_kv(c->key[layer], c->value[layer], (const int32_t*)d_ids, used, n, c->num_heads,
-                  c->head_dim, c->num_blocks, out_k, out_v, c->dtype, stream);
+  if (c->quantized)
+    rc = pa::launch_quant_read((const float*)c->key[layer], (const float*)c->value[layer],
+                               c->scales[layer], (const int32_t*)d_ids, n, c->num_heads,
+                               c->head_dim, (float*)out_k, (float*)out_v, s);
+  else
+    rc = pa_read_kv(c->key[layer], c->value[layer], (const int32_t*)d_ids, used, n, c->num_heads,
+                    c->head_dim, c->num_blocks, out_k, out_v, c->dtype, stream);
   rc = finish(s, rc);
   if (rc == PA_OK) *n_read = n;
   return rc;

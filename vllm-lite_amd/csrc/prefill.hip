@@ -666,7 +666,8 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
     T* __restrict__ out, const T* __restrict__ q, const TC* __restrict__ kc,
     const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
-    int D, int num_blocks, float scale_log2) {
+    int D, int num_blocks, float scale_log2, const float* __restrict__ kv_scales) {
+  // kv_scales: per-block scales of a quantised (int8-in-f32) cache, or null
   __shared__ float qs[512];
   __shared__ float ps[64];
   __shared__ int32_t bids[64];
@@ -693,8 +694,9 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
     const int32_t b = bids[lane / kBlock];
     if (key <= pos && b >= 0) {
       const TC* kr = kc + (((int64_t)b * Hkv + kvh) * kBlock + key % kBlock) * D;
+      const float ks = kv_scales ? kv_scales[b] : 1.0f;
       float a = 0.f;
-      for (int d = 0; d < D; ++d) a += qs[d] * Elem<TC>::load(kr + d);
+      for (int d = 0; d < D; ++d) a += qs[d] * (Elem<TC>::load(kr + d) * ks);
       s = a * scale_log2;
     }
     float bm = s;
@@ -715,8 +717,10 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
       for (int t = 0; t < nk; ++t) {
         const int32_t bt = bids[t / kBlock];
         if (bt < 0) continue;
-        a += ps[t] * Elem<TC>::load(vc + (((int64_t)bt * Hkv + kvh) * D + d) * kBlock +
-                                    (k0 + t) % kBlock);
+        const float vs = kv_scales ? kv_scales[bt] : 1.0f;
+        a += ps[t] * (Elem<TC>::load(vc + (((int64_t)bt * Hkv + kvh) * D + d) * kBlock +
+                                     (k0 + t) % kBlock) *
+                      vs);
       }
       acc[i] = a;
     }
@@ -732,12 +736,14 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
 using namespace pa;
 
 
-extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
-                              const int32_t* block_tables, int32_t max_blocks_per_seq,
-                              const int32_t* cu_q_lens, const int32_t* past_lens,
-                              int32_t num_seqs, int32_t total_q, int32_t max_q_len,
-                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                              int32_t num_blocks, float scale, int32_t dtype, pa_stream_t stream) {
+namespace {
+int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* v_cache,
+                     const float* kv_scales, const int32_t* block_tables,
+                     int32_t max_blocks_per_seq, const int32_t* cu_q_lens,
+                     const int32_t* past_lens, int32_t num_seqs, int32_t total_q,
+                     int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, int32_t num_blocks, float scale, int32_t dtype,
+                     pa_stream_t stream) {
   clear_error();
   PA_REQUIRE(dtype_ok(dtype) || dtype == PA_DTYPE_FP8_E4M3, PA_ERR_INVALID_ARG,
              "pa_prefill: unknown dtype %d", dtype);
@@ -753,8 +759,8 @@ extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, con
              PA_ERR_INVALID_ARG, "pa_prefill: null pointer");
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  const bool tiled = dtype == PA_DTYPE_BF16 && (head_dim == 64 || head_dim == 128);
-  const bool mfma = dtype == PA_DTYPE_BF16 && head_dim == 256;
+  const bool tiled = !kv_scales && dtype == PA_DTYPE_BF16 && (head_dim == 64 || head_dim == 128);
+  const bool mfma = !kv_scales && dtype == PA_DTYPE_BF16 && head_dim == 256;
   if (tiled) {
     const int G = num_heads / num_kv_heads;
     const int HW = G < 4 ? G : 4;
@@ -798,17 +804,47 @@ extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, con
       prefill_generic_kernel<uint16_t, Fp8><<<grid, 64, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const Fp8*)k_cache, (const Fp8*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2);
+          head_dim, num_blocks, scale_log2, nullptr);
     else if (dtype == PA_DTYPE_BF16)
       prefill_generic_kernel<uint16_t><<<grid, 64, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2);
+          head_dim, num_blocks, scale_log2, nullptr);
     else
       prefill_generic_kernel<float><<<grid, 64, 0, s>>>(
           (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2);
+          head_dim, num_blocks, scale_log2, kv_scales);
   }
   return check_launch("pa_prefill");
+}
+}  // namespace
+
+extern "C" int32_t pa_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, int32_t max_blocks_per_seq,
+                              const int32_t* cu_q_lens, const int32_t* past_lens,
+                              int32_t num_seqs, int32_t total_q, int32_t max_q_len,
+                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int32_t num_blocks, float scale, int32_t dtype, pa_stream_t stream) {
+  return prefill_impl(out, q, k_cache, v_cache, nullptr, block_tables, max_blocks_per_seq,
+                      cu_q_lens, past_lens, num_seqs, total_q, max_q_len, num_heads, num_kv_heads,
+                      head_dim, num_blocks, scale, dtype, stream);
+}
+
+extern "C" int32_t pa_prefill_quantized(void* out, const void* q, const float* k_cache,
+                                        const float* v_cache, const float* block_scales,
+                                        const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                        const int32_t* cu_q_lens, const int32_t* past_lens,
+                                        int32_t num_seqs, int32_t total_q, int32_t max_q_len,
+                                        int32_t num_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, int32_t num_blocks, float scale,
+                                        pa_stream_t stream) {
+  if (!block_scales) {
+    clear_error();
+    set_error("pa_prefill_quantized: null block_scales");
+    return PA_ERR_INVALID_ARG;
+  }
+  return prefill_impl(out, q, k_cache, v_cache, block_scales, block_tables, max_blocks_per_seq,
+                      cu_q_lens, past_lens, num_seqs, total_q, max_q_len, num_heads, num_kv_heads,
+                      head_dim, num_blocks, scale, PA_DTYPE_F32, stream);
 }

@@ -23,8 +23,11 @@ def _i64_array(xs):
 
 
 class PagedKvCache:
+    """quantized=True mirrors PagedKvCache::new(..., quantized = true): an f32
+    cache of int8 values with one scale per block (re-quantised per write)."""
+
     def __init__(self, num_layers, num_heads, head_dim, num_blocks, dtype=torch.float32,
-                 device="cuda"):
+                 device="cuda", quantized=False):
         self._lib = _lib.load()
         self.device = torch.device(device)
         if self.device.index is None:
@@ -33,9 +36,16 @@ class PagedKvCache:
         self.num_heads = num_heads
         self.head_dim = head_dim
         h = C.c_void_p()
+        if quantized and dtype != torch.float32:
+            raise ValueError("quantised caches are f32")
+        self.quantized = quantized
         with torch.cuda.device(self.device):
-            _check("pa_kv_cache_create", self._lib.pa_kv_cache_create(
-                num_layers, num_heads, head_dim, num_blocks, _DTYPES[dtype], C.byref(h)))
+            if quantized:
+                _check("pa_kv_cache_create_quantized", self._lib.pa_kv_cache_create_quantized(
+                    num_layers, num_heads, head_dim, num_blocks, C.byref(h)))
+            else:
+                _check("pa_kv_cache_create", self._lib.pa_kv_cache_create(
+                    num_layers, num_heads, head_dim, num_blocks, _DTYPES[dtype], C.byref(h)))
         self._h = h
 
     def close(self):
@@ -68,6 +78,22 @@ class PagedKvCache:
         """Device tensor view of one layer's V cache [NB, H, D, 16]."""
         return self._layer_tensor(self._lib.pa_kv_cache_value_ptr(self._h, layer),
                                   (self.num_blocks(), self.num_heads, self.head_dim, BLOCK_SIZE))
+
+    def scales(self, layer):
+        """Device tensor view of one layer's block scales [NB] (quantised only)."""
+        if not self.quantized:
+            raise ValueError("cache is not quantised")
+        ptr = self._lib.pa_kv_cache_scales_ptr(self._h, layer)
+        if not ptr:
+            raise PaError("pa_kv_cache_scales_ptr", -2, "layer out of bounds")
+        n = self.num_blocks()
+        iface = {"shape": (n * 4,), "typestr": "|u1", "data": (ptr, False), "strides": None,
+                 "version": 3}
+
+        class _Buf:
+            __cuda_array_interface__ = iface
+
+        return torch.as_tensor(_Buf(), device=self.device).view(torch.float32)
 
     def _layer_tensor(self, ptr, shape):
         if not ptr:

@@ -165,8 +165,9 @@ def decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len):
 
 
 def decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len, scale=None,
-           out=None, workspace=None):
-    """Decode attention: q [B, Hq, D] -> out [B, Hq, D]."""
+           out=None, workspace=None, block_scales=None):
+    """Decode attention: q [B, Hq, D] -> out [B, Hq, D].  block_scales
+    (f32 [NB]) marks the f32 caches as quantised (pa_decode_quantized)."""
     _dev(q, k_cache, v_cache, block_tables, context_lens)
     nb, hkv, d = _cache_dims(k_cache, v_cache)
     b, hq, dq = q.shape
@@ -184,6 +185,13 @@ def decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len, sca
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     lib = _lib.load()
+    if block_scales is not None:
+        _quant_scales(block_scales, k_cache, nb)
+        _check("pa_decode_quantized", lib.pa_decode_quantized(
+            _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_scales),
+            _ptr(block_tables), block_tables.shape[1], _ptr(context_lens), max_context_len, b, hq,
+            hkv, d, nb, float(scale), _ptr(workspace), ws_bytes, _stream(q)))
+        return out
     _check("pa_decode", lib.pa_decode(
         _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
         block_tables.shape[1], _ptr(context_lens), max_context_len, b, hq, hkv, d, nb,
@@ -191,9 +199,18 @@ def decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len, sca
     return out
 
 
+def _quant_scales(block_scales, k_cache, nb):
+    _dev(block_scales)
+    if block_scales.dtype != torch.float32 or block_scales.shape != (nb,):
+        raise ValueError("block_scales must be f32 [num_blocks]")
+    if k_cache.dtype != torch.float32:
+        raise ValueError("quantised caches are f32")
+
+
 def prefill(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens, max_q_len, scale=None,
-            out=None):
-    """Chunked causal prefill: q [total_q, Hq, D] -> out [total_q, Hq, D]."""
+            out=None, block_scales=None):
+    """Chunked causal prefill: q [total_q, Hq, D] -> out [total_q, Hq, D].
+    block_scales (f32 [NB]) marks the f32 caches as quantised."""
     _dev(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens)
     nb, hkv, d = _cache_dims(k_cache, v_cache)
     tq, hq, dq = q.shape
@@ -205,6 +222,13 @@ def prefill(q, k_cache, v_cache, block_tables, cu_q_lens, past_lens, max_q_len, 
     if out is None:
         out = torch.empty_like(q)
     lib = _lib.load()
+    if block_scales is not None:
+        _quant_scales(block_scales, k_cache, nb)
+        _check("pa_prefill_quantized", lib.pa_prefill_quantized(
+            _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_scales),
+            _ptr(block_tables), block_tables.shape[1], _ptr(cu_q_lens), _ptr(past_lens),
+            block_tables.shape[0], tq, max_q_len, hq, hkv, d, nb, float(scale), _stream(q)))
+        return out
     _check("pa_prefill", lib.pa_prefill(
         _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
         block_tables.shape[1], _ptr(cu_q_lens), _ptr(past_lens), block_tables.shape[0], tq,
