@@ -295,6 +295,50 @@ def cpu_baseline(w, budget_s=12.0):
                       "gather + expand_kv + dense f32 softmax attention, OpenMP"}
 
 
+def run_e2e(pa, args):
+    """Qwen2.5-0.5B-shaped engine, 24 layers, random bf16
+    weights N(0, 0.02) (seed 4), 32 requests with prompts U[64, 512] of random
+    ids, 256 greedy tokens each.  value = generated tokens / wall time of the
+    whole generation (prefill + decode)."""
+    from vllm_lite_amd import e2e
+
+    cfg = e2e.qwen25_05b()
+    w = e2e.Weights(cfg, seed=4, device=DEV)
+    n_req, max_new = 32, 256
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(64, 513, (n_req,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab, (n,), generator=g).tolist() for n in lens]
+    blocks = sum((n + max_new + 15) // 16 for n in lens) + 64
+    eng = e2e.Engine(cfg, w, blocks, device=DEV)
+    eng.generate(prompts, min(8, max_new))  # warm-up: kernels, GEMM plans, workspace
+    gen, t = eng.generate(prompts, max_new)
+    total = t["prefill_s"] + t["decode_s"]
+    decode_step = t["decode_s"] / (max_new - 1)
+    # bytes a decode step must read: every weight once, plus the K/V of the
+    # batch's contexts at the mid-generation point (bf16, Hkv heads)
+    kv_mid = 2 * sum(n + max_new // 2 for n in lens) * cfg.kv_heads * cfg.head_dim * 2 * cfg.layers
+    step_bytes = w.nbytes() + kv_mid
+    achieved = step_bytes / decode_step / 1e9
+    line = {
+        "metric": "end-to-end greedy generation output tokens/s (Qwen2.5-0.5B shape)",
+        "value": round(n_req * max_new / total, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": max_new, "warmup": 1, "ms_per_step": round(total / max_new * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random bf16 weights N(0, 0.02), random prompt ids)",
+        "config": {"workload": "config 5: Qwen2.5-0.5B-shaped engine, 24 layers, 32 requests, "
+                               "prompts U[64, 512], 256 greedy tokens",
+                   "global_batch": n_req, "seq_len": max(lens) + max_new,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "one decode step (weights + KV)", "bytes_per_step": step_bytes,
+                     "decode_step_ms": round(decode_step * 1e3, 3),
+                     "prefill_ms": round(t["prefill_s"] * 1e3, 2)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def copy_calibration(args):
     """Plain 1 GiB device-to-device copy: the known-size reference for
     scaling rocprof FETCH_SIZE / WRITE_SIZE, and the achievable-HBM check."""
@@ -323,7 +367,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "decode-fp8", "prefill", "splitk", "qwen", "copy"])
+                    choices=["decode", "decode-fp8", "prefill", "splitk", "qwen", "e2e", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -335,6 +379,8 @@ def main():
     torch.cuda.set_device(0)
     if args.config == "copy":
         return copy_calibration(args)
+    if args.config == "e2e":
+        return run_e2e(pa, args)
     w = Workload(pa, args.config)
     for _ in range(args.warmup):
         w.step()

@@ -123,6 +123,13 @@ int32_t pa_batch_prepare(pa_batch* batch, int32_t num_seqs, const int32_t* num_t
                          const int32_t* block_counts, int32_t num_blocks, pa_stream_t stream);
 
 int32_t pa_batch_num_tokens(const pa_batch* batch);
+/* Fixes the maximum context the decode launches are shaped for (0 = the
+ * step's own maximum).  With a capacity, successive decode steps of the same
+ * batch size and table width launch identical kernels (sequence lengths are
+ * read on the device), so a captured step can be replayed after each
+ * pa_batch_prepare.  A step whose context exceeds the capacity is an error.
+ * The decode workspace is sized for the capacity on the next call. */
+int32_t pa_batch_set_capacity(pa_batch* batch, int32_t max_context_len);
 /* 1 when every sequence is a single-token decode step. */
 int32_t pa_batch_is_decode(const pa_batch* batch);
 

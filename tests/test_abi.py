@@ -10,7 +10,7 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("pa.h", "pa_kv_cache.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("pa.h", "pa_kv_cache.h", "pa_dense.h")]
 
 
 def declared_symbols():

@@ -19,7 +19,9 @@ from .ops import (
     reshape_and_cache,
     reshape_and_cache_fp8,
     rope_inv_freq,
+    rms_norm,
     rope_reshape_and_cache,
+    silu_mul,
     slot_mapping,
 )
 from .kv_cache import PagedKvCache, StepBatch
@@ -37,6 +39,8 @@ __all__ = [
     "reshape_and_cache",
     "reshape_and_cache_fp8",
     "rope_inv_freq",
+    "rms_norm",
     "rope_reshape_and_cache",
+    "silu_mul",
     "slot_mapping",
 ]

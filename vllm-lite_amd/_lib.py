@@ -23,6 +23,8 @@ SIGNATURES = {
                          _p, _sz, _i32, _p]),
     "pa_prefill": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                           _i32, _f32, _i32, _p]),
+    "pa_rms_norm": (_i32, [_p, _p, _p, _p, _i32, _i32, _f32, _i32, _p]),
+    "pa_silu_mul": (_i32, [_p, _p, _i32, _i32, _i32, _p]),
     "pa_decode_quantized": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32,
                                    _i32, _i32, _f32, _p, _sz, _p]),
     "pa_prefill_quantized": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32,
@@ -51,6 +53,7 @@ SIGNATURES = {
     "pa_batch_destroy": (None, [_p]),
     "pa_batch_prepare": (_i32, [_p, _i32, _p, _p, _p, _p, _i32, _p]),
     "pa_batch_num_tokens": (_i32, [_p]),
+    "pa_batch_set_capacity": (_i32, [_p, _i32]),
     "pa_batch_is_decode": (_i32, [_p]),
     "pa_batch_attention": (_i32, [_p, _p, _i32, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _f32,
                                   _p, _p]),

@@ -12,7 +12,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libpa.so")
-SOURCES = ["cache_ops.hip", "decode.hip", "prefill.hip", "rope.hip", "quant.hip", "kv_cache.cpp", "batch.cpp"]
+SOURCES = ["cache_ops.hip", "decode.hip", "prefill.hip", "rope.hip", "quant.hip", "dense.hip", "kv_cache.cpp", "batch.cpp"]
 ARCH = os.environ.get("PA_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

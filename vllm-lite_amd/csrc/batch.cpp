@@ -47,6 +47,7 @@ struct DevBuf {
 
 struct pa_batch {
   int num_seqs = 0, num_tokens = 0, max_blocks = 0, max_q = 0, max_ctx = 0, num_blocks = 0;
+  int capacity = 0;  // fixed max context for decode launches (0 = per step)
   bool decode = false;
   // device arrays
   DevBuf positions, slots, tables, cu_q, past, ctx_lens, workspace;
@@ -68,6 +69,13 @@ extern "C" int32_t pa_batch_create(pa_batch** out) {
 extern "C" void pa_batch_destroy(pa_batch* b) { delete b; }
 
 extern "C" int32_t pa_batch_num_tokens(const pa_batch* b) { return b ? b->num_tokens : 0; }
+
+extern "C" int32_t pa_batch_set_capacity(pa_batch* b, int32_t max_context_len) {
+  pa::clear_error();
+  PA_REQUIRE(b && max_context_len >= 0, PA_ERR_INVALID_ARG, "pa_batch_set_capacity: bad arguments");
+  b->capacity = max_context_len;
+  return PA_OK;
+}
 extern "C" int32_t pa_batch_is_decode(const pa_batch* b) { return b && b->decode ? 1 : 0; }
 
 extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t* num_tokens,
@@ -210,10 +218,16 @@ extern "C" int32_t pa_batch_attention(pa_batch* b, pa_kv_cache* cache, int32_t l
   PA_REQUIRE(q_stride == 0 || q_stride == (int64_t)num_heads * d, PA_ERR_UNSUPPORTED,
              "pa_batch_attention: attention needs contiguous q rows");
   if (b->decode) {
-    const size_t need = pa_decode_workspace_size(b->num_seqs, num_heads, d, b->max_ctx);
+    // With a capacity the launch shape depends on it alone (sequences read
+    // their own lengths on the device), so the call can be replayed.
+    PA_REQUIRE(b->capacity == 0 || b->max_ctx <= b->capacity, PA_ERR_INVALID_ARG,
+               "pa_batch_attention: context %d exceeds the capacity %d", b->max_ctx,
+               b->capacity);
+    const int max_ctx = b->capacity > 0 ? b->capacity : b->max_ctx;
+    const size_t need = pa_decode_workspace_size(b->num_seqs, num_heads, d, max_ctx);
     if ((rc = b->workspace.ensure(std::max<size_t>(need, 256)))) return rc;
     return pa_decode(out, q, kc, vc, (const int32_t*)b->tables.ptr, b->max_blocks,
-                     (const int32_t*)b->ctx_lens.ptr, b->max_ctx, b->num_seqs, num_heads, hkv, d,
+                     (const int32_t*)b->ctx_lens.ptr, max_ctx, b->num_seqs, num_heads, hkv, d,
                      b->num_blocks, scale, b->workspace.ptr, b->workspace.bytes, dtype, stream);
   }
   return pa_prefill(out, q, kc, vc, (const int32_t*)b->tables.ptr, b->max_blocks,

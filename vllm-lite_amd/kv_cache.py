@@ -217,6 +217,12 @@ class StepBatch:
     def num_tokens(self):
         return self._lib.pa_batch_num_tokens(self._h)
 
+    def set_capacity(self, max_context_len):
+        """pa_batch_set_capacity: shape decode launches for a fixed maximum
+        context so a captured step can be replayed (0 = per step)."""
+        _check("pa_batch_set_capacity", self._lib.pa_batch_set_capacity(self._h,
+                                                                          int(max_context_len)))
+
     def is_decode(self):
         return bool(self._lib.pa_batch_is_decode(self._h))
 

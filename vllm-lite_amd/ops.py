@@ -283,3 +283,36 @@ def rope_reshape_and_cache(q, key, value, k_cache, v_cache, slot_mapping, positi
         _ptr(q), q.stride(0), _ptr(key), key.stride(0), _ptr(value), value.stride(0),
         _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), _ptr(positions), _ptr(inv_freq), t, hq,
         h, d, nb, _dtype_code(k_cache), _stream(q)))
+
+
+def rms_norm(residual, weight, eps, add=None, out=None):
+    """pa_rms_norm: residual += add (in place, when given), then
+    out = residual / sqrt(mean(residual^2) + eps) * weight; [rows, hidden]."""
+    _dev(residual, weight)
+    rows, hidden = residual.shape
+    if weight.shape != (hidden,) or weight.dtype != residual.dtype:
+        raise ValueError("weight must be [hidden] in the residual dtype")
+    if add is not None:
+        _dev(add)
+        if add.shape != residual.shape or add.dtype != residual.dtype:
+            raise ValueError("add must match residual")
+    if out is None:
+        out = torch.empty_like(residual)
+    lib = _lib.load()
+    _check("pa_rms_norm", lib.pa_rms_norm(
+        _ptr(out), _ptr(residual), _ptr(add), _ptr(weight), rows, hidden, float(eps),
+        _dtype_code(residual), _stream(residual)))
+    return out
+
+
+def silu_mul(gate_up, out=None):
+    """pa_silu_mul: gate_up [rows, 2 * inter] -> silu(gate) * up [rows, inter]."""
+    _dev(gate_up)
+    rows, two = gate_up.shape
+    inter = two // 2
+    if out is None:
+        out = torch.empty(rows, inter, dtype=gate_up.dtype, device=gate_up.device)
+    lib = _lib.load()
+    _check("pa_silu_mul", lib.pa_silu_mul(_ptr(out), _ptr(gate_up), rows, inter,
+                                          _dtype_code(gate_up), _stream(gate_up)))
+    return out
