@@ -21,6 +21,8 @@
 //    processed per step (32 = the MFMA K dimension of the P·V product).
 //  * decode_generic_kernel (f32 or bf16, any D <= 512, any group size): a
 //    plain reference-grade kernel, one workgroup per query head.
+#include <type_traits>
+
 #include "pa_common.hpp"
 
 namespace pa {
@@ -35,6 +37,41 @@ constexpr float kNegBig = -1.0e30f;  // "no max yet": finite so 2^(x - m) never 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ inline float shfl_xor_f(float x, int mask) { return __shfl_xor(x, mask, 64); }
+
+// K/V of a block that only this sequence reads are streamed once per decode
+// step: non-temporal loads (the `nt` cache policy) keep them from
+// displacing reusable lines and stream faster (measured ~6.8 TB/s vs
+// ~6.1 TB/s for plain 16-byte loads on MI355X).  A block that a neighbouring
+// sequence's table holds at the same index (a shared prefix) is read with
+// the default policy, so the other sequences find it in the cache.
+// The loads are raw buffer loads over one (block, head) slice, whose cache
+// policy is an instruction operand (a select between a plain and a
+// non-temporal pointer load would be merged into a plain load).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kPolicyNT = 2;  // cache-policy operand: non-temporal
+__device__ inline __amdgpu_buffer_rsrc_t slice_rsrc(const void* base, int bytes) {
+  // raw buffer (stride 0) of `bytes` bytes; 32-bit data format, so reads past
+  // the slice return zeros
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+template <int POLICY>
+__device__ inline u32x4 bload16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POLICY);
+}
+template <int POLICY>
+__device__ inline uint64_t bload8(__amdgpu_buffer_rsrc_t r, int off) {
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POLICY);
+  return (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+}
+// Whether table entry `bi` of sequence `seq` is private to it: the tables
+// of the sequences before and after hold a different block at that index.
+__device__ inline bool private_block(const int32_t* __restrict__ block_tables, int mbs, int seq,
+                                     int num_seqs, int bi, int32_t id) {
+  const bool prev = seq > 0 && block_tables[(int64_t)(seq - 1) * mbs + bi] == id;
+  const bool next = seq + 1 < num_seqs && block_tables[(int64_t)(seq + 1) * mbs + bi] == id;
+  return !prev && !next;
+}
 
 // ---------------------------------------------------------------------------
 // MFMA decode kernel.
@@ -107,22 +144,30 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
     if (b0 < 0 || b0 >= num_blocks) { b0 = 0; lim0 = 0; }
     if (b1 < 0 || b1 >= num_blocks) { b1 = 0; lim1 = 0; }
 
-    const uint16_t* k0 = kc + ((int64_t)b0 * Hkv + kvh) * head_stride + c * D + 8 * j;
-    const uint16_t* k1 = kc + ((int64_t)b1 * Hkv + kvh) * head_stride + c * D + 8 * j;
+    const int bi0 = tok0 / kBlock + ib;
+    const bool nt0 = private_block(block_tables, mbs, seq, gridDim.z, bi0, b0);
+    const bool nt1 = private_block(block_tables, mbs, seq, gridDim.z, bi0 + 1, b1);
+    constexpr int SLICE = kBlock * D * 2;  // bytes of one (block, head) of K or V
+    const auto rk0 = slice_rsrc(kc + ((int64_t)b0 * Hkv + kvh) * head_stride, SLICE);
+    const auto rk1 = slice_rsrc(kc + ((int64_t)b1 * Hkv + kvh) * head_stride, SLICE);
+    const auto rv0 = slice_rsrc(vc + ((int64_t)b0 * Hkv + kvh) * head_stride, SLICE);
+    const auto rv1 = slice_rsrc(vc + ((int64_t)b1 * Hkv + kvh) * head_stride, SLICE);
+    const int koff = (c * D + 8 * j) * 2, voff = (c * kBlock + 4 * j) * 2;
     bf16x8 ka[KS], kb[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      ka[s] = *reinterpret_cast<const bf16x8*>(k0 + 32 * s);
-      kb[s] = *reinterpret_cast<const bf16x8*>(k1 + 32 * s);
-    }
-    const uint16_t* v0 = vc + ((int64_t)b0 * Hkv + kvh) * head_stride + c * kBlock + 4 * j;
-    const uint16_t* v1 = vc + ((int64_t)b1 * Hkv + kvh) * head_stride + c * kBlock + 4 * j;
     uint64_t va[DT], vb[DT];
+    auto load_block = [&](auto policy, const __amdgpu_buffer_rsrc_t& rk,
+                          const __amdgpu_buffer_rsrc_t& rv, bf16x8 (&kx)[KS],
+                          uint64_t (&vx)[DT]) {
+      constexpr int P = decltype(policy)::value;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      va[dt] = *reinterpret_cast<const uint64_t*>(v0 + dt * 16 * kBlock);
-      vb[dt] = *reinterpret_cast<const uint64_t*>(v1 + dt * 16 * kBlock);
-    }
+      for (int s = 0; s < KS; ++s) kx[s] = __builtin_bit_cast(bf16x8, bload16<P>(rk, koff + 64 * s));
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) vx[dt] = bload8<P>(rv, voff + dt * 16 * kBlock * 2);
+    };
+    using Plain = std::integral_constant<int, 0>;
+    using Stream = std::integral_constant<int, kPolicyNT>;
+    if (nt0) load_block(Stream{}, rk0, rv0, ka, va); else load_block(Plain{}, rk0, rv0, ka, va);
+    if (nt1) load_block(Stream{}, rk1, rv1, kb, vb); else load_block(Plain{}, rk1, rv1, kb, vb);
 
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
