@@ -15,6 +15,8 @@
 //    row ranges of the same head so their K/V reads share the L1/L2.
 //  * prefill_generic_kernel (f32 or bf16, any D <= 512): one wavefront per
 //    (query row, head), reference-grade.
+#include <algorithm>
+
 #include "pa_common.hpp"
 
 namespace pa {
@@ -255,40 +257,48 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   const int HW = G < 4 ? G : 4;        // heads per workgroup
   const int TT = 64 * (4 / HW);        // query tokens per workgroup
 
-  // XCD-aware logical id.
+  // Work items (logical ids): kv head (group) major, then sequences from the
+  // most to the least attention work (work = q_len * (past + q_len / 2),
+  // ties by index; past 64 sequences the index order), then query tiles
+  // longest first.  The items are cut into 8 contiguous chunks, one per XCD
+  // (workgroups are dealt round-robin to the XCDs, so workgroup g runs on XCD
+  // g % 8), and the items of one chunk stream the same kv head's K/V through
+  // that XCD's L2.  The grid is persistent (about one workgroup per CU): the
+  // XCD's workgroups take its chunk in rounds of nslot items, the workgroup
+  // in slot s taking item s of even rounds and item nslot - 1 - s of odd
+  // rounds (within a sequence the tiles go longest first, so this pairs long
+  // and short tiles); the workgroups stay on neighbouring items (the same
+  // sequence's K/V) and none waits for a CU behind a long-running one.
   const int total = B * Hkv * head_groups * tiles_per_seq;
   const int per_xcd = (total + 7) / 8;
-  const int logical = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-  if (logical >= total) return;
-  // Logical order: kv head (group) major, then sequences from the most to
-  // the least attention work (so the tail is made of small sequences),
-  // then query tiles longest first.  Concurrent workgroups of one XCD then
-  // mostly stream the same sequence's K/V.  Every workgroup ranks the
-  // sequences the same way (work = q_len * (past + q_len / 2), ties by
-  // index); past 64 sequences the order is the index order.
-  const int kvhg = logical / (B * tiles_per_seq);
-  const int rem = logical % (B * tiles_per_seq);
-  const int tile = tiles_per_seq - 1 - rem % tiles_per_seq;
-  const int rank = rem / tiles_per_seq;
-  int seq = rank;
-  if (B <= 64) {
+  const int xcd = (int)(blockIdx.x % 8), nslot = (int)(gridDim.x / 8), slot = (int)(blockIdx.x / 8);
+  const int lo = min(total, xcd * per_xcd), hi = min(total, lo + per_xcd);
+  __shared__ int seq_of_rank[64];
+  if (B <= 64 && (int)threadIdx.x < B) {
     auto work = [&](int b) -> long long {
       const long long ql = cu_q[b + 1] - cu_q[b];
       return ql * (2 * (long long)past_lens[b] + ql);
     };
-    for (int b = 0; b < B; ++b) {
-      const long long wb = work(b);
-      int r = 0;
-      for (int o2 = 0; o2 < B; ++o2) {
-        const long long wo = work(o2);
-        r += (wo > wb) || (wo == wb && o2 < b);
-      }
-      if (r == rank) {
-        seq = b;
-        break;
-      }
+    const int b = threadIdx.x;
+    const long long wb = work(b);
+    int r = 0;
+    for (int o2 = 0; o2 < B; ++o2) {
+      const long long wo = work(o2);
+      r += (wo > wb) || (wo == wb && o2 < b);
     }
+    seq_of_rank[r] = b;
   }
+  __syncthreads();
+  auto seq_of = [&](int rank) -> int { return B <= 64 ? seq_of_rank[rank] : rank; };
+
+  // One work item: attention for one (kv head group, sequence, query tile).
+  auto process = [&](int logical) {
+  // every wavefront is done with the previous item's LDS tiles
+  __syncthreads();
+  const int kvhg = logical / (B * tiles_per_seq);
+  const int rem = logical % (B * tiles_per_seq);
+  const int tile = tiles_per_seq - 1 - rem % tiles_per_seq;
+  const int seq = seq_of(rem / tiles_per_seq);
   const int kvh = kvhg / head_groups, hg = kvhg % head_groups;
 
   const int q_begin = cu_q[seq];
@@ -657,6 +667,11 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       *reinterpret_cast<uint64_t*>(orow + 16 * dt) = *reinterpret_cast<const uint64_t*>(w);
     }
   }
+  };
+  for (int r = 0; lo + r * nslot < hi; ++r) {
+    const int item = lo + r * nslot + ((r & 1) ? nslot - 1 - slot : slot);
+    if (item < hi) process(item);
+  }
 }
 
 // Generic: one wavefront per (query row, head); keys in chunks of 64 with
@@ -736,7 +751,23 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
 using namespace pa;
 
 
+
 namespace {
+// Compute units of the current device (cached per device).
+int compute_units() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* v_cache,
                      const float* kv_scales, const int32_t* block_tables,
                      int32_t max_blocks_per_seq, const int32_t* cu_q_lens,
@@ -770,7 +801,8 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
     const long long total = (long long)num_seqs * num_kv_heads * head_groups * tiles_per_seq;
     PA_REQUIRE(total < (1ll << 31) / 8, PA_ERR_UNSUPPORTED, "pa_prefill: launch too large");
     const int per_xcd = (int)((total + 7) / 8);
-    const dim3 grid(8 * per_xcd);
+    // persistent grid: about one workgroup per CU (a multiple of the 8 XCDs)
+    const dim3 grid(8 * std::max(1, std::min(per_xcd, compute_units() / 8)));
     auto* o = (uint16_t*)out;
     auto* qq = (const uint16_t*)q;
     auto* kc = (const uint16_t*)k_cache;
