@@ -242,6 +242,23 @@ def time_attend(w, iters):
     return start.elapsed_time(stop) / iters / 1e3  # seconds
 
 
+def time_attend_flushed(w, iters, flush_bytes=512 << 20):
+    """Median duration of the dominant launch with the caches flushed before
+    each one: a 512 MiB scratch write (larger than L2 + MALL) runs between
+    launches, and HIP events bracket each launch on its own."""
+    scratch = torch.empty(flush_bytes // 4, dtype=torch.float32, device=DEV)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(iters)]
+    torch.cuda.synchronize()
+    for a, b in ev:
+        scratch.fill_(1.0)
+        a.record()
+        w.attend()
+        b.record()
+    torch.cuda.synchronize()
+    return float(np.median([a.elapsed_time(b) for a, b in ev])) / 1e3
+
+
 def cpu_baseline(w, budget_s=12.0):
     """Times the C oracle (restated reference CPU path: gather blocks to dense
     f32, expand KV to all query heads, full softmax, OpenMP over heads) on a
@@ -369,6 +386,8 @@ def main():
     ap.add_argument("--config", default="decode",
                     choices=["decode", "decode-fp8", "prefill", "splitk", "qwen", "e2e", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-flush", action="store_true",
+                    help="skip the cache-flushed timing leg (keeps a kernel trace to warm launches)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
@@ -393,6 +412,7 @@ def main():
     ms_per_step = el / args.steps * 1e3
 
     t_attn = time_attend(w, max(args.steps, 20))
+    t_flush = None if args.no_flush else time_attend_flushed(w, max(args.steps, 20))
     if w.kind == "decode":
         value = w.B * args.steps / el
         unit = "tokens/s"
@@ -403,6 +423,9 @@ def main():
                 "kernel": "pa_decode (decode_mfma_kernel + decode_reduce_kernel)",
                 "alg_bytes_per_launch": w.alg_bytes,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
+        if t_flush:
+            roof["flushed_launch_us"] = round(t_flush * 1e6, 2)
+            roof["flushed_frac"] = round(w.alg_bytes / t_flush / 1e9 / HBM_PEAK_GBS, 4)
         if args.config == "splitk":
             roof["unique_block_gbs"] = round((w.unique_kv_bytes) / t_attn / 1e9, 1)
         if w.dtype == torch.float32:
@@ -417,6 +440,9 @@ def main():
                 "traffic": measured_traffic(args.config),
                 "kernel": "pa_prefill (prefill_tiled_kernel)", "flops_per_launch": w.flops,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
+        if t_flush:
+            roof["flushed_launch_us"] = round(t_flush * 1e6, 2)
+            roof["flushed_frac"] = round(w.flops / t_flush / 1e12 / BF16_PEAK_TFLOPS, 4)
     cpu = None if args.no_cpu else cpu_baseline(w)
     line = {
         "metric": METRIC if w.kind == "decode" else "paged-attn chunked prefill TFLOP/s",

@@ -1,5 +1,5 @@
 """GPU parity of the dense side and the end-to-end engine (config 5 path):
-pa_rms_norm / pa_silu_mul against torch fp32, and the engine's logits
+pa_rms_norm / pa_layer_norm / pa_silu_mul against torch fp32, and the engine's logits
 against a plain fp32 torch forward of the same (small) model, teacher-forced
 through a prefill and several decode steps."""
 import math
@@ -35,6 +35,32 @@ def test_rms_norm(pa, dtype, hidden):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hidden", [896, 128, 100])
+def test_layer_norm(pa, dtype, hidden):
+    g = torch.Generator(device=DEV).manual_seed(hidden + 1)
+    x = (torch.randn(37, hidden, generator=g, device=DEV) * 2 + 0.5).to(dtype)
+    a = torch.randn(37, hidden, generator=g, device=DEV).to(dtype)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g, device=DEV)).to(dtype)
+    b = (0.1 * torch.randn(hidden, generator=g, device=DEV)).to(dtype)
+    res = x.clone()
+    out = pa.layer_norm(res, w, 1e-6, bias=b, add=a)
+    s = (x.float() + a.float()).to(dtype)
+    assert torch.equal(res, s)
+    # float64 reference: torch's own f32 layer_norm combines partial means
+    # inexactly, which 1 / sqrt(eps) magnifies on a near-constant row
+    ref = F.layer_norm(s.double(), (hidden,), w.double(), b.double(), 1e-6).float()
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    torch.testing.assert_close(out.float(), ref, atol=tol, rtol=tol)
+    # zero bias (NULL), no add; a constant row normalises to the bias
+    xc = x.clone()
+    xc[3] = 7.0
+    out2 = pa.layer_norm(xc.clone(), w, 1e-6)
+    ref2 = F.layer_norm(xc.double(), (hidden,), w.double(), None, 1e-6).float()
+    torch.testing.assert_close(out2.float(), ref2, atol=tol, rtol=tol)
+    assert torch.all(out2[3] == 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_silu_mul(pa, dtype):
     g = torch.Generator(device=DEV).manual_seed(1)
     gu = (torch.randn(19, 2 * 4864, generator=g, device=DEV) * 3).to(dtype)
@@ -61,6 +87,8 @@ def ref_logits(cfg, w, tokens, inv_freq):
                           z2 * cos[:, None] + z1 * sin[:, None]], -1)
 
     def norm(z, wt):
+        if cfg.norm == "layer":
+            return F.layer_norm(z, (z.shape[-1],), f(wt), None, cfg.eps)
         return z / torch.sqrt(z.pow(2).mean(-1, keepdim=True) + cfg.eps) * f(wt)
 
     hq, hkv, d = cfg.heads, cfg.kv_heads, cfg.head_dim
@@ -82,10 +110,11 @@ def ref_logits(cfg, w, tokens, inv_freq):
     return norm(x, w.norm) @ f(w.embed).T
 
 
-def test_engine_matches_fp32_forward(pa):
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+def test_engine_matches_fp32_forward(pa, norm):
     from vllm_lite_amd import e2e
     cfg = e2e.ModelConfig(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=32, inter=512,
-                          vocab=1000, rope_theta=1e4)
+                          vocab=1000, rope_theta=1e4, norm=norm)
     w = e2e.Weights(cfg, seed=7, device=DEV)
     eng = e2e.Engine(cfg, w, num_blocks=64, device=DEV)
     rng = np.random.default_rng(0)

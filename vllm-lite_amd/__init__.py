@@ -19,6 +19,7 @@ from .ops import (
     reshape_and_cache,
     reshape_and_cache_fp8,
     rope_inv_freq,
+    layer_norm,
     rms_norm,
     rope_reshape_and_cache,
     silu_mul,
@@ -39,6 +40,7 @@ __all__ = [
     "reshape_and_cache",
     "reshape_and_cache_fp8",
     "rope_inv_freq",
+    "layer_norm",
     "rms_norm",
     "rope_reshape_and_cache",
     "silu_mul",

@@ -6,18 +6,20 @@ weights, run the way the reference's CausalLm runs it
 (crates/model/src/causal_lm/model/mod.rs:143-164, decoder block
 crates/model/src/components/decoder_block/mod.rs:157-198), but batched: one
 StepBatch per engine step, and per layer
-    residual add + RMSNorm      pa_rms_norm
+    residual add + norm         pa_rms_norm | pa_layer_norm
     QKV projection (+ bias)     hipBLASLt GEMM (torch.nn.functional.linear)
     RoPE + KV write + attention StepBatch.attention (pa_batch_attention)
     O projection                hipBLASLt GEMM
-    residual add + RMSNorm      pa_rms_norm
+    residual add + norm         pa_rms_norm | pa_layer_norm
     gate|up projection          hipBLASLt GEMM
     SwiGLU                      pa_silu_mul
     down projection             hipBLASLt GEMM
-The norms use RMSNorm (as the benchmark configuration states; the
-reference's CausalLm constructs a zero-bias LayerNorm for these models,
-crates/model/src/qwen3/model.rs:19).  Norm weights start at 1, every other
-weight is N(0, 0.02).
+The norm is chosen explicitly by ModelConfig.norm: "rms" (RMSNorm, what the
+benchmark configuration states) or "layer" (the zero-bias LayerNorm the
+reference's CausalLm constructs for these models,
+crates/model/src/qwen3/model.rs:19,
+crates/model/src/components/decoder_block/factory.rs:42-46).  Norm weights
+start at 1, every other weight is N(0, 0.02).
 """
 import dataclasses
 import math
@@ -41,6 +43,7 @@ class ModelConfig:
     vocab: int = 151936
     rope_theta: float = 1e6
     eps: float = 1e-6
+    norm: str = "rms"  # "rms" | "layer" (zero-bias LayerNorm)
 
 
 def qwen25_05b():
@@ -91,6 +94,9 @@ class Engine:
             self.device)
         self.free = list(range(num_blocks))
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
+        if cfg.norm not in ("rms", "layer"):
+            raise ValueError(f"unknown norm {cfg.norm!r}")
+        self._norm = ops.rms_norm if cfg.norm == "rms" else ops.layer_norm
 
     def forward(self, tokens, logit_rows):
         """One step over the prepared batch: tokens [T] (int64, device) ->
@@ -102,17 +108,17 @@ class Engine:
         h = torch.empty_like(x)
         add = None
         for layer in range(c.layers):
-            ops.rms_norm(x, w.ln1[layer], c.eps, add=add, out=h)
+            self._norm(x, w.ln1[layer], c.eps, add=add, out=h)
             qkv = F.linear(h, w.wqkv[layer], w.bqkv[layer])
             q = qkv[:, :hq * d].contiguous().view(t, hq, d)  # the kernels take dense q rows
             k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
             v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
             attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq, self.scale)
             o = F.linear(attn.view(t, hq * d), w.wo[layer])
-            ops.rms_norm(x, w.ln2[layer], c.eps, add=o, out=h)
+            self._norm(x, w.ln2[layer], c.eps, add=o, out=h)
             act = ops.silu_mul(F.linear(h, w.wgu[layer]))
             add = F.linear(act, w.wd[layer])
-        ops.rms_norm(x, w.norm, c.eps, add=add, out=h)
+        self._norm(x, w.norm, c.eps, add=add, out=h)
         return F.linear(h[logit_rows], w.embed).float()
 
     def generate(self, prompts, max_new):

@@ -285,23 +285,43 @@ def rope_reshape_and_cache(q, key, value, k_cache, v_cache, slot_mapping, positi
         h, d, nb, _dtype_code(k_cache), _stream(q)))
 
 
-def rms_norm(residual, weight, eps, add=None, out=None):
-    """pa_rms_norm: residual += add (in place, when given), then
-    out = residual / sqrt(mean(residual^2) + eps) * weight; [rows, hidden]."""
+def _norm_args(residual, weight, add, out, bias=None):
     _dev(residual, weight)
     rows, hidden = residual.shape
-    if weight.shape != (hidden,) or weight.dtype != residual.dtype:
-        raise ValueError("weight must be [hidden] in the residual dtype")
+    for name, t in (("weight", weight), ("bias", bias)):
+        if t is not None and (t.shape != (hidden,) or t.dtype != residual.dtype):
+            raise ValueError(f"{name} must be [hidden] in the residual dtype")
+    if bias is not None:
+        _dev(bias)
     if add is not None:
         _dev(add)
         if add.shape != residual.shape or add.dtype != residual.dtype:
             raise ValueError("add must match residual")
     if out is None:
         out = torch.empty_like(residual)
+    return rows, hidden, out
+
+
+def rms_norm(residual, weight, eps, add=None, out=None):
+    """pa_rms_norm: residual += add (in place, when given), then
+    out = residual / sqrt(mean(residual^2) + eps) * weight; [rows, hidden]."""
+    rows, hidden, out = _norm_args(residual, weight, add, out)
     lib = _lib.load()
     _check("pa_rms_norm", lib.pa_rms_norm(
         _ptr(out), _ptr(residual), _ptr(add), _ptr(weight), rows, hidden, float(eps),
         _dtype_code(residual), _stream(residual)))
+    return out
+
+
+def layer_norm(residual, weight, eps, bias=None, add=None, out=None):
+    """pa_layer_norm (LnLayerNorm, crates/model/src/components/norm/layer_norm.rs:26-39):
+    residual += add (in place, when given), then
+    out = (residual - mean) / sqrt(var + eps) * weight + bias; [rows, hidden]."""
+    rows, hidden, out = _norm_args(residual, weight, add, out, bias)
+    lib = _lib.load()
+    _check("pa_layer_norm", lib.pa_layer_norm(
+        _ptr(out), _ptr(residual), _ptr(add), _ptr(weight), _ptr(bias), rows, hidden,
+        float(eps), _dtype_code(residual), _stream(residual)))
     return out
 
 
