@@ -16,6 +16,7 @@
 //  * prefill_generic_kernel (f32 or bf16, any D <= 512): one wavefront per
 //    (query row, head), reference-grade.
 #include <algorithm>
+#include <type_traits>
 
 #include "pa_common.hpp"
 
@@ -29,6 +30,8 @@ __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float shfl_xor_f(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
 constexpr int kWaves = 4;
+template <int V>
+using IC = std::integral_constant<int, V>;
 
 // Lane layout as in decode_mfma_kernel (lane = 16 j + c):
 //   QK:  A = K block (row = key c), B = Qᵀ (col = query row c of tile nt)
@@ -248,7 +251,12 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   constexpr int NBUF = 3;      // LDS tile buffers
   constexpr int TILE_BYTES = KT * D * 2;  // one K (or V) tile
   constexpr int DMA_PER_WAVE = TILE_BYTES / 1024 / W;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NBUF][2][TILE_BYTES];
+  constexpr int RPI = 64 / CPR;        // K rows per 1 KB chunk
+  constexpr int CPB = D * 32 / 1024;   // 1 KB chunks per V block
+  // 1 KB chunk i of a K tile and of a V tile lie in the same cache block
+  // (i / CPB), and a wavefront's chunks stay within one block
+  static_assert(RPI * CPB == kBlock && CPB % DMA_PER_WAVE == 0, "one block per wavefront copy");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2][NBUF][TILE_BYTES];
 
   const int lane = threadIdx.x & 63;
   const int wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -344,37 +352,36 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     for (int dt = 0; dt < DT; ++dt) o[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Block ids.  Each wavefront's HBM -> LDS copies of a tile all read one
+  // cache block (block `wblk` of the tile's 4), so per tile a wavefront
+  // loads just that id, one tile ahead of its use.  The index is clamped to
+  // the sequence's last block (keys past key_end are masked and their V
+  // zeroed) and an id outside the pool reads block 0.  Whether any id of the
+  // item's table lies outside the pool is found once per item (`bad_ids`);
+  // only then are a tile's per-block validity bits needed (slow path).
   const int32_t* btab = block_tables + (int64_t)seq * mbs;
   const int64_t head_stride = (int64_t)kBlock * D;
-
-  // The 4 block ids of a key tile, fetched one tile ahead of their use
-  // (scalar loads, wave-uniform), with bit b of `valid` set when block b
-  // exists in the table and lies inside the pool.  Invalid ids read block 0
-  // and are masked.
-  struct TileIds {
-    int32_t id0, id1, id2, id3;
-    int valid;
+  const int wblk = (wave_s * DMA_PER_WAVE) / CPB;
+  int bad = 0;
+  for (int b = threadIdx.x; b < nblk; b += blockDim.x) {
+    const int32_t id = btab[b];
+    bad |= (id < 0 || id >= num_blocks) ? 1 : 0;
+  }
+  const bool bad_ids = __syncthreads_or(bad) != 0;
+  auto fetch_id = [&](int kt) -> int32_t {
+    const int32_t id = btab[min(kt * (KT / kBlock) + wblk, max(nblk - 1, 0))];
+    return (id >= 0 && id < num_blocks) ? id : 0;
   };
-  auto fetch_ids = [&](int kt) -> TileIds {
-    TileIds t;
-    t.valid = 0;
-    int32_t raw[4];
+  auto tile_valid = [&](int kt) -> int {
+    if (!bad_ids) return (1 << (KT / kBlock)) - 1;
+    int v = 0;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
+    for (int b = 0; b < KT / kBlock; ++b) {
       const int bi = kt * (KT / kBlock) + b;
-      raw[b] = bi < nblk ? btab[bi] : -1;
-      const bool ok = raw[b] >= 0 && raw[b] < num_blocks;
-      t.valid |= ok ? (1 << b) : 0;
-      raw[b] = ok ? raw[b] : 0;
+      const int32_t id = bi < nblk ? btab[bi] : -1;
+      v |= (id >= 0 && id < num_blocks) ? (1 << b) : 0;
     }
-    t.id0 = raw[0];
-    t.id1 = raw[1];
-    t.id2 = raw[2];
-    t.id3 = raw[3];
-    return t;
-  };
-  auto pick = [](const TileIds& t, int b) -> int32_t {
-    return b == 0 ? t.id0 : b == 1 ? t.id1 : b == 2 ? t.id2 : t.id3;
+    return v;
   };
   // K row swizzle: 16-byte chunk ch of tile row r sits at chunk position
   // ch ^ kswz(r).  The rows one QK operand read touches (see qk) differ in
@@ -387,35 +394,31 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // over all banks whether the LDS serves 8 or 16 lanes of 16 bytes a cycle.
   auto vswz = [](int d) -> int { return ((d >> 2) ^ (d >> 3)) & 1; };
   // Per-lane element offsets of this wavefront's HBM -> LDS copies (the
-  // same for every tile) and the block each copy reads.
-  constexpr int RPI = 64 / CPR;        // K rows per 1 KB chunk
-  constexpr int CPB = D * 32 / 1024;   // 1 KB chunks per V block
-  int koff[DMA_PER_WAVE], voff[DMA_PER_WAVE], kblk[DMA_PER_WAVE], vblk[DMA_PER_WAVE];
+  // same for every tile).
+  int koff[DMA_PER_WAVE], voff[DMA_PER_WAVE];
 #pragma unroll
   for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
     const int i = wave_s * DMA_PER_WAVE + i0;  // 1 KB chunk of the tile
     const int r = i * RPI + lane / CPR;
     koff[i0] = (r % kBlock) * D + ((lane % CPR) ^ kswz(r)) * 8;
-    kblk[i0] = (i * RPI) / kBlock;
     const int d = (i % CPB) * 32 + lane / 2;
     voff[i0] = d * kBlock + ((lane & 1) ^ vswz(d)) * 8;
-    vblk[i0] = i / CPB;
   }
-  // Issues this wavefront's share of the HBM -> LDS copies of key tile kt.
-  auto issue_tile = [&](const TileIds& t, int buf) {
+  // Issues this wavefront's share of the HBM -> LDS copies of a key tile
+  // into LDS buffer `buf`; `id` is the cache block those copies read.
+  auto issue_tile = [&](int32_t id, int buf) {
+    const int64_t boff = ((int64_t)id * Hkv + kvh) * head_stride;
+    const uint16_t* kbase = kc + boff;
+    const uint16_t* vbase = vc + boff;
 #pragma unroll
     for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
       const int i = wave_s * DMA_PER_WAVE + i0;
-      const int32_t kb_id = pick(t, kblk[i0]);
-      const int32_t vb_id = pick(t, vblk[i0]);
-      const uint16_t* kbase = kc + ((int64_t)kb_id * Hkv + kvh) * head_stride;
-      const uint16_t* vbase = vc + ((int64_t)vb_id * Hkv + kvh) * head_stride;
       __builtin_amdgcn_global_load_lds(
           (const void*)(kbase + koff[i0]),
-          (__attribute__((address_space(3))) void*)(&smem[buf][0][i * 1024]), 16, 0, 0);
+          (__attribute__((address_space(3))) void*)(&smem[0][buf][i * 1024]), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(
           (const void*)(vbase + voff[i0]),
-          (__attribute__((address_space(3))) void*)(&smem[buf][1][i * 1024]), 16, 0, 0);
+          (__attribute__((address_space(3))) void*)(&smem[1][buf][i * 1024]), 16, 0, 0);
     }
   };
   // A tile that reaches past the last key, or holds a block id outside the
@@ -424,14 +427,14 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // needs no per-step masking (their P is 0 and 0 * 0 = 0).  Uniform over
   // the workgroup; ends with a barrier when it writes.  Returns whether the
   // tile needs key masking.
-  auto zero_stale = [&](int kt, int buf, const TileIds& t) -> bool {
-    const bool special = kt * KT + KT > key_end || t.valid != (1 << (KT / kBlock)) - 1;
+  auto zero_stale = [&](int kt, int buf, int valid) -> bool {
+    const bool special = kt * KT + KT > key_end || valid != (1 << (KT / kBlock)) - 1;
     if (!special) return false;
-    uint16_t* vz = reinterpret_cast<uint16_t*>(&smem[buf][1][0]);
+    uint16_t* vz = reinterpret_cast<uint16_t*>(&smem[1][buf][0]);
     for (int e = threadIdx.x; e < KT * D; e += blockDim.x) {
       const int key = e / D, d = e % D;
       const int b = key / kBlock, t16 = key % kBlock;
-      const bool ok = kt * KT + key < key_end && ((t.valid >> b) & 1);
+      const bool ok = kt * KT + key < key_end && ((valid >> b) & 1);
       if (!ok) {
         const int half = (t16 / 8) ^ vswz(d);
         vz[(b * D + d) * kBlock + half * 8 + t16 % 8] = 0;
@@ -440,15 +443,16 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     __syncthreads();
     return true;
   };
-  // Sᵀ for the 32 keys of step `st` of the tile in buffer `b`.  MFMA tile
+  // Sᵀ for the 32 keys of step ST of the tile in buffer `buf`.  MFMA tile
   // kk's row i holds key 8 (i / 4) + 4 kk + i % 4 of the step, so the lane
   // (c, j) that receives rows 4j .. 4j+3 of both tiles holds keys
   // 8j .. 8j+7: eight consecutive keys of block j / 2.
-  auto qk_load = [&](int b, int st, bf16x8 (&ka)[2][KS]) {
-    const uint8_t* ks = &smem[b][0][0];
+  auto qk_load = [&](int buf, auto stc, bf16x8 (&ka)[2][KS]) {
+    constexpr int ST = decltype(stc)::value;
+    const uint8_t* ks = &smem[0][buf][0];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const int r = st * 32 + 8 * (c >> 2) + 4 * kk + (c & 3);
+      const int r = ST * 32 + 8 * (c >> 2) + 4 * kk + (c & 3);
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const int ch = (4 * s + j) ^ kswz(r);
@@ -469,76 +473,78 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     }
   };
 
-  int buf = 0;              // LDS buffer of the current tile
   bool tile_special;        // current tile needs key masking
+  int valid_cur;            // validity bits of the current tile's 4 blocks
+  int32_t id_ahead = 0;     // this wavefront's block id of the tile two ahead
   // Prologue: tiles 0 and 1 in flight, wait for tile 0.
-  TileIds ids_cur = fetch_ids(0);
-  TileIds ids_next = ids_cur, ids_next2 = ids_cur;
-  issue_tile(ids_cur, 0);
+  issue_tile(fetch_id(0), 0);
   if (n_kt > 1) {
-    ids_next = fetch_ids(1);
-    issue_tile(ids_next, 1);
+    issue_tile(fetch_id(1), 1);
     __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DMA_PER_WAVE) & 0xF) | (((2 * DMA_PER_WAVE) >> 4) << 14));
   } else {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   }
   __syncthreads();
-  tile_special = zero_stale(0, 0, ids_cur);
+  valid_cur = tile_valid(0);
+  tile_special = zero_stale(0, 0, valid_cur);
 
   bf16x8 ones;  // all-ones MFMA operand for the row sums
 #pragma unroll
   for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
   f32x4 S0[NT][2], S1[NT][2];
-  if (wave_steps > 0) {
+  {
     bf16x8 ka[2][KS];
-    qk_load(0, 0, ka);
+    qk_load(0, IC<0>{}, ka);
     qk_mfma(ka, S0);
   }
 
-  // One 32-key step: softmax of S (already computed), then in one basic
-  // block the P·V products of this step and the Sᵀ products of the next.
-  auto step = [&](int n, f32x4 (&S)[NT][2], f32x4 (&Snext)[NT][2]) {
-    const int kt = n >> 1, st = n & 1;
-    const bool act = true; (void)wave_steps;
-    // K fragments of the next step: when it is in this tile they are read
-    // now, so the softmax prep below covers their LDS latency.
-    bf16x8 ka[2][KS];
+  // One 32-key step (step ST of tile kt, held in LDS buffer `buf`):
+  // softmax of S (already computed), then in one basic block the P·V
+  // products of this step and the Sᵀ products of the next.
+  auto step = [&](int buf, auto stc, int kt, f32x4 (&S)[NT][2], f32x4 (&Snext)[NT][2]) {
+    constexpr int ST = decltype(stc)::value;
+    const int next = buf == NBUF - 1 ? 0 : buf + 1;
+    const int ahead = next == NBUF - 1 ? 0 : next + 1;
     // This step's Vᵀ fragments (dims 16 dt + c, keys 8j .. 8j+7 = one
-    // 16-byte half of the 32-byte row of block 2 st + j / 2), read first so
+    // 16-byte half of the 32-byte row of block 2 ST + j / 2), read first so
     // the softmax covers their latency.
     bf16x8 va[DT];
-    if (act) {
-      const uint8_t* vrow = &smem[buf][1][0] + (2 * st + (j >> 1)) * (D * 32) + c * 32;
+    {
+      const uint8_t* vrow = &smem[1][buf][0] + (2 * ST + (j >> 1)) * (D * 32) + c * 32;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int d = 16 * dt + c;
         va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 + (((j & 1) ^ vswz(d)) * 16));
       }
     }
-    if (act && st == 0) qk_load(buf, 1, ka);
-    // Tile boundary, at the start of a tile's second step: the next tile
-    // has landed (all waves), the buffer two tiles ahead is free again (every
-    // wavefront has finished the tile before this one), and the next tile's
-    // first K fragments are read now so this step's softmax covers them.
-    int next_buf = buf;
-    if (st == 1) {
+    // K fragments of the next step, read now so the softmax prep below
+    // covers their LDS latency.
+    bf16x8 ka[2][KS];
+    if constexpr (ST == 0) {
+      qk_load(buf, IC<1>{}, ka);
+      // this wavefront's block of the tile two ahead, a step before its copy
+      if (kt + 2 < n_kt) id_ahead = fetch_id(kt + 2);
+    } else {
+      // Tile boundary, at the start of a tile's second step: the next tile
+      // has landed (all waves), the buffer two tiles ahead is free again
+      // (every wavefront has finished the tile before this one), and the
+      // next tile's first K fragments are read now so this step's softmax
+      // covers them.  Past the last tile they are read from a buffer of
+      // stale data and the products are never used.
       if (kt + 1 < n_kt) {
-        next_buf = buf == NBUF - 1 ? 0 : buf + 1;
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): only tile kt + 1 is in flight
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kt + 2 < n_kt) issue_tile(ids_next2, next_buf == NBUF - 1 ? 0 : next_buf + 1);
+        if (kt + 2 < n_kt) issue_tile(id_ahead, ahead);
       }
-      qk_load(next_buf, 0, ka);
+      qk_load(next, IC<0>{}, ka);
     }
-    // Block ids of the tile two ahead, loaded a step before they are needed.
-    if (st == 0 && kt + 2 < n_kt) ids_next2 = fetch_ids(kt + 2);
-    if (act) {
-      const int kb = n * 32;  // first key of this step; x[i] <-> key kb + 8j + i
+    {
+      const int kb = (2 * kt + ST) * 32;  // first key of this step; x[i] <-> key kb + 8j + i
       if (tile_special || kb + 31 > past + r0) {
         // keys past the end, in invalid blocks, or above a row's diagonal
-        const int blk_lim = ((ids_cur.valid >> (2 * st + (j >> 1))) & 1) ? key_end : 0;
+        const int blk_lim = ((valid_cur >> (2 * ST + (j >> 1))) & 1) ? key_end : 0;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const int row_pos = past + r0 + 16 * nt + c;
@@ -564,7 +570,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       // only then is the exact max formed across the four lanes of the row
       // and the accumulator rescaled.  The first step always sets the max
       // (m starts at 0, which says nothing about the row's scores).
-      const bool first = n == 0;
+      const bool first = ST == 0 && kt == 0;
       if (first || __builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
@@ -586,10 +592,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       }
     }
 
-    if (act) {
-      // Operands first: this step's Vᵀ fragments and the next step's K
-      // fragments (dims 16 dt + c, keys 8j .. 8j+7 = one 16-byte half of
-      // the 32-byte row of block 2 st + j / 2).
+    {
       // The next step's Sᵀ is computed even past this wavefront's last
       // step (it is then unused): keeping it unconditional keeps this one
       // basic block.  Its MFMAs are interleaved by hand with this step's
@@ -638,17 +641,20 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       for (int nt = 0; nt < NT; ++nt)
         lacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[nt], lacc[nt], 0, 0, 0);
     }
-    if (st == 1 && kt + 1 < n_kt) {
-      buf = next_buf;
-      ids_cur = ids_next;
-      ids_next = ids_next2;
-      tile_special = zero_stale(kt + 1, buf, ids_cur);
+    if constexpr (ST == 1) {
+      if (kt + 1 < n_kt) {
+        valid_cur = tile_valid(kt + 1);
+        tile_special = zero_stale(kt + 1, next, valid_cur);
+      }
     }
   };
 
-  for (int kt = 0; kt < n_kt; ++kt) {
-    step(2 * kt, S0, S1);
-    step(2 * kt + 1, S1, S0);
+  // Tile kt sits in LDS buffer kt % NBUF.  (Unrolling this loop over the
+  // buffers, which would make every LDS address an immediate offset, costs
+  // register spills.)
+  for (int kt = 0, buf = 0; kt < n_kt; ++kt, buf = buf == NBUF - 1 ? 0 : buf + 1) {
+    step(buf, IC<0>{}, kt, S0, S1);
+    step(buf, IC<1>{}, kt, S1, S0);
   }
 
   if (!rows_active) return;
