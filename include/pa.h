@@ -199,6 +199,9 @@ size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t hea
  *   scale         softmax scale, e.g. attn_factor / sqrt(D)
  *   workspace     pa_decode_workspace_size() bytes (may be NULL if 0)
  * out[s, h] = softmax(scale * q[s, h] · K[s, h/g]ᵀ) · V[s, h/g].
+ * A table entry outside [0, num_blocks) contributes no keys (its 16
+ * positions are masked); the reference would fail on such an id instead
+ * (candle's narrow in read_kv), and its scheduler never produces one.
  * Replaces RopeGqaAttention::forward_decode's attention
  * (crates/model/src/components/attention/rope_gqa.rs:385-429) =
  * read_decode_kv + expand_kv + paged_attention
@@ -230,7 +233,8 @@ int32_t pa_decode_quantized(void* out, const void* q, const float* k_cache, cons
  *   max_q_len     host upper bound of the per-sequence query count
  * Query row i of sequence s sits at absolute position past_lens[s] + i and
  * attends keys j <= past_lens[s] + i, all read from the cache (write the
- * chunk's K/V with pa_reshape_and_cache first).
+ * chunk's K/V with pa_reshape_and_cache first).  Table entries outside
+ * [0, num_blocks) contribute no keys, as in pa_decode.
  * Replaces forward_prefill / forward_prefill_continue's attention
  * (rope_gqa.rs:261-372): tiled_attention (util.rs:188-234) for past = 0 and
  * compute_gqa_attention + prefill_continue_causal_mask

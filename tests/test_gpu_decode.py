@@ -163,3 +163,35 @@ def test_empty_context_gives_zeros(pa, oracle):
     pa.decode(q, kc, vc, torch.tensor([[0], [1]], dtype=torch.int32, device=DEV),
               torch.tensor([0, 3], dtype=torch.int32, device=DEV), 3, out=out)
     assert torch.all(out[0] == 0)
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d", [("bf16", 32, 8, 128), ("f32", 14, 2, 64)])
+def test_ids_outside_pool_are_absent_keys(pa, oracle, dtype, hq, hkv, d):
+    # A table entry outside [0, num_blocks) contributes no keys; decode
+    # attention does not depend on key order, so the result equals attention
+    # over the table without those entries and a context shorter by their
+    # 16 keys each.
+    rng = np.random.default_rng(5)
+    case = make_decode_case(rng, 3, hq, hkv, d, [100, 300, 40], dtype=dtype)
+    q, kc, vc = case["q"], case["k_cache"], case["v_cache_ref"]
+    bt, ctx = case["block_tables"], case["ctx"]
+    nb = kc.shape[0]
+    drop = [{2, 4}, {0, 9, 10, 17}, set()]
+    bad = bt.copy()
+    for b, ds in enumerate(drop):
+        for i, x in enumerate(sorted(ds)):
+            bad[b, x] = nb + i if i % 2 else -1 - i
+    out = pa.decode(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bad),
+                    to_dev(ctx), int(ctx.max()))
+    got = oracle.bf16_to_f32(to_np(out)) if dtype == "bf16" else to_np(out)
+    rows = [[x for i, x in enumerate(bt[b]) if i not in drop[b]] for b in range(len(bt))]
+    bt_c = np.zeros_like(bt)
+    for b, r in enumerate(rows):
+        bt_c[b, :len(r)] = r
+    ctx_c = (ctx - 16 * np.asarray([len(ds) for ds in drop])).astype(np.int32)
+    B = q.shape[0]
+    ref = oracle.paged_attention(oracle.as_f32(q), oracle.as_f32(kc), oracle.as_f32(vc), bt_c,
+                                 np.arange(B + 1), ctx_c - 1)
+    assert np.isfinite(got).all()
+    tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
+    assert_close(got, ref, *tol, f"decode with out-of-pool ids {dtype} {hq}/{hkv}x{d}")

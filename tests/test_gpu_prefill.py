@@ -107,3 +107,39 @@ def test_prefill_stale_nan_beyond_context(pa, oracle):
     got, ref = run_prefill(pa, oracle, q, kc, vc, bt, cu, past, "bf16")
     assert np.isfinite(got).all()
     assert_close(got, ref, BF16_ATOL, BF16_RTOL, "stale NaN")
+
+
+def compact(bt, past, drop):
+    """The table without the entries `drop[b]` (whole blocks of the past) and
+    the past length without their 16 keys each."""
+    rows = [[x for i, x in enumerate(bt[b]) if i not in drop[b]] for b in range(len(bt))]
+    out = np.zeros_like(bt)
+    for b, r in enumerate(rows):
+        out[b, :len(r)] = r
+    return out, (past - 16 * np.asarray([len(d) for d in drop])).astype(np.int32)
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d", [("bf16", 32, 8, 128), ("bf16", 14, 2, 64),
+                                            ("f32", 8, 2, 64)])
+def test_prefill_ids_outside_pool_are_absent_keys(pa, oracle, dtype, hq, hkv, d):
+    # A table entry outside [0, num_blocks) contributes no keys.  With such
+    # entries only among the past blocks every query row sees all of them,
+    # so the result equals attention over the table without those entries
+    # and a past shorter by 16 keys per entry (key order and the causal
+    # relation of the remaining keys are unchanged).
+    rng = np.random.default_rng(d + hq)
+    pasts, chunks = [200, 100, 0], [150, 33, 20]
+    q, kc, vc, bt, cu, past = make_prefill_case(oracle, rng, pasts, chunks, hq, hkv, d, dtype)
+    nb = kc.shape[0]
+    drop = [{1, 5, 6}, {0}, set()]
+    bad = bt.copy()
+    bad[0, 1], bad[0, 5], bad[0, 6], bad[1, 0] = nb + 3, -1, nb, -7
+    out = pa.prefill(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bad),
+                     to_dev(cu), to_dev(past), int(np.diff(cu).max()))
+    got = oracle.bf16_to_f32(to_np(out)) if dtype == "bf16" else to_np(out)
+    bt_c, past_c = compact(bt, past, drop)
+    ref = oracle.paged_attention(oracle.as_f32(q), oracle.as_f32(kc), oracle.as_f32(vc), bt_c,
+                                 cu, past_c)
+    assert np.isfinite(got).all()
+    tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
+    assert_close(got, ref, *tol, f"prefill with out-of-pool ids {dtype} {hq}/{hkv}x{d}")
