@@ -390,9 +390,9 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     return CPR >= 16 ? (r & 3) | (((r >> 3) & 3) << 2) : (r & 3) | (((r >> 3) & 1) << 2);
   };
   // V row swizzle: the two 16-byte halves of dim row d are swapped when
-  // bits 2 and 3 of d differ, so the 16 rows one operand read touches spread
-  // over all banks whether the LDS serves 8 or 16 lanes of 16 bytes a cycle.
-  auto vswz = [](int d) -> int { return ((d >> 2) ^ (d >> 3)) & 1; };
+  // bit 2 of d is set.  (Measured read rates of the operand pattern, per CU:
+  // ~175 B/clk with this swizzle or none, ~100 B/clk when bit 3 takes part.)
+  auto vswz = [](int d) -> int { return (d >> 2) & 1; };
   // Per-lane element offsets of this wavefront's HBM -> LDS copies (the
   // same for every tile).
   int koff[DMA_PER_WAVE], voff[DMA_PER_WAVE];
@@ -618,12 +618,19 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
             pv[nt][i] = fast_exp2(S[nt][i >> 2][i & 3]);
           }
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int x = NQK * EPM; x < NEXP; ++x) {
         const int nt = x / 8, i = x % 8;
         pv[nt][i] = fast_exp2(S[nt][i >> 2][i & 3]);
+      }
+      // The interleave is imposed on the machine scheduler (compiler passes
+      // before it may reorder the exponentials freely): groups of one MFMA
+      // then EPM transcendental instructions, in this order.
+#pragma unroll
+      for (int g = 0; g < NQK; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x400, EPM, 0);  // transcendental
       }
       bf16x8 pb[NT];
 #pragma unroll
