@@ -259,6 +259,26 @@ def time_attend_flushed(w, iters, flush_bytes=512 << 20):
     return float(np.median([a.elapsed_time(b) for a, b in ev])) / 1e3
 
 
+def gemm_ceiling(n=8192, iters=10):
+    """Measured bf16 MFMA ceiling of this GPU: a square hipBLASLt GEMM
+    (torch.matmul) of side n, in TFLOP/s.  The datasheet's 2.5 PFLOP/s is
+    the roofline peak; this is what a tuned GEMM sustains on the same box."""
+    a = torch.randn(n, n, device=DEV, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=DEV, dtype=torch.bfloat16)
+    for _ in range(2):
+        a @ b
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        a @ b
+    stop.record()
+    torch.cuda.synchronize()
+    t = start.elapsed_time(stop) / iters / 1e3
+    return 2.0 * n ** 3 / t / 1e12
+
+
 def cpu_baseline(w, budget_s=12.0):
     """Times the C oracle (restated reference CPU path: gather blocks to dense
     f32, expand KV to all query heads, full softmax, OpenMP over heads) on a
@@ -443,6 +463,10 @@ def main():
         if t_flush:
             roof["flushed_launch_us"] = round(t_flush * 1e6, 2)
             roof["flushed_frac"] = round(w.flops / t_flush / 1e12 / BF16_PEAK_TFLOPS, 4)
+        if not args.no_flush:
+            ceil = gemm_ceiling()
+            roof["gemm_ceiling_tflops"] = round(ceil, 1)
+            roof["frac_of_gemm_ceiling"] = round(value / ceil, 4)
     cpu = None if args.no_cpu else cpu_baseline(w)
     line = {
         "metric": METRIC if w.kind == "decode" else "paged-attn chunked prefill TFLOP/s",

@@ -537,6 +537,164 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// f32 caches (plain, or int8-in-f32 with one scale per block): one workgroup
+// of 1024 threads per (partition of kPart tokens, kv head, sequence) serving
+// all G query heads of the group, so each K / V byte is read once for the
+// group.  Small decode batches are latency-bound, so the work of a thread
+// is kept short and every load is issued at the start:
+//   QK:  four adjacent lanes per token, each a quarter of the K row (the
+//        four read one contiguous row), partial dot products with the G
+//        query rows (LDS) combined by two lane shuffles.
+//   softmax: one wavefront per query head, over the partition.
+//   PV:  lane (d, r) owns dim d of the blocks r, r + R, ... (R = 1024 / D);
+//        the R lanes of one dim are adjacent, so their partial sums are
+//        combined by lane shuffles.
+// Partial results use the split-K workspace format of decode_reduce_kernel.
+constexpr int kF32MaxG = 16;
+template <int D>
+__global__ __launch_bounds__(1024) void decode_f32_group_kernel(
+    float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ kc,
+    const float* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ context_lens, int Hq, int Hkv, int num_blocks,
+    float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    const float* __restrict__ kv_scales) {
+  static_assert(256 % D == 0 && D % 16 == 0, "head_dim must divide 256, in 16-float steps");
+  constexpr int NPB = kPart / kBlock;        // blocks per partition
+  constexpr int R = 1024 / D;                // lanes per dim in P·V (a power of two <= 64)
+  constexpr int NBT = NPB >= R ? NPB / R : 1;  // blocks per lane in P·V
+  constexpr int KQ = D / 16;                 // float4 per lane of a K row quarter
+  __shared__ __attribute__((aligned(16))) float qs[kF32MaxG * D];
+  __shared__ __attribute__((aligned(16))) float ps[kF32MaxG][kPart];
+  __shared__ int32_t bs[NPB];
+  __shared__ float bsc[NPB];
+  __shared__ float mls[kF32MaxG][2];
+  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int G = Hq / Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The block ids and the query rows are loaded in the same round trip as
+  // the context length (they depend only on the partition's position).
+  const int tok0 = part * kPart;
+  const int bi0 = tok0 / kBlock;
+  int32_t braw = -1;
+  if (tid < NPB && bi0 + tid < mbs) braw = block_tables[(int64_t)seq * mbs + bi0 + tid];
+  for (int e = tid; e < G * D; e += 1024) qs[e] = q[((int64_t)seq * Hq + kvh * G) * D + e];
+  const int ctx = min(context_lens[seq], mbs * kBlock);
+  if (tok0 >= ctx) {
+    if (num_parts == 1)
+      for (int e = tid; e < G * D; e += 1024) out[((int64_t)seq * Hq + kvh * G) * D + e] = 0.f;
+    return;
+  }
+  const int n = min(ctx - tok0, kPart);
+  const int nb = (n + kBlock - 1) / kBlock;
+  if (tid < NPB) {
+    const bool ok = tid < nb && braw >= 0 && braw < num_blocks;
+    bs[tid] = ok ? braw : -1;
+    bsc[tid] = ok && kv_scales ? kv_scales[braw] : 1.0f;
+  }
+  __syncthreads();
+
+  // V rows of this lane's P·V share, loaded before anything else needs them
+  const int d = wave * (64 / R) + lane / R, r = lane % R;
+  float4 vx[NBT][4];
+#pragma unroll
+  for (int i = 0; i < NBT; ++i) {
+    const int bi = r + i * R;
+    const int32_t b = bi < nb ? bs[bi] : -1;
+    const float* vr = vc + (((int64_t)(b >= 0 ? b : 0) * Hkv + kvh) * D + d) * kBlock;
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+      vx[i][x] = b >= 0 ? *reinterpret_cast<const float4*>(vr + 4 * x) : float4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // QK: token t, quarter qq of its row
+  {
+    const int t = tid >> 2, qq = tid & 3;
+    const int32_t b = t < n ? bs[t / kBlock] : -1;
+    const float* kr = kc + (((int64_t)(b >= 0 ? b : 0) * Hkv + kvh) * kBlock + t % kBlock) * D +
+                      qq * (D / 4);
+    float4 kx[KQ];
+#pragma unroll
+    for (int i = 0; i < KQ; ++i)
+      kx[i] = b >= 0 ? *reinterpret_cast<const float4*>(kr + 4 * i) : float4{0.f, 0.f, 0.f, 0.f};
+    const float ks = b >= 0 ? bsc[t / kBlock] * scale_log2 : 0.f;
+    for (int g = 0; g < G; ++g) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < KQ; ++i) {
+        const float4 qx = *reinterpret_cast<const float4*>(&qs[g * D + qq * (D / 4) + 4 * i]);
+        acc += qx.x * kx[i].x + qx.y * kx[i].y + qx.z * kx[i].z + qx.w * kx[i].w;
+      }
+      acc += __shfl_xor(acc, 1, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      if (qq == 0) ps[g][t] = b >= 0 ? acc * ks : -INFINITY;
+    }
+  }
+  __syncthreads();
+
+  // softmax over the partition, one wavefront per query head
+  if (wave < G) {
+    const int g = wave;
+    float v[kPart / 64];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kPart / 64; ++i) {
+      v[i] = ps[g][lane + 64 * i];
+      mx = fmaxf(mx, v[i]);
+    }
+    for (int w = 32; w > 0; w >>= 1) mx = fmaxf(mx, __shfl_xor(mx, w, 64));
+    const float m = mx == -INFINITY ? kNegBig : mx;
+    float l = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPart / 64; ++i) {
+      const float p = exp2f(v[i] - m);
+      ps[g][lane + 64 * i] = p;
+      l += p;
+    }
+    for (int w = 32; w > 0; w >>= 1) l += __shfl_xor(l, w, 64);
+    if (lane == 0) {
+      mls[g][0] = m;
+      mls[g][1] = l;
+    }
+  }
+  __syncthreads();
+
+  // PV: lane (d, r) over the blocks r, r + R, ..., then the R lanes of dim d
+  // combined; lane r == 0 writes
+  for (int g = 0; g < G; ++g) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NBT; ++i) {
+      const int bi = r + i * R;
+      if (bi < nb) {
+        const float* pg = &ps[g][bi * kBlock];
+        float a = 0.f;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const float4 px = *reinterpret_cast<const float4*>(pg + 4 * x);
+          a += px.x * vx[i][x].x + px.y * vx[i][x].y + px.z * vx[i][x].z + px.w * vx[i][x].w;
+        }
+        acc += a * bsc[bi];
+      }
+    }
+#pragma unroll
+    for (int w = 1; w < R; w <<= 1) acc += __shfl_xor(acc, w, 64);
+    if (r == 0) {
+      const int64_t row = (int64_t)seq * Hq + kvh * G + g;
+      if (num_parts == 1) {
+        const float l = mls[g][1];
+        out[row * D + d] = l > 0.f ? acc / l : 0.f;
+      } else {
+        ws_o[(row * num_parts + part) * D + d] = acc;
+        if (d == 0) {
+          ws_ml[2 * (row * num_parts + part)] = mls[g][0];
+          ws_ml[2 * (row * num_parts + part) + 1] = mls[g][1];
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Partition merge: one workgroup of 256 threads per (sequence, query head).
 // The partitions' (m, l) are reduced over the workgroup to M and L; thread
 // t then accumulates output dims of lane t % 64 over the partitions
@@ -641,6 +799,10 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   const bool fp8 = dtype == PA_DTYPE_FP8_E4M3;
   const bool mfma = !kv_scales && (dtype == PA_DTYPE_BF16 || fp8) && G <= 16 &&
                     (head_dim == 64 || head_dim == 128 || head_dim == 256);
+  // f32: the group kernel for head dims that divide 256 (in 4-float steps)
+  // and groups of at most kF32MaxG heads, the generic kernel otherwise
+  const bool f32_group = dtype == PA_DTYPE_F32 && G <= kF32MaxG && head_dim <= 256 &&
+                         256 % head_dim == 0 && head_dim % 16 == 0;
   const int part_len = mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len) : kPart;
   const int np = num_partitions(max_context_len, part_len);
   PA_REQUIRE(np <= 1024, PA_ERR_UNSUPPORTED,
@@ -692,6 +854,17 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
           (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
           num_blocks, scale_log2, np, ws_o, ws_ml, nullptr);
+    else if (f32_group) {
+#define PA_LAUNCH_F32(DD)                                                                     decode_f32_group_kernel<DD><<<dim3(np, num_kv_heads, num_seqs), 1024, 0, s>>>(                   (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,                  block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, num_blocks,       scale_log2, np, ws_o, ws_ml, kv_scales)
+      switch (head_dim) {
+        case 16: PA_LAUNCH_F32(16); break;
+        case 32: PA_LAUNCH_F32(32); break;
+        case 64: PA_LAUNCH_F32(64); break;
+        case 128: PA_LAUNCH_F32(128); break;
+        default: PA_LAUNCH_F32(256); break;
+      }
+#undef PA_LAUNCH_F32
+    }
     else
       decode_generic_kernel<float><<<grid, 256, 0, s>>>(
           (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,
