@@ -65,10 +65,10 @@ class Workload:
         self.pa = pa
         self.name = name
         g = torch.Generator().manual_seed({"decode": 1, "decode-fp8": 1, "prefill": 2,
-                                           "splitk": 3, "qwen": 0}[name])
+                                           "prefill-fp8": 2, "splitk": 3, "qwen": 0}[name])
         dg = torch.Generator(device=DEV).manual_seed(1234)
         self.kind = "decode"
-        self.fp8 = name == "decode-fp8"
+        self.fp8 = name in ("decode-fp8", "prefill-fp8")
         if name in ("decode", "decode-fp8"):
             B, hq, hkv, d, ctx = 64, 32, 8, 128, 4096
             self.dtype = torch.bfloat16
@@ -118,7 +118,7 @@ class Workload:
             kv_scale = 1.0
             self.workload = ("config 1: Qwen2.5-0.5B decode f32, B 8, 14/2 x 64, "
                              "ctx U[128, 1024], pool 1024 blocks")
-        elif name == "prefill":
+        elif name in ("prefill", "prefill-fp8"):
             self.kind = "prefill"
             hq, hkv, d = 32, 8, 128
             self.dtype = torch.bfloat16
@@ -144,6 +144,10 @@ class Workload:
             self.flops = 4.0 * self.pairs * hq * d
             self.workload = ("config 3: Llama-3-8B chunked causal prefill bf16, 4 x 2048 new "
                              "tokens on past 0/512/1024/2048, 32/8 x 128")
+            if self.fp8:
+                self.workload = ("config 3 shape over an FP8-E4M3 KV cache (reference codes), "
+                                 "q/out bf16, 4 x 2048 new tokens on past 0/512/1024/2048, "
+                                 "32/8 x 128")
         else:
             raise SystemExit(f"unknown config {name}")
         self.B, self.hq, self.hkv, self.d = B, hq, hkv, d
@@ -192,7 +196,8 @@ class Workload:
         else:
             self.out = torch.empty_like(self.q)
             tokens_all = sum(p + 2048 for p in [0, 512, 1024, 2048])
-            self.alg_bytes = (2 * tokens_all * hkv * d * es + 2 * self.q.numel() * es)
+            kv_es = 1 if self.fp8 else es
+            self.alg_bytes = (2 * tokens_all * hkv * d * kv_es + 2 * self.q.numel() * es)
 
     def write_step(self):
         if self.fp8:
@@ -404,7 +409,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="decode",
-                    choices=["decode", "decode-fp8", "prefill", "splitk", "qwen", "e2e", "copy"])
+                    choices=["decode", "decode-fp8", "prefill", "prefill-fp8", "splitk", "qwen",
+                             "e2e", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-flush", action="store_true",
                     help="skip the cache-flushed timing leg (keeps a kernel trace to warm launches)")
@@ -458,7 +464,8 @@ def main():
         roof = {"bound": "mfma", "achieved": round(value, 2), "peak": BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(value / BF16_PEAK_TFLOPS, 4),
                 "traffic": measured_traffic(args.config),
-                "kernel": "pa_prefill (prefill_tiled_kernel)", "flops_per_launch": w.flops,
+                "kernel": ("pa_prefill (prefill_tiled_kernel, FP8 tiles)" if w.fp8 else
+                           "pa_prefill (prefill_tiled_kernel)"), "flops_per_launch": w.flops,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
         if t_flush:
             roof["flushed_launch_us"] = round(t_flush * 1e6, 2)

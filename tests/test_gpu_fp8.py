@@ -150,3 +150,35 @@ def test_prefill_fp8(pa, oracle):
     ref = oracle.paged_attention(oracle.bf16_to_f32(q), oracle.fp8_decode(kc),
                                  oracle.fp8_decode(vc), bt, cu, past)
     assert_close(got, ref, BF16_ATOL, BF16_RTOL, "fp8 prefill")
+
+
+@pytest.mark.parametrize("hq,hkv,d,pasts,chunks", [
+    (32, 8, 128, [0, 512, 130], [300, 200, 77]),   # config 3 heads, several tiles
+    (14, 2, 64, [0, 37, 1000], [129, 64, 5]),
+    (8, 8, 128, [16, 0], [1, 90]),
+])
+def test_prefill_fp8_tiled_shapes(pa, oracle, hq, hkv, d, pasts, chunks):
+    # the LDS-tiled kernel on FP8 caches: K / V tiles copied as FP8 and
+    # converted to bf16 per operand fragment
+    rng = np.random.default_rng(hq * d + len(pasts))
+    B = len(pasts)
+    nblk = [(p + c + 15) // 16 for p, c in zip(pasts, chunks)]
+    nb = sum(nblk) + 5
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = np.zeros((B, max(nblk)), np.int32)
+    o = 0
+    for b in range(B):
+        bt[b, :nblk[b]] = perm[o:o + nblk[b]]
+        o += nblk[b]
+    kc = oracle.fp8_encode(rng.standard_normal((nb, hkv, 16, d), dtype=np.float32) * 2)
+    vc = oracle.fp8_encode(rng.standard_normal((nb, hkv, 16, d), dtype=np.float32))
+    q = oracle.f32_to_bf16(rng.standard_normal((sum(chunks), hq, d), dtype=np.float32))
+    cu = np.concatenate([[0], np.cumsum(chunks)]).astype(np.int32)
+    past = np.asarray(pasts, np.int32)
+    out = pa.prefill(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt),
+                     to_dev(cu), to_dev(past), max(chunks))
+    got = oracle.bf16_to_f32(to_np(out))
+    ref = oracle.paged_attention(oracle.bf16_to_f32(q), oracle.fp8_decode(kc),
+                                 oracle.fp8_decode(vc), bt, cu, past)
+    assert np.isfinite(got).all()
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, f"fp8 prefill {hq}/{hkv}x{d}")

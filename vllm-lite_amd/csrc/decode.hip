@@ -279,14 +279,6 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
 //  * P·V: reduction slot 8 j + i is token 8 (j & 1) + i of block j >> 1, so
 //    the Vᵀ operand of dims 16 dt + c is one 8-byte load from the
 //    token-minor block.
-__device__ inline bf16x8 fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
-  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
-  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
-  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
-  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
-  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
 template <int D>
 __global__ __launch_bounds__(64) void decode_fp8_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,

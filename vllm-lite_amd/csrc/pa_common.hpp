@@ -20,6 +20,17 @@ typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
+// Eight FP8-E4M3 codes (little-endian bytes of lo, hi) to bf16, exactly
+// (every E4M3 value is a bf16 value), with the hardware's unscaled
+// conversion.
+__device__ inline bf16x8 fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+  const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+  const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+  return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
 // bf16 <-> f32 on raw 16-bit patterns (round to nearest even, NaN kept quiet).
 __host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);

@@ -237,22 +237,28 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
 // sequences, and the tiles that share K/V then share that XCD's L2.  Within
 // a chunk the sequences go from most to least work, and within a sequence
 // the later (longer) query tiles go first.
-template <int D, int NT>
+template <int D, int NT, typename TC>
 __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const TC* __restrict__ kc,
+    const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
     int num_blocks, float scale_log2, int B, int tiles_per_seq, int head_groups) {
   constexpr int KS = D / 32;   // QK reduction steps
   constexpr int DT = D / 16;   // PV output tiles
-  constexpr int CPR = D / 8;   // 16-byte chunks per K row
+  // Cache elements: bf16 (TC = uint16_t) or FP8-E4M3 (TC = uint8_t), the
+  // latter converted to bf16 (exactly) as operand fragments are read.
+  constexpr bool FP8 = sizeof(TC) == 1;
+  constexpr int ES = sizeof(TC);
+  constexpr int CPR = D * ES / 16;  // 16-byte chunks per K row
   constexpr int KT = 64;       // keys per LDS tile
   constexpr int W = 16 / NT;   // wavefronts per workgroup (64 query rows x 4 heads)
   constexpr int NBUF = 3;      // LDS tile buffers
-  constexpr int TILE_BYTES = KT * D * 2;  // one K (or V) tile
-  constexpr int DMA_PER_WAVE = TILE_BYTES / 1024 / W;
-  constexpr int RPI = 64 / CPR;        // K rows per 1 KB chunk
-  constexpr int CPB = D * 32 / 1024;   // 1 KB chunks per V block
+  constexpr int TILE_BYTES = KT * D * ES;  // one K (or V) tile
+  constexpr int NCH = TILE_BYTES / 1024;   // 1 KB copy chunks per tile
+  constexpr int DMA_PER_WAVE = NCH >= W ? NCH / W : 1;
+  constexpr int DMA_WAVES = NCH >= W ? W : NCH;  // wavefronts that copy
+  constexpr int RPI = 64 / CPR;              // K rows per 1 KB chunk
+  constexpr int CPB = D * kBlock * ES / 1024;  // 1 KB chunks per V block
   // 1 KB chunk i of a K tile and of a V tile lie in the same cache block
   // (i / CPB), and a wavefront's chunks stay within one block
   static_assert(RPI * CPB == kBlock && CPB % DMA_PER_WAVE == 0, "one block per wavefront copy");
@@ -393,6 +399,14 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // bit 2 of d is set.  (Measured read rates of the operand pattern, per CU:
   // ~175 B/clk with this swizzle or none, ~100 B/clk when bit 3 takes part.)
   auto vswz = [](int d) -> int { return (d >> 2) & 1; };
+  // FP8 K rows (D bytes) are read in 8-byte units (one MFMA fragment); unit
+  // u of row r sits at unit position u ^ fsw(r).  Bit 0 is never flipped,
+  // so an aligned 16-byte pair of units stays contiguous (one copy lane),
+  // and the 32 lanes served together hit distinct bank pairs.  FP8 V dim
+  // rows are 16 bytes and need no swizzle.
+  auto fsw = [](int r) -> int {
+    return D >= 128 ? (((r >> 1) & 1) << 1) | (((r >> 3) & 3) << 2) : ((r >> 3) & 3) << 1;
+  };
   // Per-lane element offsets of this wavefront's HBM -> LDS copies (the
   // same for every tile).
   int koff[DMA_PER_WAVE], voff[DMA_PER_WAVE];
@@ -400,16 +414,22 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
     const int i = wave_s * DMA_PER_WAVE + i0;  // 1 KB chunk of the tile
     const int r = i * RPI + lane / CPR;
-    koff[i0] = (r % kBlock) * D + ((lane % CPR) ^ kswz(r)) * 8;
-    const int d = (i % CPB) * 32 + lane / 2;
-    voff[i0] = d * kBlock + ((lane & 1) ^ vswz(d)) * 8;
+    if constexpr (FP8) {
+      koff[i0] = (r % kBlock) * D + ((lane % CPR) ^ (fsw(r) >> 1)) * 16;
+      voff[i0] = ((i % CPB) * 64 + lane) * kBlock;
+    } else {
+      koff[i0] = (r % kBlock) * D + ((lane % CPR) ^ kswz(r)) * 8;
+      const int d = (i % CPB) * 32 + lane / 2;
+      voff[i0] = d * kBlock + ((lane & 1) ^ vswz(d)) * 8;
+    }
   }
   // Issues this wavefront's share of the HBM -> LDS copies of a key tile
   // into LDS buffer `buf`; `id` is the cache block those copies read.
   auto issue_tile = [&](int32_t id, int buf) {
     const int64_t boff = ((int64_t)id * Hkv + kvh) * head_stride;
-    const uint16_t* kbase = kc + boff;
-    const uint16_t* vbase = vc + boff;
+    const TC* kbase = kc + boff;
+    const TC* vbase = vc + boff;
+    if (NCH < W && wave_s >= DMA_WAVES) return;  // the tile has fewer chunks than wavefronts
 #pragma unroll
     for (int i0 = 0; i0 < DMA_PER_WAVE; ++i0) {
       const int i = wave_s * DMA_PER_WAVE + i0;
@@ -430,13 +450,13 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   auto zero_stale = [&](int kt, int buf, int valid) -> bool {
     const bool special = kt * KT + KT > key_end || valid != (1 << (KT / kBlock)) - 1;
     if (!special) return false;
-    uint16_t* vz = reinterpret_cast<uint16_t*>(&smem[1][buf][0]);
+    TC* vz = reinterpret_cast<TC*>(&smem[1][buf][0]);
     for (int e = threadIdx.x; e < KT * D; e += blockDim.x) {
       const int key = e / D, d = e % D;
       const int b = key / kBlock, t16 = key % kBlock;
       const bool ok = kt * KT + key < key_end && ((valid >> b) & 1);
       if (!ok) {
-        const int half = (t16 / 8) ^ vswz(d);
+        const int half = FP8 ? t16 / 8 : (t16 / 8) ^ vswz(d);
         vz[(b * D + d) * kBlock + half * 8 + t16 % 8] = 0;
       }
     }
@@ -455,8 +475,13 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       const int r = ST * 32 + 8 * (c >> 2) + 4 * kk + (c & 3);
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const int ch = (4 * s + j) ^ kswz(r);
-        ka[kk][s] = *reinterpret_cast<const bf16x8*>(ks + r * (D * 2) + ch * 16);
+        if constexpr (FP8) {
+          const uint2 w = *reinterpret_cast<const uint2*>(ks + r * D + ((4 * s + j) ^ fsw(r)) * 8);
+          ka[kk][s] = fp8x8_to_bf16(w.x, w.y);
+        } else {
+          const int ch = (4 * s + j) ^ kswz(r);
+          ka[kk][s] = *reinterpret_cast<const bf16x8*>(ks + r * (D * 2) + ch * 16);
+        }
       }
     }
   };
@@ -510,11 +535,20 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     // the softmax covers their latency.
     bf16x8 va[DT];
     {
-      const uint8_t* vrow = &smem[1][buf][0] + (2 * ST + (j >> 1)) * (D * 32) + c * 32;
+      if constexpr (FP8) {
+        const uint8_t* vrow = &smem[1][buf][0] + ((2 * ST + (j >> 1)) * D + c) * 16 + 8 * (j & 1);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int d = 16 * dt + c;
-        va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 + (((j & 1) ^ vswz(d)) * 16));
+        for (int dt = 0; dt < DT; ++dt) {
+          const uint2 w = *reinterpret_cast<const uint2*>(vrow + dt * 16 * 16);
+          va[dt] = fp8x8_to_bf16(w.x, w.y);
+        }
+      } else {
+        const uint8_t* vrow = &smem[1][buf][0] + (2 * ST + (j >> 1)) * (D * 32) + c * 32;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int d = 16 * dt + c;
+          va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 + (((j & 1) ^ vswz(d)) * 16));
+        }
       }
     }
     // K fragments of the next step, read now so the softmax prep below
@@ -803,7 +837,9 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
              PA_ERR_INVALID_ARG, "pa_prefill: null pointer");
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  const bool tiled = !kv_scales && dtype == PA_DTYPE_BF16 && (head_dim == 64 || head_dim == 128);
+  const bool fp8 = dtype == PA_DTYPE_FP8_E4M3;
+  const bool tiled = !kv_scales && (dtype == PA_DTYPE_BF16 || fp8) &&
+                     (head_dim == 64 || head_dim == 128);
   const bool mfma = !kv_scales && dtype == PA_DTYPE_BF16 && head_dim == 256;
   if (tiled) {
     const int G = num_heads / num_kv_heads;
@@ -818,17 +854,24 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
     const dim3 grid(8 * std::max(1, std::min(per_xcd, compute_units() / 8)));
     auto* o = (uint16_t*)out;
     auto* qq = (const uint16_t*)q;
-    auto* kc = (const uint16_t*)k_cache;
-    auto* vc = (const uint16_t*)v_cache;
     constexpr int NT = 2;
-    if (head_dim == 128)
-      prefill_tiled_kernel<128, NT><<<grid, 64 * (16 / NT), 0, s>>>(
-          o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,
-          num_kv_heads, num_blocks, scale_log2, num_seqs, tiles_per_seq, head_groups);
-    else
-      prefill_tiled_kernel<64, NT><<<grid, 64 * (16 / NT), 0, s>>>(
-          o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,
-          num_kv_heads, num_blocks, scale_log2, num_seqs, tiles_per_seq, head_groups);
+#define PA_LAUNCH_TILED(DD, TC)                                                               \
+  prefill_tiled_kernel<DD, NT, TC><<<grid, 64 * (16 / NT), 0, s>>>(                           \
+      o, qq, (const TC*)k_cache, (const TC*)v_cache, block_tables, max_blocks_per_seq,        \
+      cu_q_lens, past_lens, num_heads, num_kv_heads, num_blocks, scale_log2, num_seqs,        \
+      tiles_per_seq, head_groups)
+    if (fp8) {
+      if (head_dim == 128)
+        PA_LAUNCH_TILED(128, uint8_t);
+      else
+        PA_LAUNCH_TILED(64, uint8_t);
+    } else {
+      if (head_dim == 128)
+        PA_LAUNCH_TILED(128, uint16_t);
+      else
+        PA_LAUNCH_TILED(64, uint16_t);
+    }
+#undef PA_LAUNCH_TILED
   } else if (mfma) {
     constexpr int NT = 2;
     const int rows_per_wg = 16 * NT * kWaves;
