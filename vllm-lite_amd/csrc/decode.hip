@@ -73,6 +73,46 @@ __device__ inline bool private_block(const int32_t* __restrict__ block_tables, i
   return !prev && !next;
 }
 
+// Merge of the partial results held by the NW wavefronts of a workgroup,
+// one partition each, together all partitions of one (kv head, sequence):
+// through LDS, with the log-sum-exp rule of decode_reduce_kernel
+//     M = max_w m_w,  out = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w,
+// written as the bf16 output of the group's G query heads (empty partitions
+// hold m = kNegBig, l = 0, o = 0 and drop out).  Lane (c, j) holds head c's
+// o[dt][r] for dims 16 dt + 4 j + r, as the MFMA decode kernels leave it.
+template <int D, int NW>
+__device__ inline void merge_in_workgroup(uint16_t* __restrict__ out_group, const f32x4 (&o)[D / 16],
+                                          float m, float lsum, int c, int j, int G) {
+  __shared__ float so[NW][16][D];
+  __shared__ float sml[NW][16][2];
+  const int wave = threadIdx.x >> 6;
+  if (c < G) {
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) so[wave][c][16 * dt + 4 * j + r] = o[dt][r];
+    if (j == 0) {
+      sml[wave][c][0] = m;
+      sml[wave][c][1] = lsum;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * D; idx += 64 * NW) {
+    const int hc = idx / D, d = idx % D;
+    float mx = kNegBig;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sml[w][hc][0]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float a = fast_exp2(sml[w][hc][0] - mx);
+      num += a * so[w][hc][d];
+      den += a * sml[w][hc][1];
+    }
+    out_group[idx] = f32_to_bf16_bits(den > 0.f ? num / den : 0.f);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // MFMA decode kernel.
 //
@@ -88,8 +128,8 @@ __device__ inline bool private_block(const int32_t* __restrict__ block_tables, i
 //      8j+r / 8j+4+r are tokens 4j+r of the first / second block of the step,
 //      which is exactly what the lane already holds from QK.  Result: lane
 //      holds Oᵀ[dim 16dt + 4j + r][head c].
-template <int D>
-__global__ __launch_bounds__(64) void decode_mfma_kernel(
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
@@ -97,14 +137,19 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
     float* __restrict__ ws_ml) {
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
-  const int lane = threadIdx.x;
+  // NW > 1: the workgroup's wavefronts take partitions blockIdx.x * NW + w
+  // (the launch uses it only when one workgroup holds all of them) and merge
+  // them in LDS; NW = 1: one partition, merged by decode_reduce_kernel.
+  const int lane = threadIdx.x & 63;
   const int c = lane & 15, j = lane >> 4;
-  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int part = blockIdx.x * NW + (NW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0);
+  const int kvh = blockIdx.y, seq = blockIdx.z;
   // Clamp to what the block table can address so a bad length never reads
   // past the table.
   const int ctx = min(context_lens[seq], mbs * kBlock);
   const int tok0 = part * part_len;
-  if (tok0 >= ctx) {
+  const bool empty = tok0 >= ctx;
+  if (NW == 1 && empty) {
     // Empty context: the output is defined as zeros.
     if (num_parts == 1 && c < G) {
       uint16_t* orow = out + ((int64_t)seq * Hq + kvh * G + c) * D;
@@ -112,8 +157,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
     }
     return;
   }
-  const int tok_end = min(ctx, tok0 + part_len);
-  const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;
+  const int tok_end = empty ? tok0 : min(ctx, tok0 + part_len);
+  const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;  // 0 for an empty partition
 
   const int head = kvh * G + c;
   bf16x8 qv[KS];
@@ -237,6 +282,10 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
 
   lsum += shfl_xor_f(lsum, 16);
   lsum += shfl_xor_f(lsum, 32);
+  if constexpr (NW > 1) {
+    merge_in_workgroup<D, NW>(out + ((int64_t)seq * Hq + kvh * G) * D, o, m, lsum, c, j, G);
+    return;
+  }
   if (c >= G) return;
   if (num_parts == 1) {
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
@@ -279,8 +328,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(
 //  * P·V: reduction slot 8 j + i is token 8 (j & 1) + i of block j >> 1, so
 //    the Vᵀ operand of dims 16 dt + c is one 8-byte load from the
 //    token-minor block.
-template <int D>
-__global__ __launch_bounds__(64) void decode_fp8_kernel(
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
     const uint8_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
@@ -289,20 +338,25 @@ __global__ __launch_bounds__(64) void decode_fp8_kernel(
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
   constexpr int DL = D / 4;   // dims (bytes) of a K row per lane group
-  const int lane = threadIdx.x;
+  // NW > 1: the workgroup's wavefronts take partitions blockIdx.x * NW + w
+  // (the launch uses it only when one workgroup holds all of them) and merge
+  // them in LDS; NW = 1: one partition, merged by decode_reduce_kernel.
+  const int lane = threadIdx.x & 63;
   const int c = lane & 15, j = lane >> 4;
-  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int part = blockIdx.x * NW + (NW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0);
+  const int kvh = blockIdx.y, seq = blockIdx.z;
   const int ctx = min(context_lens[seq], mbs * kBlock);
   const int tok0 = part * part_len;
-  if (tok0 >= ctx) {
+  const bool empty = tok0 >= ctx;
+  if (NW == 1 && empty) {
     if (num_parts == 1 && c < G) {
       uint16_t* orow = out + ((int64_t)seq * Hq + kvh * G + c) * D;
       for (int d = 4 * j; d < D; d += 16) *reinterpret_cast<uint64_t*>(orow + d) = 0;
     }
     return;
   }
-  const int tok_end = min(ctx, tok0 + part_len);
-  const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;
+  const int tok_end = empty ? tok0 : min(ctx, tok0 + part_len);
+  const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;  // 0 for an empty partition
 
   const int head = kvh * G + c;
   bf16x8 qv[KS];
@@ -412,6 +466,10 @@ __global__ __launch_bounds__(64) void decode_fp8_kernel(
 
   lsum += shfl_xor_f(lsum, 16);
   lsum += shfl_xor_f(lsum, 32);
+  if constexpr (NW > 1) {
+    merge_in_workgroup<D, NW>(out + ((int64_t)seq * Hq + kvh * G) * D, o, m, lsum, c, j, G);
+    return;
+  }
   if (c >= G) return;
   if (num_parts == 1) {
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
@@ -799,9 +857,12 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   const int np = num_partitions(max_context_len, part_len);
   PA_REQUIRE(np <= 1024, PA_ERR_UNSUPPORTED,
              "pa_decode: context of %d tokens needs %d > 1024 partitions", max_context_len, np);
+  // MFMA kernels: up to 4 partitions are taken by one workgroup (one
+  // wavefront each) and merged in LDS, with no workspace and no reduce launch.
+  const int merge_waves = (mfma && np > 1 && np <= 4) ? (np == 2 ? 2 : 4) : 1;
   float* ws_o = nullptr;
   float* ws_ml = nullptr;
-  if (np > 1) {
+  if (np > 1 && merge_waves == 1) {
     const size_t need = (size_t)num_seqs * num_heads * np * (head_dim + 2) * sizeof(float);
     PA_REQUIRE(workspace && workspace_bytes >= need, PA_ERR_WORKSPACE,
                "pa_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
@@ -811,13 +872,23 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   if (mfma) {
-    const dim3 grid(np, num_kv_heads, num_seqs);
+    const dim3 grid(merge_waves > 1 ? 1 : np, num_kv_heads, num_seqs);
     auto* o = (uint16_t*)out;
     auto* qq = (const uint16_t*)q;
-#define PA_LAUNCH_MFMA(KERNEL, TC, DD)                                                          \
-  KERNEL<DD><<<grid, 64, 0, s>>>(o, qq, (const TC*)k_cache, (const TC*)v_cache, block_tables,  \
-                                 max_blocks_per_seq, context_lens, num_heads, num_kv_heads, G, \
-                                 num_blocks, scale_log2, np, part_len, ws_o, ws_ml)
+#define PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, NW)                                                 \
+  KERNEL<DD, NW><<<grid, 64 * NW, 0, s>>>(                                                    \
+      o, qq, (const TC*)k_cache, (const TC*)v_cache, block_tables, max_blocks_per_seq,        \
+      context_lens, num_heads, num_kv_heads, G, num_blocks, scale_log2, np, part_len, ws_o,   \
+      ws_ml)
+#define PA_LAUNCH_MFMA(KERNEL, TC, DD)                                                        \
+  do {                                                                                        \
+    if (merge_waves == 2)                                                                     \
+      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 2);                                                   \
+    else if (merge_waves == 4)                                                                \
+      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 4);                                                   \
+    else                                                                                      \
+      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 1);                                                   \
+  } while (0)
     if (fp8) {
       if (head_dim == 64)
         PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 64);
@@ -834,6 +905,7 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
         PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 256);
     }
 #undef PA_LAUNCH_MFMA
+#undef PA_LAUNCH_MFMA_NW
   } else {
     const dim3 grid(np, num_heads, num_seqs);
     if (fp8)
@@ -864,7 +936,7 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
           num_blocks, scale_log2, np, ws_o, ws_ml, kv_scales);
   }
   int32_t rc = check_launch("pa_decode");
-  if (rc != PA_OK || np == 1) return rc;
+  if (rc != PA_OK || np == 1 || merge_waves > 1) return rc;
   const dim3 rgrid(num_seqs * num_heads);
   if (dtype == PA_DTYPE_BF16 || fp8)
     decode_reduce_kernel<uint16_t><<<rgrid, 256, 0, s>>>((uint16_t*)out, ws_o, ws_ml,
