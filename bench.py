@@ -346,6 +346,7 @@ def run_e2e(pa, args):
 
     cfg = e2e.qwen25_05b()
     w = e2e.Weights(cfg, seed=4, device=DEV)
+    w.pack()  # load-time layout step of pa_linear's weights
     n_req, max_new = 32, 256
     g = torch.Generator().manual_seed(5)
     lens = torch.randint(64, 513, (n_req,), generator=g).tolist()

@@ -1,9 +1,10 @@
 /*
  * pa_dense.h -- the dense side around the paged-attention path, for an
  * end-to-end decoder step: RMSNorm or LayerNorm (with the residual add fused
- * in) and the SwiGLU activation.  The projections themselves are plain GEMMs and run in
- * hipBLASLt.  Conventions as pa.h (device pointers, stream-ordered, PA_OK or
- * a negative pa_status); dtype PA_DTYPE_F32 or PA_DTYPE_BF16, math in f32.
+ * in), the SwiGLU activation, and skinny-M linear projections for decode
+ * steps (larger batches use hipBLASLt).  Conventions as pa.h (device
+ * pointers, stream-ordered, PA_OK or a negative pa_status); dtype
+ * PA_DTYPE_F32 or PA_DTYPE_BF16, math in f32.
  */
 #ifndef VLLM_LITE_AMD_PA_DENSE_H
 #define VLLM_LITE_AMD_PA_DENSE_H
@@ -42,6 +43,38 @@ int32_t pa_layer_norm(void* out, void* residual, const void* add, const void* we
  * silu(x) = x / (1 + e^-x).  gate_up [rows, 2 * inter], out [rows, inter]. */
 int32_t pa_silu_mul(void* out, const void* gate_up, int32_t rows, int32_t inter, int32_t dtype,
                     pa_stream_t stream);
+
+/* Activation epilogues of pa_linear. */
+enum { PA_ACT_NONE = 0, PA_ACT_SILU_MUL = 1 };
+
+/* The decoder's linear projections for the few-row batches of a decode step
+ * (candle_nn::Linear as the reference's attention and MLP use it: the QKV
+ * projection with bias, crates/model/src/components/attention/rope_gqa.rs:261-302,
+ * the output projection, and the MLP's gate/up/down projections,
+ * crates/model/src/components/mlp/swiglu.rs:18-31), plus the tied LM head:
+ *   act PA_ACT_NONE:      out[r][n] = sum_k x[r][k] * weight[n][k] (+ bias[n])
+ *   act PA_ACT_SILU_MUL:  weight is the fused gate|up matrix [2 N, K] and
+ *                         out[r][n] = silu(g) * u with g, u the gate / up
+ *                         outputs of column n rounded to bf16 (pa_silu_mul on
+ *                         the unfused projection's output); bias must be NULL.
+ * x [rows, K], weight [N or 2 N, K], out [rows, N], all contiguous bf16 and
+ * 16-byte aligned, bias [N] or NULL; K (in_features) a multiple of 32, N
+ * (out_features) a multiple of 16.  f32 accumulation.
+ * packed = 1: weight is in the layout of pa_linear_pack (rows N or 2 N).
+ * Built for rows <= 64, where the weights dominate the traffic; the weights
+ * are re-read once per 32 rows.  bf16 only (PA_ERR_UNSUPPORTED otherwise). */
+int32_t pa_linear(void* out, const void* x, const void* weight, const void* bias, int32_t rows,
+                  int32_t out_features, int32_t in_features, int32_t act, int32_t packed,
+                  int32_t dtype, pa_stream_t stream);
+
+/* Repacks a row-major bf16 weight [rows, cols] (rows a multiple of 16, cols
+ * of 32) into the fragment order pa_linear reads with packed = 1: every
+ * 16-row x 32-column MFMA operand fragment becomes one contiguous kilobyte,
+ * the fragments of a 16-row tile consecutive along the columns.  Same size as
+ * the input; packed and weight must not overlap.  No reference counterpart:
+ * a load-time layout step for the weights pa_linear streams. */
+int32_t pa_linear_pack(void* packed, const void* weight, int32_t rows, int32_t cols,
+                       int32_t dtype, pa_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -66,11 +66,21 @@ def test_argument_errors_without_gpu(lib):
     rc = lib.pa_decode(null, null, null, null, null, 4, null, 65, 1, 8, 2, 64, 16, 1.0, null, 0,
                        1, null)
     assert rc == -2
-    # missing workspace for a split launch (null pointers are checked first)
+    # missing workspace for a launch merged by the reduce kernel (more than 4
+    # partitions; null pointers are checked first)
     rc = lib.pa_decode(C.c_void_p(8), C.c_void_p(8), C.c_void_p(8), C.c_void_p(8),
-                       C.c_void_p(8), 64, C.c_void_p(8), 1024, 1, 8, 2, 64, 16, 1.0, null, 0, 1,
+                       C.c_void_p(8), 256, C.c_void_p(8), 4096, 1, 8, 2, 64, 16, 1.0, null, 0, 1,
                        null)
     assert rc == -4 and b"workspace" in lib.pa_last_error()
+    # pa_linear: f32, K not a multiple of 32, N not a multiple of 16, bias with SwiGLU
+    p = C.c_void_p(16)
+    assert lib.pa_linear(p, p, p, null, 4, 64, 96, 0, 0, 0, null) == -3
+    assert lib.pa_linear(p, p, p, null, 4, 64, 80, 0, 0, 1, null) == -3
+    assert b"multiple of 32" in lib.pa_last_error()
+    assert lib.pa_linear(p, p, p, null, 4, 40, 96, 0, 0, 1, null) == -3
+    assert lib.pa_linear(p, p, p, p, 4, 48, 96, 1, 0, 1, null) == -1
+    assert lib.pa_linear(null, null, null, null, 0, 64, 96, 0, 0, 1, null) == 0
+    assert lib.pa_linear_pack(p, C.c_void_p(32), 24, 64, 1, null) == -3  # rows not a multiple of 16
     # read_kv: table cannot hold seq_len
     rc = lib.pa_read_kv(null, null, null, 1, 17, 2, 4, 4, null, null, 0, null)
     assert rc == -2

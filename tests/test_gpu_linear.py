@@ -1,0 +1,84 @@
+"""GPU parity of pa_linear (the skinny-M projections of a decode step) against
+an fp32 torch matmul of the same bf16 operands: plain, with bias, and with the
+fused SwiGLU epilogue; ragged row counts around the 32-row tile, K split over
+one and many wavefronts; argument errors."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def operands(m, n, k, seed, wscale=0.02):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=DEV) * wscale).to(torch.bfloat16)
+    b = (torch.randn(n, generator=g, device=DEV) * 0.1).to(torch.bfloat16)
+    return x, w, b
+
+
+def close(out, ref):
+    # bf16 output of an f32-accumulated product: half an ulp of bf16 plus the
+    # f32 summation-order difference
+    torch.testing.assert_close(out.float(), ref, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 32, 32), (5, 64, 896), (32, 1152, 896), (33, 896, 4864),
+                                   (64, 896, 896), (17, 256, 4864), (31, 4096, 96),
+                                   (9, 48, 64), (40, 1008, 128)])
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("packed", [False, True])
+def test_linear_matches_fp32(pa, m, n, k, with_bias, packed):
+    x, w, b = operands(m, n, k, m * 7 + n + k)
+    out = pa.linear(x, pa.ops.PackedWeight(w) if packed else w, bias=b if with_bias else None)
+    ref = x.float() @ w.float().T
+    if with_bias:
+        ref = ref + b.float()
+    assert out.shape == (m, n) and out.dtype == torch.bfloat16
+    close(out, ref)
+
+
+@pytest.mark.parametrize("m,inter,k", [(32, 4864, 896), (3, 16, 64), (40, 48, 4864)])
+def test_linear_swiglu_matches_unfused(pa, m, inter, k):
+    x, w, _ = operands(m, 2 * inter, k, m + inter + k, wscale=0.05)
+    out = pa.linear(x, w, act=pa.ops.ACT_SILU_MUL)
+    gu = (x.float() @ w.float().T).to(torch.bfloat16).float()  # the unfused projection's output
+    ref = F.silu(gu[:, :inter]) * gu[:, inter:]
+    assert out.shape == (m, inter)
+    close(out, ref)
+    # and the same as the unfused path through pa_silu_mul, and from packed weights
+    unfused = pa.silu_mul(pa.linear(x, w))
+    close(out, unfused.float())
+    assert torch.equal(pa.linear(x, pa.ops.PackedWeight(w), act=pa.ops.ACT_SILU_MUL), out)
+
+
+@pytest.mark.parametrize("n,k", [(16, 32), (48, 96), (896, 4864)])
+def test_pack_layout(pa, n, k):
+    # fragment (tile, step) is 1 KB; lane 16 j + c holds row 16 tile + c,
+    # columns 32 step + 8 j .. +7 -- an independent torch restatement
+    _, w, _ = operands(1, n, k, n + k)
+    packed = pa.ops.PackedWeight(w).data
+    ref = w.view(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(n, k)
+    assert torch.equal(packed, ref)
+
+
+def test_lm_head_shape(pa):
+    # the tied LM head of the Qwen2.5-0.5B shape: 151936 outputs, K = 896
+    x, w, _ = operands(32, 151936, 896, 5)
+    out = pa.linear(x, w)
+    close(out, x.float() @ w.float().T)
+
+
+def test_linear_rejects_unsupported(pa):
+    x, w, b = operands(4, 64, 96, 1)
+    with pytest.raises(pa.PaError):
+        pa.linear(x[:, :80].contiguous(), w[:, :80].contiguous())  # K not a multiple of 32
+    with pytest.raises(pa.PaError):
+        pa.linear(x, w[:40].contiguous())  # N not a multiple of 16
+    with pytest.raises(pa.PaError):
+        pa.linear(x.float(), w.float())  # f32
+    with pytest.raises(pa.PaError):
+        pa.linear(x, w, bias=b[:32].contiguous(), act=pa.ops.ACT_SILU_MUL)
+    empty = pa.linear(x[:0], w)
+    assert empty.shape == (0, 64)

@@ -20,6 +20,7 @@ from .ops import (
     reshape_and_cache_fp8,
     rope_inv_freq,
     layer_norm,
+    linear,
     rms_norm,
     rope_reshape_and_cache,
     silu_mul,
@@ -41,6 +42,7 @@ __all__ = [
     "reshape_and_cache_fp8",
     "rope_inv_freq",
     "layer_norm",
+    "linear",
     "rms_norm",
     "rope_reshape_and_cache",
     "silu_mul",

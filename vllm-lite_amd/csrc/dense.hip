@@ -1,6 +1,8 @@
 // Dense-side kernels of an end-to-end decoder step (pa_dense.h): residual
 // add + RMSNorm or LayerNorm, and the SwiGLU activation.  All are HBM-bound
 // row passes.
+#include <algorithm>
+
 #include "pa_common.hpp"
 #include "../../include/pa_dense.h"
 
@@ -99,6 +101,162 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(T* __restrict__ out,
   }
 }
 
+
+// Skinny-M linear layer (decode-step projections): Y[M, N] = X[M, K] · W[N, K]ᵀ
+// in bf16 with f32 accumulation, for M of a few tens of rows, where the
+// weights dominate the bytes (HBM-bound, ~M flops per weight byte).
+// v_mfma_f32_16x16x32_bf16 on Yᵀ tiles: A = 16 weight rows (lane: row c,
+// k 8j .. 8j+7, streamed from HBM; from the packed layout of
+// linear_pack_kernel every fragment is one contiguous KB), B = 16 batch rows
+// of X (same k slice, from L2), D = Yᵀ[weight row 4j + r][batch row c].
+// A wavefront computes NT x 16 weight rows x 32 batch rows over its share of
+// the K steps (32 each), loading the operands of the next stage of U steps
+// while it multiplies the current one; NT > 1 reuses each X fragment for NT
+// weight tiles.
+// The kw wavefronts of a workgroup (up to 16 for NT = 1 with U = 4, else 8)
+// split K and sum their partial tiles in LDS; wavefront 0 applies the
+// epilogue:
+//   EPI 0: none, EPI 1: + bias[n],
+//   EPI 2 (NT = 2): SwiGLU on a fused gate|up weight [2 I, K]: the two weight
+//          tiles are gate rows a0 + c and up rows I + a0 + c, and
+//          out[m][a] = silu(bf16(g)) * bf16(u) (the rounding of the unfused
+//          path, whose projection output is bf16).
+// Weight tiles of the last column block that lie past N (N a multiple of 16)
+// read row n0 and are not stored.
+template <int EPI, int NT, bool PK, int U>
+__global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ bias, int M, int N, int K, int kw) {
+  static_assert(EPI != 2 || NT == 2, "SwiGLU pairs one gate and one up tile");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, j = lane >> 4;
+  const int nsteps = K / 32;
+  const int s0 = wave * nsteps / kw, s1 = (wave + 1) * nsteps / kw;
+  const int m0 = blockIdx.y * 32;
+  const int n0 = blockIdx.x * (EPI == 2 ? 16 : 16 * NT);
+  // Weight fragment of tile t (16 rows from row r0) at step s:
+  //   row-major:  w + (r0 + c) * K + 32 s + 8 j
+  //   packed:     w + ((r0 / 16 * nsteps + s) * 64 + lane) * 8  (one contiguous KB)
+  const uint16_t* wp[NT];
+  bool tv[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    tv[t] = EPI == 2 || n0 + 16 * t < N;
+    const int64_t r0 = EPI == 2 ? (t == 0 ? n0 : (int64_t)N + n0) : (tv[t] ? n0 + 16 * t : n0);
+    wp[t] = PK ? w + (r0 / 16 * nsteps * 64 + lane) * 8 : w + (r0 + c) * K + 8 * j;
+  }
+  const uint16_t* xp0 = x + (int64_t)(m0 + c < M ? m0 + c : 0) * K + 8 * j;
+  const uint16_t* xp1 = x + (int64_t)(m0 + 16 + c < M ? m0 + 16 + c : 0) * K + 8 * j;
+  f32x4 acc[NT][2];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[t][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  bf16x8 a[2][U][NT], b[2][U][2];
+  // Loads are unconditional (a step past the wavefront's share reloads its
+  // last step, whose product is then skipped; a batch row past M reads row 0,
+  // whose output column is never stored), so the compiler can count them.
+  auto load = [&](int st, bf16x8 (&aa)[U][NT], bf16x8 (&bb)[U][2]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int step = min(st + u, s1 - 1);
+      const int k = step * 32;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        aa[u][t] = *reinterpret_cast<const bf16x8*>(wp[t] + (PK ? step * 512 : k));
+      bb[u][0] = *reinterpret_cast<const bf16x8*>(xp0 + k);
+      bb[u][1] = *reinterpret_cast<const bf16x8*>(xp1 + k);
+    }
+  };
+  auto mma = [&](int st, const bf16x8 (&aa)[U][NT], const bf16x8 (&bb)[U][2]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (st + u < s1) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aa[u][t], bb[u][q], acc[t][q], 0, 0, 0);
+      }
+    }
+  };
+  if (s0 < s1) load(s0, a[0], b[0]);
+  for (int s = s0; s < s1; s += 2 * U) {
+    if (s + U < s1) load(s + U, a[1], b[1]);
+    mma(s, a[0], b[0]);
+    if (s + U >= s1) break;
+    if (s + 2 * U < s1) load(s + 2 * U, a[0], b[0]);
+    mma(s + U, a[1], b[1]);
+  }
+
+  __shared__ f32x4 red[NT == 1 && U == 4 ? 15 : 7][2 * NT][64];
+  if (kw > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int q = 0; q < 2 * NT; ++q) red[wave - 1][q][lane] = acc[q >> 1][q & 1];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int v = 0; v < kw - 1; ++v)
+#pragma unroll
+      for (int q = 0; q < 2 * NT; ++q) acc[q >> 1][q & 1] += red[v][q][lane];
+  }
+#pragma unroll
+  for (int bb = 0; bb < 2; ++bb) {
+    const int m = m0 + 16 * bb + c;
+    if (m >= M) continue;
+    if constexpr (EPI == 2) {
+      uint16_t o4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][bb][r]));
+        const float u = bf16_bits_to_f32(f32_to_bf16_bits(acc[1][bb][r]));
+        o4[r] = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
+      }
+      *reinterpret_cast<uint64_t*>(out + (int64_t)m * N + n0 + 4 * j) =
+          *reinterpret_cast<const uint64_t*>(o4);
+    } else {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        if (!tv[t]) continue;
+        const int n = n0 + 16 * t + 4 * j;
+        uint16_t o4[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float y = acc[t][bb][r];
+          if constexpr (EPI == 1) y += bf16_bits_to_f32(bias[n + r]);
+          o4[r] = f32_to_bf16_bits(y);
+        }
+        *reinterpret_cast<uint64_t*>(out + (int64_t)m * N + n) = *reinterpret_cast<const uint64_t*>(o4);
+      }
+    }
+  }
+}
+
+// Packs a row-major bf16 weight [N, K] (N a multiple of 16, K of 32) into the
+// MFMA-fragment order linear_skinny_kernel<., ., true> reads: fragment
+// (tile, step) = rows 16 tile .. +15, columns 32 step .. +31 is 1 KB at
+// ((tile * K / 32 + step) * 64) * 8 elements, lane l = 16 j + c holding row
+// 16 tile + c, columns 32 step + 8 j .. +7.  One thread per 16-byte piece.
+__global__ __launch_bounds__(256) void linear_pack_kernel(uint16_t* __restrict__ dst,
+                                                          const uint16_t* __restrict__ src, int N,
+                                                          int K) {
+  const int64_t total = (int64_t)N * K / 8;
+  const int nsteps = K / 32;
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < total;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(q & 63);
+    const int64_t frag = q >> 6;
+    const int64_t tile = frag / nsteps;
+    const int step = (int)(frag % nsteps);
+    const int64_t row = tile * 16 + (lane & 15);
+    const int col = step * 32 + 8 * (lane >> 4);
+    *reinterpret_cast<uint4*>(dst + q * 8) = *reinterpret_cast<const uint4*>(src + row * K + col);
+  }
+}
+
 }  // namespace
 }  // namespace pa
 
@@ -160,4 +318,87 @@ extern "C" int32_t pa_silu_mul(void* out, const void* gate_up, int32_t rows, int
   else
     silu_mul_kernel<float><<<blocks, 256, 0, s>>>((float*)out, (const float*)gate_up, inter, n);
   return check_launch("pa_silu_mul");
+}
+
+extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const void* bias,
+                             int32_t rows, int32_t out_features, int32_t in_features, int32_t act,
+                             int32_t packed, int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype == PA_DTYPE_BF16, PA_ERR_UNSUPPORTED, "pa_linear: dtype %d (bf16 only)", dtype);
+  PA_REQUIRE(act == PA_ACT_NONE || act == PA_ACT_SILU_MUL, PA_ERR_INVALID_ARG,
+             "pa_linear: unknown activation %d", act);
+  PA_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0, PA_ERR_INVALID_ARG,
+             "pa_linear: bad sizes");
+  PA_REQUIRE(in_features % 32 == 0, PA_ERR_UNSUPPORTED,
+             "pa_linear: in_features %d not a multiple of 32", in_features);
+  PA_REQUIRE(out_features % 16 == 0, PA_ERR_UNSUPPORTED,
+             "pa_linear: out_features %d not a multiple of 16", out_features);
+  PA_REQUIRE(act == PA_ACT_NONE || !bias, PA_ERR_INVALID_ARG,
+             "pa_linear: bias with the SwiGLU epilogue");
+  if (rows == 0) return PA_OK;
+  PA_REQUIRE(out && x && weight, PA_ERR_INVALID_ARG, "pa_linear: null pointer");
+  PA_REQUIRE(((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out) % 16 == 0, PA_ERR_INVALID_ARG,
+             "pa_linear: x, weight and out must be 16-byte aligned");
+  PA_REQUIRE((rows + 31) / 32 <= 65535, PA_ERR_UNSUPPORTED, "pa_linear: %d rows", rows);
+  // Weight tiles per wavefront: 4 for wide outputs (each X fragment then
+  // feeds 4 tiles), 1 where 2 would leave fewer than ~512 wavefronts, else 2.
+  // K split: NT = 1 runs up to 16 wavefronts per workgroup, with one stage of
+  // 8 steps when K is short and stages of 4 otherwise; NT > 1 up to 8
+  // wavefronts of about 8 steps (two stages of 4).
+  const int nsteps = in_features / 32;
+  int kw = std::max(1, std::min(8, (nsteps + 7) / 8));
+  int nt = 2;
+  if (act != PA_ACT_SILU_MUL) {
+    if ((out_features + 63) / 64 >= 1024) nt = 4;
+    else if ((long long)((out_features + 31) / 32) * kw < 512) nt = 1;
+  }
+  int stage = 4;
+  if (nt == 1) {
+    if (nsteps <= 64) {
+      stage = 8;
+    } else {
+      kw = std::min(16, (nsteps + 7) / 8);
+    }
+  }
+  const int cols = act == PA_ACT_SILU_MUL ? 16 : 16 * nt;
+  const dim3 grid((out_features + cols - 1) / cols, (rows + 31) / 32);
+  hipStream_t s = (hipStream_t)stream;
+  auto* o = (uint16_t*)out;
+  auto* xx = (const uint16_t*)x;
+  auto* ww = (const uint16_t*)weight;
+  auto* bb = (const uint16_t*)bias;
+#define PA_LAUNCH_LINEAR_U(EPI, NT, UU)                                                       \
+  (packed ? linear_skinny_kernel<EPI, NT, true, UU><<<grid, 64 * kw, 0, s>>>(                  \
+                o, xx, ww, bb, rows, out_features, in_features, kw)                            \
+          : linear_skinny_kernel<EPI, NT, false, UU><<<grid, 64 * kw, 0, s>>>(                 \
+                o, xx, ww, bb, rows, out_features, in_features, kw))
+#define PA_LAUNCH_LINEAR(EPI, NT)                                                             \
+  (NT == 1 && stage == 8 ? PA_LAUNCH_LINEAR_U(EPI, 1, 8) : PA_LAUNCH_LINEAR_U(EPI, NT, 4))
+  if (act == PA_ACT_SILU_MUL)
+    PA_LAUNCH_LINEAR_U(2, 2, 4);
+  else if (bias)
+    nt == 4 ? PA_LAUNCH_LINEAR_U(1, 4, 4) : nt == 2 ? PA_LAUNCH_LINEAR_U(1, 2, 4) : PA_LAUNCH_LINEAR(1, 1);
+  else
+    nt == 4 ? PA_LAUNCH_LINEAR_U(0, 4, 4) : nt == 2 ? PA_LAUNCH_LINEAR_U(0, 2, 4) : PA_LAUNCH_LINEAR(0, 1);
+#undef PA_LAUNCH_LINEAR
+#undef PA_LAUNCH_LINEAR_U
+  return check_launch("pa_linear");
+}
+
+extern "C" int32_t pa_linear_pack(void* packed, const void* weight, int32_t rows, int32_t cols,
+                                  int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype == PA_DTYPE_BF16, PA_ERR_UNSUPPORTED, "pa_linear_pack: dtype %d (bf16 only)",
+             dtype);
+  PA_REQUIRE(rows > 0 && cols > 0 && rows % 16 == 0 && cols % 32 == 0, PA_ERR_UNSUPPORTED,
+             "pa_linear_pack: %d x %d (rows a multiple of 16, cols of 32)", rows, cols);
+  PA_REQUIRE(packed && weight && packed != weight, PA_ERR_INVALID_ARG,
+             "pa_linear_pack: null or aliased pointers");
+  PA_REQUIRE(((uintptr_t)packed | (uintptr_t)weight) % 16 == 0, PA_ERR_INVALID_ARG,
+             "pa_linear_pack: pointers must be 16-byte aligned");
+  const int64_t pieces = (int64_t)rows * cols / 8;
+  const int blocks = (int)std::min<int64_t>((pieces + 255) / 256, 65536);
+  linear_pack_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>((uint16_t*)packed,
+                                                              (const uint16_t*)weight, rows, cols);
+  return check_launch("pa_linear_pack");
 }

@@ -7,13 +7,20 @@ weights, run the way the reference's CausalLm runs it
 crates/model/src/components/decoder_block/mod.rs:157-198), but batched: one
 StepBatch per engine step, and per layer
     residual add + norm         pa_rms_norm | pa_layer_norm
-    QKV projection (+ bias)     hipBLASLt GEMM (torch.nn.functional.linear)
+    Q and K|V projections       two projections over row slices of the fused
+      (+ bias)                  QKV weight, so q comes out contiguous
     RoPE + KV write + attention StepBatch.attention (pa_batch_attention)
-    O projection                hipBLASLt GEMM
+    O projection
     residual add + norm         pa_rms_norm | pa_layer_norm
-    gate|up projection          hipBLASLt GEMM
-    SwiGLU                      pa_silu_mul
-    down projection             hipBLASLt GEMM
+    gate|up projection + SwiGLU pa_linear's fused epilogue (small batches) or
+                                a GEMM then pa_silu_mul
+    down projection
+Projections of batches of at most SKINNY_ROWS rows (decode steps, the LM head
+over the last tokens) run in pa_linear over weights repacked once at load
+time (pa_linear_pack: every MFMA operand fragment one contiguous kilobyte);
+larger batches (prefill chunks) and the long-K down projection, for which
+hipBLASLt's split-K GEMM is faster (9.5 vs 14.9 us measured), run in
+hipBLASLt (torch.nn.functional.linear).
 The norm is chosen explicitly by ModelConfig.norm: "rms" (RMSNorm, what the
 benchmark configuration states) or "layer" (the zero-bias LayerNorm the
 reference's CausalLm constructs for these models,
@@ -30,6 +37,10 @@ import torch.nn.functional as F
 
 from . import ops
 from .kv_cache import PagedKvCache, StepBatch
+
+
+SKINNY_ROWS = 64
+SKINNY_MAX_K = 1024  # in_features above this stay on hipBLASLt
 
 
 @dataclasses.dataclass
@@ -70,6 +81,23 @@ class Weights:
         self.wgu = [w(2 * cfg.inter, h) for _ in range(cfg.layers)]
         self.wd = [w(h, cfg.inter) for _ in range(cfg.layers)]
         self.norm = torch.ones(h, dtype=dtype, device=device)
+        self.packed = None
+
+    def pack(self):
+        """Repacks the weights pa_linear reads (QKV as separate Q and K|V row
+        blocks, O, gate|up, the tied embedding as LM head) into its fragment
+        layout; the row-major tensors stay for the hipBLASLt path."""
+        def fits(wt):  # shapes pa_linear_pack takes
+            return wt.shape[0] % 16 == 0 and wt.shape[1] % 32 == 0
+
+        nq = self.wo[0].shape[1]
+        blocks = {"q": [x[:nq] for x in self.wqkv], "kv": [x[nq:] for x in self.wqkv],
+                  "o": self.wo, "gu": self.wgu}
+        p = {name: [ops.PackedWeight(x) for x in ws]
+             for name, ws in blocks.items() if all(fits(x) for x in ws)}
+        if fits(self.embed):
+            p["lm_head"] = ops.PackedWeight(self.embed)
+        self.packed = p
 
     def nbytes(self):
         ts = [self.embed, self.norm]
@@ -104,22 +132,44 @@ class Engine:
         c, w = self.cfg, self.w
         t = tokens.shape[0]
         hq, hkv, d = c.heads, c.kv_heads, c.head_dim
+        skinny = t <= SKINNY_ROWS
+
+        def linear(inp, weight, bias=None, packed=None):
+            if skinny and ops.linear_supports(inp, weight) and inp.shape[1] <= SKINNY_MAX_K:
+                return ops.linear(inp, packed if packed is not None else weight, bias)
+            return F.linear(inp, weight, bias)
+
+        pk = w.packed or {}
+
+        def packed(name, layer):
+            return pk[name][layer] if name in pk else None
+
         x = F.embedding(tokens, w.embed)          # residual stream [T, hidden]
         h = torch.empty_like(x)
         add = None
+        nq = hq * d
         for layer in range(c.layers):
             self._norm(x, w.ln1[layer], c.eps, add=add, out=h)
-            qkv = F.linear(h, w.wqkv[layer], w.bqkv[layer])
-            q = qkv[:, :hq * d].contiguous().view(t, hq, d)  # the kernels take dense q rows
-            k = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
-            v = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+            wqkv, bqkv = w.wqkv[layer], w.bqkv[layer]
+            # the kernels take dense q rows
+            q = linear(h, wqkv[:nq], bqkv[:nq], packed("q", layer)).view(t, hq, d)
+            kv = linear(h, wqkv[nq:], bqkv[nq:], packed("kv", layer))
+            k = kv[:, :hkv * d].view(t, hkv, d)
+            v = kv[:, hkv * d:].view(t, hkv, d)
             attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq, self.scale)
-            o = F.linear(attn.view(t, hq * d), w.wo[layer])
+            o = linear(attn.view(t, nq), w.wo[layer], packed=packed("o", layer))
             self._norm(x, w.ln2[layer], c.eps, add=o, out=h)
-            act = ops.silu_mul(F.linear(h, w.wgu[layer]))
-            add = F.linear(act, w.wd[layer])
+            if skinny and ops.linear_supports(h, w.wgu[layer]) and c.hidden <= SKINNY_MAX_K:
+                gu = packed("gu", layer)
+                act = ops.linear(h, gu if gu is not None else w.wgu[layer], act=ops.ACT_SILU_MUL)
+            else:
+                act = ops.silu_mul(F.linear(h, w.wgu[layer]))
+            add = linear(act, w.wd[layer])
         self._norm(x, w.norm, c.eps, add=add, out=h)
-        return F.linear(h[logit_rows], w.embed).float()
+        rows = h[logit_rows]
+        if rows.shape[0] <= SKINNY_ROWS and ops.linear_supports(rows, w.embed):
+            return ops.linear(rows, pk.get("lm_head", w.embed)).float()
+        return F.linear(rows, w.embed).float()
 
     def generate(self, prompts, max_new):
         """Greedy generation for every prompt (lists of token ids).  Returns

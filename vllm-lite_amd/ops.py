@@ -336,3 +336,54 @@ def silu_mul(gate_up, out=None):
     _check("pa_silu_mul", lib.pa_silu_mul(_ptr(out), _ptr(gate_up), rows, inter,
                                           _dtype_code(gate_up), _stream(gate_up)))
     return out
+
+
+ACT_NONE, ACT_SILU_MUL = 0, 1
+
+
+def linear_supports(x, weight):
+    """Whether pa_linear takes these operands (bf16, K a multiple of 32, N a
+    multiple of 16; the fused gate|up weight has an even number of 16-row
+    halves whenever its N is a multiple of 32)."""
+    return (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and
+            x.shape[-1] % 32 == 0 and weight.shape[0] % 16 == 0)
+
+
+class PackedWeight:
+    """A bf16 weight [N, K] repacked by pa_linear_pack (see pa_dense.h); pass
+    it to linear() in place of the row-major tensor."""
+
+    def __init__(self, weight):
+        _dev(weight)
+        if not weight.is_contiguous():
+            raise ValueError("pa_linear_pack takes a contiguous weight")
+        self.shape = tuple(weight.shape)
+        self.dtype = weight.dtype
+        self.data = torch.empty_like(weight)
+        _check("pa_linear_pack", _lib.load().pa_linear_pack(
+            _ptr(self.data), _ptr(weight), weight.shape[0], weight.shape[1],
+            _dtype_code(weight), _stream(weight)))
+
+
+def linear(x, weight, bias=None, act=ACT_NONE, out=None):
+    """pa_linear: x [rows, K] bf16, weight [N, K] (or the fused gate|up
+    [2 N, K] with act=ACT_SILU_MUL), row-major or a PackedWeight -> out
+    [rows, N] bf16."""
+    packed = isinstance(weight, PackedWeight)
+    wt = weight.data if packed else weight
+    _dev(x, wt)
+    rows, k = x.shape
+    n = weight.shape[0] // (2 if act == ACT_SILU_MUL else 1)
+    if weight.shape[1] != k:
+        raise ValueError(f"weight {tuple(weight.shape)} does not match x {tuple(x.shape)}")
+    if not (x.is_contiguous() and wt.is_contiguous()):
+        raise ValueError("pa_linear takes contiguous x and weight")
+    if bias is not None and (bias.shape != (n,) or not bias.is_contiguous()):
+        raise ValueError(f"bias {tuple(bias.shape)} does not match {n} outputs")
+    if out is None:
+        out = torch.empty(rows, n, dtype=x.dtype, device=x.device)
+    lib = _lib.load()
+    _check("pa_linear", lib.pa_linear(_ptr(out), _ptr(x), _ptr(wt),
+                                      _ptr(bias) if bias is not None else None, rows, n, k, act,
+                                      1 if packed else 0, _dtype_code(x), _stream(x)))
+    return out
