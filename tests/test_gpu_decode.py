@@ -79,6 +79,24 @@ def test_config2_full_batch_long_partitions(pa, oracle):
     assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "config 2 full")
 
 
+@pytest.mark.parametrize("b,hkv,ctx_max,waves", [(32, 2, 760, 8), (2, 8, 1024, 8),
+                                                 (32, 8, 900, 4), (16, 8, 1500, 1)])
+def test_partitions_merged_in_workgroup(pa, oracle, b, hkv, ctx_max, waves):
+    # decode launches whose partitions one workgroup merges in LDS: 128-token
+    # partitions, up to 8 (small batches, contexts <= 1024: the engine's
+    # decode step), 256-token partitions, up to 4; and more than 8 partitions
+    # (the reduce kernel), all with ragged contexts including 1 and 128 / 129
+    rng = np.random.default_rng(b * hkv + ctx_max)
+    ctx = rng.integers(1, ctx_max + 1, size=b)
+    ctx[0], ctx[1] = ctx_max, 1
+    if b > 3:
+        ctx[2], ctx[3] = 128, 129
+    case = make_decode_case(rng, b, 4 * hkv, hkv, 128 if hkv == 8 else 64, ctx, dtype="bf16",
+                            kv_scale=0.5)
+    got, _ = run_decode(pa, oracle, case, "bf16")
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, f"merge {waves}")
+
+
 def test_long_ragged_contexts_512_partitions(pa, oracle):
     # contexts past 8k with enough work items: 512-token partitions
     rng = np.random.default_rng(12)

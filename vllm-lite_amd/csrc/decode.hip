@@ -802,11 +802,15 @@ int num_partitions(int max_ctx, int part_len) {
 // and ragged contexts with 512-token partitions (several wavefronts per
 // SIMD balance the uneven lengths); small batches need short partitions to
 // fill the GPU at all.
-int choose_partition(int num_seqs, int num_kv_heads, int max_ctx) {
+// Small batches of short contexts (fewer than 512 items at 256 tokens, at
+// most 1024 tokens) take 128-token partitions, up to 8 per (kv head,
+// sequence), which one workgroup merges in LDS.
+int choose_partition(int num_seqs, int num_kv_heads, int max_ctx, int head_dim) {
   const long long units = (long long)num_seqs * num_kv_heads;
   auto items = [&](int p) { return units * ((max_ctx + p - 1) / p); };
   if (max_ctx <= 8192 && items(2048) >= 1024) return 2048;
   if (items(512) >= 1024) return 512;
+  if (items(kPart) < 512 && max_ctx <= 1024 && head_dim <= 128) return kPart / 2;
   return kPart;
 }
 
@@ -853,13 +857,19 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   // and groups of at most kF32MaxG heads, the generic kernel otherwise
   const bool f32_group = dtype == PA_DTYPE_F32 && G <= kF32MaxG && head_dim <= 256 &&
                          256 % head_dim == 0 && head_dim % 16 == 0;
-  const int part_len = mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len) : kPart;
+  const int part_len =
+      mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len, head_dim) : kPart;
   const int np = num_partitions(max_context_len, part_len);
   PA_REQUIRE(np <= 1024, PA_ERR_UNSUPPORTED,
              "pa_decode: context of %d tokens needs %d > 1024 partitions", max_context_len, np);
-  // MFMA kernels: up to 4 partitions are taken by one workgroup (one
-  // wavefront each) and merged in LDS, with no workspace and no reduce launch.
-  const int merge_waves = (mfma && np > 1 && np <= 4) ? (np == 2 ? 2 : 4) : 1;
+  // MFMA kernels: up to 4 partitions (8 for head_dim <= 128) are taken by one
+  // workgroup (one wavefront each) and merged in LDS, with no workspace and no
+  // reduce launch.
+  const int merge_waves = !mfma || np <= 1 ? 1
+                          : np == 2         ? 2
+                          : np <= 4         ? 4
+                          : (np <= 8 && head_dim <= 128) ? 8
+                                                         : 1;
   float* ws_o = nullptr;
   float* ws_ml = nullptr;
   if (np > 1 && merge_waves == 1) {
@@ -886,6 +896,8 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
       PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 2);                                                   \
     else if (merge_waves == 4)                                                                \
       PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 4);                                                   \
+    else if (merge_waves == 8)                                                                \
+      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, (DD <= 128 ? 8 : 4));                                 \
     else                                                                                      \
       PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 1);                                                   \
   } while (0)
