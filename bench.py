@@ -447,7 +447,6 @@ def main():
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(args.config),
-                "kernel": "pa_decode (decode_mfma_kernel + decode_reduce_kernel)",
                 "alg_bytes_per_launch": w.alg_bytes,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
         if t_flush:
@@ -455,10 +454,15 @@ def main():
             roof["flushed_frac"] = round(w.alg_bytes / t_flush / 1e9 / HBM_PEAK_GBS, 4)
         if args.config == "splitk":
             roof["unique_block_gbs"] = round((w.unique_kv_bytes) / t_attn / 1e9, 1)
-        if w.dtype == torch.float32:
-            roof["kernel"] = "pa_decode (decode_generic_kernel + decode_reduce_kernel)"
-        if w.fp8:
-            roof["kernel"] = "pa_decode (decode_fp8_kernel + decode_reduce_kernel)"
+        # configs 2 (bf16, FP8): two 2048-token partitions per (kv head,
+        # sequence), merged in the workgroup; config 4: 512-token partitions and
+        # the reduce kernel; config 1 (f32): the group kernel and the reduce kernel
+        roof["kernel"] = {
+            "decode": "pa_decode (decode_mfma_kernel, partitions merged in the workgroup)",
+            "decode-fp8": "pa_decode (decode_fp8_kernel, partitions merged in the workgroup)",
+            "splitk": "pa_decode (decode_mfma_kernel + decode_reduce_kernel)",
+            "qwen": "pa_decode (decode_f32_group_kernel + decode_reduce_kernel)",
+        }[args.config]
     else:
         value = w.flops / t_attn / 1e12
         unit = "TFLOP/s"
