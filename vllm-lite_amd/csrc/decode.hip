@@ -380,43 +380,64 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
   const bool v_second = (j >> 1) != 0;              // this lane's P·V tokens are in block 1
   const int tv0 = 8 * (j & 1);
 
-  for (int ib = 0; ib < nblk; ib += 2) {
-    int32_t b0 = btab[ib];
+  // One step = two blocks; its raw K/V bytes and the blocks' valid lengths.
+  // Steps are software-pipelined two deep (the bytes of step n + 1 are
+  // requested before step n is computed): an FP8 step moves half the bytes of
+  // a bf16 step, so one step in flight per wavefront would leave HBM
+  // latency-bound.
+  struct Step {
+    u32x4 k0[KS / 2], k1[KS / 2];  // 16 bytes = two reduction steps, token tk0 / tk0 + 4
+    uint64_t v[DT];
+    int lim0, lim1;
+  };
+  // Block ids through the scalar cache with a wait on the scalar counter only.
+  // (Written out because the register-only asm below keeps the compiler from
+  // proving the table unmodified; it would then read it with vector loads,
+  // each followed by vmcnt(0), draining the K/V loads in flight.)
+  auto table_id = [&](int idx) -> int32_t {
+    int32_t v;
+    asm volatile("s_load_dword %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+                 : "=s"(v)
+                 : "s"(btab), "s"(idx * 4));
+    return v;
+  };
+  auto load_step = [&](int ib, Step& st) {
+    int32_t b0 = table_id(ib);
     const bool has1 = ib + 1 < nblk;
-    int32_t b1 = has1 ? btab[ib + 1] : b0;
+    int32_t b1 = table_id(has1 ? ib + 1 : ib);
     const int rem = tok_end - (tok0 + ib * kBlock);
-    int lim0 = rem < kBlock ? rem : kBlock;
-    int lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
-    if (b0 < 0 || b0 >= num_blocks) { b0 = 0; lim0 = 0; }
-    if (b1 < 0 || b1 >= num_blocks) { b1 = 0; lim1 = 0; }
-
+    st.lim0 = rem < kBlock ? rem : kBlock;
+    st.lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
+    if (b0 < 0 || b0 >= num_blocks) { b0 = 0; st.lim0 = 0; }
+    if (b1 < 0 || b1 >= num_blocks) { b1 = 0; st.lim1 = 0; }
     const uint8_t* kr =
         kc + ((int64_t)(k_second ? b1 : b0) * Hkv + kvh) * head_stride + tk0 * D + DL * j;
-    uint2 kw0[KS], kw1[KS];  // 8 bytes per reduction step, token tk0 / tk0 + 4
-#pragma unroll
-    for (int s = 0; s < KS; s += 2) {
-      const uint4 x0 = *reinterpret_cast<const uint4*>(kr + 8 * s);
-      const uint4 x1 = *reinterpret_cast<const uint4*>(kr + 4 * D + 8 * s);
-      kw0[s] = uint2{x0.x, x0.y};
-      kw0[s + 1] = uint2{x0.z, x0.w};
-      kw1[s] = uint2{x1.x, x1.y};
-      kw1[s + 1] = uint2{x1.z, x1.w};
-    }
     const uint8_t* vr =
         vc + ((int64_t)(v_second ? b1 : b0) * Hkv + kvh) * head_stride + c * kBlock + tv0;
-    uint64_t vw[DT];
+    // Non-temporal, unconditionally: a branch between load kinds makes the
+    // compiler's wait counts conservative (vmcnt(0) before the first use),
+    // which drains the pipeline.
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) vw[dt] = *reinterpret_cast<const uint64_t*>(vr + dt * 16 * kBlock);
-
+    for (int s = 0; s < KS / 2; ++s) {
+      st.k0[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kr + 16 * s));
+      st.k1[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kr + 4 * D + 16 * s));
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      st.v[dt] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(vr + dt * 16 * kBlock));
+  };
+  auto compute = [&](Step& st) {
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(kw0[s].x, kw0[s].y), qv[s], s0,
-                                                   0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(kw1[s].x, kw1[s].y), qv[s], s1,
-                                                   0, 0, 0);
+      const u32x4& w0 = st.k0[s / 2];
+      const u32x4& w1 = st.k1[s / 2];
+      const int h = 2 * (s & 1);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(w0[h], w0[h + 1]), qv[s], s0, 0,
+                                                   0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(w1[h], w1[h + 1]), qv[s], s1, 0,
+                                                   0, 0);
     }
-
     // x[i] <-> token tv0 + i of this lane's block (s0: i < 4, s1: i >= 4)
     float x[8];
 #pragma unroll
@@ -424,8 +445,8 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
       x[r] = s0[r] * scale_log2;
       x[4 + r] = s1[r] * scale_log2;
     }
-    if (lim0 < kBlock || lim1 < kBlock) {  // wave-uniform
-      const int lim = v_second ? lim1 : lim0;
+    if (st.lim0 < kBlock || st.lim1 < kBlock) {  // wave-uniform
+      const int lim = v_second ? st.lim1 : st.lim0;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (tv0 + i >= lim) x[i] = -INFINITY;
@@ -434,7 +455,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
       const int n = min(max(lim - tv0, 0), 8);
       const uint64_t mk = n >= 8 ? ~0ull : ((1ull << (8 * n)) - 1);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) vw[dt] &= mk;
+      for (int dt = 0; dt < DT; ++dt) st.v[dt] &= mk;
     }
 
     float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
@@ -461,7 +482,22 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          fp8x8_to_bf16((uint32_t)vw[dt], (uint32_t)(vw[dt] >> 32)), pb, o[dt], 0, 0, 0);
+          fp8x8_to_bf16((uint32_t)st.v[dt], (uint32_t)(st.v[dt] >> 32)), pb, o[dt], 0, 0, 0);
+  };
+
+  // The q loads complete here, once: a wait for them that the compiler placed
+  // inside the loop would be vmcnt(0) on every iteration and drain the
+  // pipeline.
+#pragma unroll
+  for (int s = 0; s < KS; ++s) asm volatile("" ::"v"(qv[s]));
+  Step sa, sb;
+  if (nblk > 0) load_step(0, sa);
+  for (int ib = 0; ib < nblk; ib += 4) {
+    if (ib + 2 < nblk) load_step(ib + 2, sb);
+    compute(sa);
+    if (ib + 2 >= nblk) break;
+    if (ib + 4 < nblk) load_step(ib + 4, sa);
+    compute(sb);
   }
 
   lsum += shfl_xor_f(lsum, 16);
