@@ -44,8 +44,9 @@ int32_t pa_layer_norm(void* out, void* residual, const void* add, const void* we
 int32_t pa_silu_mul(void* out, const void* gate_up, int32_t rows, int32_t inter, int32_t dtype,
                     pa_stream_t stream);
 
-/* Activation epilogues of pa_linear. */
+/* Activation epilogues and flags of pa_linear. */
 enum { PA_ACT_NONE = 0, PA_ACT_SILU_MUL = 1 };
+enum { PA_LINEAR_RMS_IN = 1, PA_LINEAR_ADD_OUT = 2 };
 
 /* The decoder's linear projections for the few-row batches of a decode step
  * (candle_nn::Linear as the reference's attention and MLP use it: the QKV
@@ -61,20 +62,32 @@ enum { PA_ACT_NONE = 0, PA_ACT_SILU_MUL = 1 };
  * 16-byte aligned, bias [N] or NULL; K (in_features) a multiple of 32, N
  * (out_features) a multiple of 16.  f32 accumulation.
  * packed = 1: weight is in the layout of pa_linear_pack (rows N or 2 N).
+ * flags (0 or a combination):
+ *   PA_LINEAR_RMS_IN   the rows of x are RMS-normalised on the fly: the result
+ *                      is multiplied by 1 / sqrt(mean_k(x[r][k]^2) + eps) (the
+ *                      decoder's RMSNorm, crates/model/src/components/norm/
+ *                      rms_norm.rs:26-50, in front of the projection); the
+ *                      norm weight is folded into the weight's columns by
+ *                      pa_linear_pack's col_scale;
+ *   PA_LINEAR_ADD_OUT  out is the residual stream and is updated in place,
+ *                      out[r][n] = bf16(out[r][n] + bf16(y[r][n])) (the
+ *                      decoder block's residual add); not with SwiGLU.
  * Built for rows <= 64, where the weights dominate the traffic; the weights
  * are re-read once per 32 rows.  bf16 only (PA_ERR_UNSUPPORTED otherwise). */
 int32_t pa_linear(void* out, const void* x, const void* weight, const void* bias, int32_t rows,
                   int32_t out_features, int32_t in_features, int32_t act, int32_t packed,
-                  int32_t dtype, pa_stream_t stream);
+                  int32_t flags, float eps, int32_t dtype, pa_stream_t stream);
 
 /* Repacks a row-major bf16 weight [rows, cols] (rows a multiple of 16, cols
  * of 32) into the fragment order pa_linear reads with packed = 1: every
  * 16-row x 32-column MFMA operand fragment becomes one contiguous kilobyte,
- * the fragments of a 16-row tile consecutive along the columns.  Same size as
- * the input; packed and weight must not overlap.  No reference counterpart:
- * a load-time layout step for the weights pa_linear streams. */
-int32_t pa_linear_pack(void* packed, const void* weight, int32_t rows, int32_t cols,
-                       int32_t dtype, pa_stream_t stream);
+ * the fragments of a 16-row tile consecutive along the columns.  col_scale
+ * [cols] (bf16) or NULL: each column is multiplied by it (rounded to bf16),
+ * which folds a norm weight in front of the projection.  Same size as the
+ * input; packed and weight must not overlap.  No reference counterpart: a
+ * load-time layout step for the weights pa_linear streams. */
+int32_t pa_linear_pack(void* packed, const void* weight, const void* col_scale, int32_t rows,
+                       int32_t cols, int32_t dtype, pa_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -110,14 +110,17 @@ def ref_logits(cfg, w, tokens, inv_freq):
     return norm(x, w.norm) @ f(w.embed).T
 
 
-@pytest.mark.parametrize("norm,packed", [("rms", False), ("rms", True), ("layer", True)])
+@pytest.mark.parametrize("norm,packed", [("rms", False), ("rms", "plain"), ("rms", True),
+                                         ("layer", True)])
 def test_engine_matches_fp32_forward(pa, norm, packed):
     from vllm_lite_amd import e2e
     cfg = e2e.ModelConfig(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=32, inter=512,
                           vocab=1008, rope_theta=1e4, norm=norm)
     w = e2e.Weights(cfg, seed=7, device=DEV)
     if packed:
-        w.pack()  # pa_linear over packed weights, LM head included (1008 rows)
+        # pa_linear over packed weights, LM head included (1008 rows); True:
+        # norms folded into the projections (the fused decode step for RMSNorm)
+        w.pack(fold_rms=packed is True)
     eng = e2e.Engine(cfg, w, num_blocks=64, device=DEV)
     rng = np.random.default_rng(0)
     prompts = [list(rng.integers(0, cfg.vocab, n)) for n in (5, 20, 33)]

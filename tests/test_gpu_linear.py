@@ -82,3 +82,51 @@ def test_linear_rejects_unsupported(pa):
         pa.linear(x, w, bias=b[:32].contiguous(), act=pa.ops.ACT_SILU_MUL)
     empty = pa.linear(x[:0], w)
     assert empty.shape == (0, 64)
+
+
+def rms_ref(x, gamma, eps):
+    xf = x.float()
+    return xf / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * gamma.float()
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 896, 896), (5, 256, 896), (40, 64, 4864)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_linear_rms_in_matches_norm_then_matmul(pa, m, n, k, with_bias):
+    # PA_LINEAR_RMS_IN with the norm weight folded into the packed columns ==
+    # RMSNorm then the projection (fp32 reference)
+    x, w, b = operands(m, n, k, m + 3 * n + k)
+    x = (x.float() * 3 + 0.5).to(torch.bfloat16)
+    g = torch.Generator(device=DEV).manual_seed(k)
+    gamma = (1 + 0.2 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    out = pa.linear(x, pa.ops.PackedWeight(w, col_scale=gamma), bias=b if with_bias else None,
+                    rms_eps=1e-6)
+    ref = rms_ref(x, gamma, 1e-6) @ w.float().T
+    if with_bias:
+        ref = ref + b.float()
+    close(out, ref)
+
+
+def test_linear_rms_in_swiglu(pa):
+    m, inter, k = 32, 4864, 896
+    x, w, _ = operands(m, 2 * inter, k, 11, wscale=0.05)
+    gamma = torch.full((k,), 0.75, dtype=torch.bfloat16, device=DEV)
+    out = pa.linear(x, pa.ops.PackedWeight(w, col_scale=gamma), act=pa.ops.ACT_SILU_MUL,
+                    rms_eps=1e-6)
+    gu = (rms_ref(x, gamma, 1e-6) @ w.float().T).to(torch.bfloat16).float()
+    # g and u are rounded to bf16 on both sides (as the unfused path does), from
+    # different accumulation orders and a norm-scaled weight: either may land one
+    # bf16 ulp (2^-8 relative) apart, which silu(g) * u carries twice
+    torch.testing.assert_close(out.float(), F.silu(gu[:, :inter]) * gu[:, inter:], atol=2e-2,
+                               rtol=3e-2)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_linear_adds_into_residual(pa, packed):
+    m, n, k = 33, 896, 896
+    x, w, _ = operands(m, n, k, 13)
+    res = (torch.randn(m, n, device=DEV) * 2).to(torch.bfloat16)
+    expect = (res.float() + (x.float() @ w.float().T).to(torch.bfloat16).float())
+    out = res.clone()
+    got = pa.linear(x, pa.ops.PackedWeight(w) if packed else w, out=out, add_to_out=True)
+    assert got.data_ptr() == out.data_ptr()
+    close(out, expect)

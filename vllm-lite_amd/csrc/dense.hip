@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(T* __restrict__ out,
 template <int EPI, int NT, bool PK, int U>
 __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const uint16_t* __restrict__ bias, int M, int N, int K, int kw) {
+    const uint16_t* __restrict__ bias, int M, int N, int K, int kw, int flags, float eps) {
   static_assert(EPI != 2 || NT == 2, "SwiGLU pairs one gate and one up tile");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -153,6 +153,10 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int b = 0; b < 2; ++b) acc[t][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // PA_LINEAR_RMS_IN: per-lane sums of squares of the X fragments (batch rows
+  // c and 16 + c, this lane's 8 columns of each step)
+  const bool rms = (flags & PA_LINEAR_RMS_IN) != 0;
+  float ss[2] = {0.f, 0.f};
 
   bf16x8 a[2][U][NT], b[2][U][2];
   // Loads are unconditional (a step past the wavefront's share reloads its
@@ -179,6 +183,15 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
 #pragma unroll
           for (int q = 0; q < 2; ++q)
             acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aa[u][t], bb[u][q], acc[t][q], 0, 0, 0);
+        if (rms) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float v = (float)bb[u][q][i];
+              ss[q] += v * v;
+            }
+        }
       }
     }
   };
@@ -191,7 +204,21 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
     mma(s + U, a[1], b[1]);
   }
 
-  __shared__ f32x4 red[NT == 1 && U == 4 ? 15 : 7][2 * NT][64];
+  constexpr int MAXW = NT == 1 && U == 4 ? 16 : 8;
+  __shared__ f32x4 red[MAXW - 1][2 * NT][64];
+  __shared__ float rss[MAXW][2][16];
+  if (rms) {
+    // a batch row's columns are spread over the 4 lanes j of its c
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      ss[q] += __shfl_xor(ss[q], 16, 64);
+      ss[q] += __shfl_xor(ss[q], 32, 64);
+    }
+    if (j == 0) {
+      rss[wave][0][c] = ss[0];
+      rss[wave][1][c] = ss[1];
+    }
+  }
   if (kw > 1) {
     if (wave > 0) {
 #pragma unroll
@@ -202,7 +229,21 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
     for (int v = 0; v < kw - 1; ++v)
 #pragma unroll
       for (int q = 0; q < 2 * NT; ++q) acc[q >> 1][q & 1] += red[v][q][lane];
+  } else if (rms) {
+    __syncthreads();
   }
+  // 1 / rms of the batch rows (1 without PA_LINEAR_RMS_IN); the norm weight
+  // is folded into the packed weight's columns
+  float inv[2] = {1.f, 1.f};
+  if (rms) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      float t = 0.f;
+      for (int v = 0; v < kw; ++v) t += rss[v][q][c];
+      inv[q] = 1.0f / sqrtf(t / (float)K + eps);
+    }
+  }
+  const bool add_out = (flags & PA_LINEAR_ADD_OUT) != 0;
 #pragma unroll
   for (int bb = 0; bb < 2; ++bb) {
     const int m = m0 + 16 * bb + c;
@@ -211,8 +252,8 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
       uint16_t o4[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][bb][r]));
-        const float u = bf16_bits_to_f32(f32_to_bf16_bits(acc[1][bb][r]));
+        const float g = bf16_bits_to_f32(f32_to_bf16_bits(acc[0][bb][r] * inv[bb]));
+        const float u = bf16_bits_to_f32(f32_to_bf16_bits(acc[1][bb][r] * inv[bb]));
         o4[r] = f32_to_bf16_bits(g / (1.0f + expf(-g)) * u);
       }
       *reinterpret_cast<uint64_t*>(out + (int64_t)m * N + n0 + 4 * j) =
@@ -222,14 +263,20 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
       for (int t = 0; t < NT; ++t) {
         if (!tv[t]) continue;
         const int n = n0 + 16 * t + 4 * j;
+        uint64_t* dst = reinterpret_cast<uint64_t*>(out + (int64_t)m * N + n);
+        uint16_t prev[4];
+        if (add_out) *reinterpret_cast<uint64_t*>(prev) = *dst;
         uint16_t o4[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float y = acc[t][bb][r];
+          float y = acc[t][bb][r] * inv[bb];
           if constexpr (EPI == 1) y += bf16_bits_to_f32(bias[n + r]);
+          // residual add: the projection output rounded to bf16 first, as
+          // when it is materialised and added by the norm kernel
+          if (add_out) y = bf16_bits_to_f32(prev[r]) + bf16_bits_to_f32(f32_to_bf16_bits(y));
           o4[r] = f32_to_bf16_bits(y);
         }
-        *reinterpret_cast<uint64_t*>(out + (int64_t)m * N + n) = *reinterpret_cast<const uint64_t*>(o4);
+        *dst = *reinterpret_cast<const uint64_t*>(o4);
       }
     }
   }
@@ -239,10 +286,12 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
 // MFMA-fragment order linear_skinny_kernel<., ., true> reads: fragment
 // (tile, step) = rows 16 tile .. +15, columns 32 step .. +31 is 1 KB at
 // ((tile * K / 32 + step) * 64) * 8 elements, lane l = 16 j + c holding row
-// 16 tile + c, columns 32 step + 8 j .. +7.  One thread per 16-byte piece.
+// 16 tile + c, columns 32 step + 8 j .. +7, optionally times col_scale[col]
+// (rounded to bf16).  One thread per 16-byte piece.
 __global__ __launch_bounds__(256) void linear_pack_kernel(uint16_t* __restrict__ dst,
-                                                          const uint16_t* __restrict__ src, int N,
-                                                          int K) {
+                                                          const uint16_t* __restrict__ src,
+                                                          const uint16_t* __restrict__ col_scale,
+                                                          int N, int K) {
   const int64_t total = (int64_t)N * K / 8;
   const int nsteps = K / 32;
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < total;
@@ -253,7 +302,14 @@ __global__ __launch_bounds__(256) void linear_pack_kernel(uint16_t* __restrict__
     const int step = (int)(frag % nsteps);
     const int64_t row = tile * 16 + (lane & 15);
     const int col = step * 32 + 8 * (lane >> 4);
-    *reinterpret_cast<uint4*>(dst + q * 8) = *reinterpret_cast<const uint4*>(src + row * K + col);
+    uint4 v = *reinterpret_cast<const uint4*>(src + row * K + col);
+    if (col_scale) {
+      uint16_t* e = reinterpret_cast<uint16_t*>(&v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        e[i] = f32_to_bf16_bits(bf16_bits_to_f32(e[i]) * bf16_bits_to_f32(col_scale[col + i]));
+    }
+    *reinterpret_cast<uint4*>(dst + q * 8) = v;
   }
 }
 
@@ -322,7 +378,8 @@ extern "C" int32_t pa_silu_mul(void* out, const void* gate_up, int32_t rows, int
 
 extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const void* bias,
                              int32_t rows, int32_t out_features, int32_t in_features, int32_t act,
-                             int32_t packed, int32_t dtype, pa_stream_t stream) {
+                             int32_t packed, int32_t flags, float eps, int32_t dtype,
+                             pa_stream_t stream) {
   clear_error();
   PA_REQUIRE(dtype == PA_DTYPE_BF16, PA_ERR_UNSUPPORTED, "pa_linear: dtype %d (bf16 only)", dtype);
   PA_REQUIRE(act == PA_ACT_NONE || act == PA_ACT_SILU_MUL, PA_ERR_INVALID_ARG,
@@ -335,6 +392,12 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
              "pa_linear: out_features %d not a multiple of 16", out_features);
   PA_REQUIRE(act == PA_ACT_NONE || !bias, PA_ERR_INVALID_ARG,
              "pa_linear: bias with the SwiGLU epilogue");
+  PA_REQUIRE((flags & ~(PA_LINEAR_RMS_IN | PA_LINEAR_ADD_OUT)) == 0, PA_ERR_INVALID_ARG,
+             "pa_linear: unknown flags %d", flags);
+  PA_REQUIRE(!(flags & PA_LINEAR_ADD_OUT) || act == PA_ACT_NONE, PA_ERR_INVALID_ARG,
+             "pa_linear: residual add with the SwiGLU epilogue");
+  PA_REQUIRE(!(flags & PA_LINEAR_RMS_IN) || eps > 0.f, PA_ERR_INVALID_ARG,
+             "pa_linear: eps must be positive");
   if (rows == 0) return PA_OK;
   PA_REQUIRE(out && x && weight, PA_ERR_INVALID_ARG, "pa_linear: null pointer");
   PA_REQUIRE(((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out) % 16 == 0, PA_ERR_INVALID_ARG,
@@ -369,9 +432,9 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   auto* bb = (const uint16_t*)bias;
 #define PA_LAUNCH_LINEAR_U(EPI, NT, UU)                                                       \
   (packed ? linear_skinny_kernel<EPI, NT, true, UU><<<grid, 64 * kw, 0, s>>>(                  \
-                o, xx, ww, bb, rows, out_features, in_features, kw)                            \
+                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps)               \
           : linear_skinny_kernel<EPI, NT, false, UU><<<grid, 64 * kw, 0, s>>>(                 \
-                o, xx, ww, bb, rows, out_features, in_features, kw))
+                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps))
 #define PA_LAUNCH_LINEAR(EPI, NT)                                                             \
   (NT == 1 && stage == 8 ? PA_LAUNCH_LINEAR_U(EPI, 1, 8) : PA_LAUNCH_LINEAR_U(EPI, NT, 4))
   if (act == PA_ACT_SILU_MUL)
@@ -385,8 +448,8 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   return check_launch("pa_linear");
 }
 
-extern "C" int32_t pa_linear_pack(void* packed, const void* weight, int32_t rows, int32_t cols,
-                                  int32_t dtype, pa_stream_t stream) {
+extern "C" int32_t pa_linear_pack(void* packed, const void* weight, const void* col_scale,
+                                  int32_t rows, int32_t cols, int32_t dtype, pa_stream_t stream) {
   clear_error();
   PA_REQUIRE(dtype == PA_DTYPE_BF16, PA_ERR_UNSUPPORTED, "pa_linear_pack: dtype %d (bf16 only)",
              dtype);
@@ -398,7 +461,7 @@ extern "C" int32_t pa_linear_pack(void* packed, const void* weight, int32_t rows
              "pa_linear_pack: pointers must be 16-byte aligned");
   const int64_t pieces = (int64_t)rows * cols / 8;
   const int blocks = (int)std::min<int64_t>((pieces + 255) / 256, 65536);
-  linear_pack_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>((uint16_t*)packed,
-                                                              (const uint16_t*)weight, rows, cols);
+  linear_pack_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
+      (uint16_t*)packed, (const uint16_t*)weight, (const uint16_t*)col_scale, rows, cols);
   return check_launch("pa_linear_pack");
 }

@@ -20,7 +20,9 @@ over the last tokens) run in pa_linear over weights repacked once at load
 time (pa_linear_pack: every MFMA operand fragment one contiguous kilobyte);
 larger batches (prefill chunks) and the long-K down projection, for which
 hipBLASLt's split-K GEMM is faster (9.5 vs 14.9 us measured), run in
-hipBLASLt (torch.nn.functional.linear).
+hipBLASLt (torch.nn.functional.linear).  With RMSNorm and weights packed with
+the norm weights folded in (Weights.pack()), a decode step runs the fused
+layer of Engine._forward_fused: six launches per layer.
 The norm is chosen explicitly by ModelConfig.norm: "rms" (RMSNorm, what the
 benchmark configuration states) or "layer" (the zero-bias LayerNorm the
 reference's CausalLm constructs for these models,
@@ -83,23 +85,34 @@ class Weights:
         self.norm = torch.ones(h, dtype=dtype, device=device)
         self.packed = None
 
-    def pack(self):
+    def pack(self, fold_rms=True):
         """Repacks the weights pa_linear reads (QKV as separate Q and K|V row
         blocks, O, gate|up, the tied embedding as LM head) into its fragment
-        layout; the row-major tensors stay for the hipBLASLt path."""
+        layout; the row-major tensors stay for the hipBLASLt path.  fold_rms:
+        fold each RMSNorm weight into the columns of the projection after it
+        (ln1 into Q and K|V, ln2 into gate|up, the final norm into the LM head),
+        for the engine's fused decode step (pa_linear normalises its input
+        rows itself)."""
         def fits(wt):  # shapes pa_linear_pack takes
             return wt.shape[0] % 16 == 0 and wt.shape[1] % 32 == 0
 
+        n = len(self.wqkv)
         nq = self.wo[0].shape[1]
-        blocks = {"q": [x[:nq] for x in self.wqkv], "kv": [x[nq:] for x in self.wqkv],
-                  "o": self.wo, "gu": self.wgu}
-        p = {name: [ops.PackedWeight(x) for x in ws]
-             for name, ws in blocks.items() if all(fits(x) for x in ws)}
+        ln1 = self.ln1 if fold_rms else [None] * n
+        ln2 = self.ln2 if fold_rms else [None] * n
+        blocks = {"q": [(x[:nq], g) for x, g in zip(self.wqkv, ln1)],
+                  "kv": [(x[nq:], g) for x, g in zip(self.wqkv, ln1)],
+                  "o": [(x, None) for x in self.wo],
+                  "gu": [(x, g) for x, g in zip(self.wgu, ln2)]}
+        p = {name: [ops.PackedWeight(x, col_scale=g) for x, g in ws]
+             for name, ws in blocks.items() if all(fits(x) for x, _ in ws)}
         if fits(self.embed):
-            p["lm_head"] = ops.PackedWeight(self.embed)
+            p["lm_head"] = ops.PackedWeight(self.embed, col_scale=self.norm if fold_rms else None)
+        p["rms_folded"] = fold_rms
         self.packed = p
 
     def nbytes(self):
+        """Bytes of the model's weights (row-major; a step reads each once)."""
         ts = [self.embed, self.norm]
         for lst in (self.ln1, self.ln2, self.wqkv, self.bqkv, self.wo, self.wgu, self.wd):
             ts += lst
@@ -144,6 +157,10 @@ class Engine:
         def packed(name, layer):
             return pk[name][layer] if name in pk else None
 
+        if (skinny and pk.get("rms_folded") and c.norm == "rms" and
+                all(name in pk for name in ("q", "kv", "o", "gu", "lm_head"))):
+            return self._forward_fused(tokens, logit_rows)
+
         x = F.embedding(tokens, w.embed)          # residual stream [T, hidden]
         h = torch.empty_like(x)
         add = None
@@ -170,6 +187,31 @@ class Engine:
         if rows.shape[0] <= SKINNY_ROWS and ops.linear_supports(rows, w.embed):
             return ops.linear(rows, pk.get("lm_head", w.embed)).float()
         return F.linear(rows, w.embed).float()
+
+    def _forward_fused(self, tokens, logit_rows):
+        """Decode-step forward with the RMSNorms folded into the projections:
+        per layer Q and K|V (pa_linear normalising its input rows, ln1 folded
+        into the packed weights), attention, O added into the residual stream
+        in place, gate|up + SwiGLU (ln2 folded), down added into the residual
+        stream by hipBLASLt (beta = 1); the final norm is folded into the LM
+        head.  Six launches per layer instead of nine."""
+        c, w, pk = self.cfg, self.w, self.w.packed
+        t = tokens.shape[0]
+        hq, hkv, d = c.heads, c.kv_heads, c.head_dim
+        nq = hq * d
+        x = F.embedding(tokens, w.embed)  # residual stream [T, hidden]
+        for layer in range(c.layers):
+            bqkv = w.bqkv[layer]
+            q = ops.linear(x, pk["q"][layer], bqkv[:nq], rms_eps=c.eps).view(t, hq, d)
+            kv = ops.linear(x, pk["kv"][layer], bqkv[nq:], rms_eps=c.eps)
+            k = kv[:, :hkv * d].view(t, hkv, d)
+            v = kv[:, hkv * d:].view(t, hkv, d)
+            attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq, self.scale)
+            ops.linear(attn.view(t, nq), pk["o"][layer], out=x, add_to_out=True)
+            act = ops.linear(x, pk["gu"][layer], act=ops.ACT_SILU_MUL, rms_eps=c.eps)
+            x.addmm_(act, w.wd[layer].t())
+        rows = x[logit_rows].contiguous()
+        return ops.linear(rows, pk["lm_head"], rms_eps=c.eps).float()
 
     def generate(self, prompts, max_new):
         """Greedy generation for every prompt (lists of token ids).  Returns

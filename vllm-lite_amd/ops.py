@@ -339,6 +339,7 @@ def silu_mul(gate_up, out=None):
 
 
 ACT_NONE, ACT_SILU_MUL = 0, 1
+LINEAR_RMS_IN, LINEAR_ADD_OUT = 1, 2
 
 
 def linear_supports(x, weight):
@@ -351,24 +352,30 @@ def linear_supports(x, weight):
 
 class PackedWeight:
     """A bf16 weight [N, K] repacked by pa_linear_pack (see pa_dense.h); pass
-    it to linear() in place of the row-major tensor."""
+    it to linear() in place of the row-major tensor.  col_scale [K] (bf16):
+    folded into the columns (a norm weight in front of the projection)."""
 
-    def __init__(self, weight):
+    def __init__(self, weight, col_scale=None):
         _dev(weight)
         if not weight.is_contiguous():
             raise ValueError("pa_linear_pack takes a contiguous weight")
+        if col_scale is not None and (col_scale.shape != (weight.shape[1],) or
+                                      col_scale.dtype != weight.dtype):
+            raise ValueError("col_scale must be [K] in the weight's dtype")
         self.shape = tuple(weight.shape)
         self.dtype = weight.dtype
         self.data = torch.empty_like(weight)
         _check("pa_linear_pack", _lib.load().pa_linear_pack(
-            _ptr(self.data), _ptr(weight), weight.shape[0], weight.shape[1],
+            _ptr(self.data), _ptr(weight), _ptr(col_scale), weight.shape[0], weight.shape[1],
             _dtype_code(weight), _stream(weight)))
 
 
-def linear(x, weight, bias=None, act=ACT_NONE, out=None):
+def linear(x, weight, bias=None, act=ACT_NONE, out=None, rms_eps=None, add_to_out=False):
     """pa_linear: x [rows, K] bf16, weight [N, K] (or the fused gate|up
     [2 N, K] with act=ACT_SILU_MUL), row-major or a PackedWeight -> out
-    [rows, N] bf16."""
+    [rows, N] bf16.  rms_eps: RMS-normalise the rows of x on the fly (the
+    norm weight folded into a PackedWeight's col_scale); add_to_out: out is
+    the residual stream, updated in place with the result."""
     packed = isinstance(weight, PackedWeight)
     wt = weight.data if packed else weight
     _dev(x, wt)
@@ -381,9 +388,14 @@ def linear(x, weight, bias=None, act=ACT_NONE, out=None):
     if bias is not None and (bias.shape != (n,) or not bias.is_contiguous()):
         raise ValueError(f"bias {tuple(bias.shape)} does not match {n} outputs")
     if out is None:
+        if add_to_out:
+            raise ValueError("add_to_out needs out")
         out = torch.empty(rows, n, dtype=x.dtype, device=x.device)
+    flags = (LINEAR_RMS_IN if rms_eps is not None else 0) | (LINEAR_ADD_OUT if add_to_out else 0)
     lib = _lib.load()
     _check("pa_linear", lib.pa_linear(_ptr(out), _ptr(x), _ptr(wt),
                                       _ptr(bias) if bias is not None else None, rows, n, k, act,
-                                      1 if packed else 0, _dtype_code(x), _stream(x)))
+                                      1 if packed else 0, flags,
+                                      float(rms_eps) if rms_eps is not None else 0.0,
+                                      _dtype_code(x), _stream(x)))
     return out
