@@ -138,8 +138,9 @@ int32_t pa_batch_is_decode(const pa_batch* batch);
  * then attends with pa_decode (all-decode batch) or pa_prefill (anything
  * else; decode rows become one-row chunks) into out [T, Hq, D].
  *   q [T, Hq, D] (rotated in place when inv_freq != NULL), key / value
- *   [T, Hkv, D] with token strides (0 = contiguous), inv_freq [D/2] device
- *   f32 or NULL, scale = attn_factor / sqrt(D).
+ *   [T, Hkv, D], each with a token stride in elements (0 = contiguous; q, k
+ *   and v may be views of one fused QKV projection output), inv_freq [D/2]
+ *   device f32 or NULL, scale = attn_factor / sqrt(D).
  * Allocates (once, grown on demand) the decode workspace. */
 int32_t pa_batch_attention(pa_batch* batch, pa_kv_cache* cache, int32_t layer, int32_t num_heads,
                            void* q, int64_t q_stride, const void* key, int64_t key_stride,

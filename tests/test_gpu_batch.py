@@ -63,7 +63,8 @@ def test_engine_loop(pa, oracle, dtype, rope):
             if dtype == "bf16":
                 qkv = oracle.f32_to_bf16(qkv)
             g = to_dev(qkv)
-            q = g[:, :hq].contiguous()
+            # layer 1: q as a strided view of the fused QKV rows
+            q = g[:, :hq] if layer == 1 else g[:, :hq].contiguous()
             out = batch.attention(cache, layer, q, g[:, hq:hq + hkv], g[:, hq + hkv:],
                                   to_dev(inv) if rope else None)
             qr, kr = qkv[:, :hq], qkv[:, hq:hq + hkv]

@@ -10,6 +10,8 @@
 // launch and one attention launch for the whole batch.
 #include <hip/hip_runtime.h>
 
+#include "pa_internal.hpp"
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -215,8 +217,6 @@ extern "C" int32_t pa_batch_attention(pa_batch* b, pa_kv_cache* cache, int32_t l
                               key_stride, value_stride, dtype, stream);
   }
   if (rc != PA_OK) return rc;
-  PA_REQUIRE(q_stride == 0 || q_stride == (int64_t)num_heads * d, PA_ERR_UNSUPPORTED,
-             "pa_batch_attention: attention needs contiguous q rows");
   if (b->decode) {
     // With a capacity the launch shape depends on it alone (sequences read
     // their own lengths on the device), so the call can be replayed.
@@ -226,12 +226,13 @@ extern "C" int32_t pa_batch_attention(pa_batch* b, pa_kv_cache* cache, int32_t l
     const int max_ctx = b->capacity > 0 ? b->capacity : b->max_ctx;
     const size_t need = pa_decode_workspace_size(b->num_seqs, num_heads, d, max_ctx);
     if ((rc = b->workspace.ensure(std::max<size_t>(need, 256)))) return rc;
-    return pa_decode(out, q, kc, vc, (const int32_t*)b->tables.ptr, b->max_blocks,
-                     (const int32_t*)b->ctx_lens.ptr, max_ctx, b->num_seqs, num_heads, hkv, d,
-                     b->num_blocks, scale, b->workspace.ptr, b->workspace.bytes, dtype, stream);
+    return pa::decode_strided(out, q, q_stride, kc, vc, (const int32_t*)b->tables.ptr,
+                              b->max_blocks, (const int32_t*)b->ctx_lens.ptr, max_ctx,
+                              b->num_seqs, num_heads, hkv, d, b->num_blocks, scale,
+                              b->workspace.ptr, b->workspace.bytes, dtype, stream);
   }
-  return pa_prefill(out, q, kc, vc, (const int32_t*)b->tables.ptr, b->max_blocks,
-                    (const int32_t*)b->cu_q.ptr, (const int32_t*)b->past.ptr, b->num_seqs,
-                    b->num_tokens, b->max_q, num_heads, hkv, d, b->num_blocks, scale, dtype,
-                    stream);
+  return pa::prefill_strided(out, q, q_stride, kc, vc, (const int32_t*)b->tables.ptr,
+                             b->max_blocks, (const int32_t*)b->cu_q.ptr,
+                             (const int32_t*)b->past.ptr, b->num_seqs, b->num_tokens, b->max_q,
+                             num_heads, hkv, d, b->num_blocks, scale, dtype, stream);
 }

@@ -24,6 +24,7 @@
 #include <type_traits>
 
 #include "pa_common.hpp"
+#include "pa_internal.hpp"
 
 namespace pa {
 namespace {
@@ -134,7 +135,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
     float scale_log2, int num_parts, int part_len, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml) {
+    float* __restrict__ ws_ml, int64_t q_row) {
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
   // NW > 1: the workgroup's wavefronts take partitions blockIdx.x * NW + w
@@ -165,7 +166,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     if (c < G)
-      qv[s] = *reinterpret_cast<const bf16x8*>(q + ((int64_t)seq * Hq + head) * D + 32 * s + 8 * j);
+      qv[s] = *reinterpret_cast<const bf16x8*>(q + (int64_t)seq * q_row + (int64_t)head * D + 32 * s + 8 * j);
     else
       qv[s] = bf16x8{};
   }
@@ -334,7 +335,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
     const uint8_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
     float scale_log2, int num_parts, int part_len, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml) {
+    float* __restrict__ ws_ml, int64_t q_row) {
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
   constexpr int DL = D / 4;   // dims (bytes) of a K row per lane group
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     if (c < G)
-      qv[s] = *reinterpret_cast<const bf16x8*>(q + ((int64_t)seq * Hq + head) * D + DL * j + 8 * s);
+      qv[s] = *reinterpret_cast<const bf16x8*>(q + (int64_t)seq * q_row + (int64_t)head * D + DL * j + 8 * s);
     else
       qv[s] = bf16x8{};
   }
@@ -538,7 +539,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
     const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int D, int num_blocks,
     float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    const float* __restrict__ kv_scales) {
+    const float* __restrict__ kv_scales, int64_t q_row) {
   // kv_scales: per-block scales of a quantised (int8-in-f32) cache, or null
   __shared__ float qs[512];
   __shared__ float ps[kPart];
@@ -559,7 +560,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
   const int n = min(ctx - tok0, kPart);
   const int tid = threadIdx.x;
   for (int d = tid; d < D; d += blockDim.x)
-    qs[d] = Elem<T>::load(q + ((int64_t)seq * Hq + h) * D + d);
+    qs[d] = Elem<T>::load(q + (int64_t)seq * q_row + (int64_t)h * D + d);
   if (tid < (n + kBlock - 1) / kBlock) {
     const int32_t b = block_tables[(int64_t)seq * mbs + tok0 / kBlock + tid];
     bs[tid] = (b >= 0 && b < num_blocks) ? b : -1;
@@ -643,7 +644,7 @@ __global__ __launch_bounds__(1024) void decode_f32_group_kernel(
     const float* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int num_blocks,
     float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    const float* __restrict__ kv_scales) {
+    const float* __restrict__ kv_scales, int64_t q_row) {
   static_assert(256 % D == 0 && D % 16 == 0, "head_dim must divide 256, in 16-float steps");
   constexpr int NPB = kPart / kBlock;        // blocks per partition
   constexpr int R = 1024 / D;                // lanes per dim in P·V (a power of two <= 64)
@@ -663,7 +664,7 @@ __global__ __launch_bounds__(1024) void decode_f32_group_kernel(
   const int bi0 = tok0 / kBlock;
   int32_t braw = -1;
   if (tid < NPB && bi0 + tid < mbs) braw = block_tables[(int64_t)seq * mbs + bi0 + tid];
-  for (int e = tid; e < G * D; e += 1024) qs[e] = q[((int64_t)seq * Hq + kvh * G) * D + e];
+  for (int e = tid; e < G * D; e += 1024) qs[e] = q[(int64_t)seq * q_row + (int64_t)kvh * G * D + e];
   const int ctx = min(context_lens[seq], mbs * kBlock);
   if (tok0 >= ctx) {
     if (num_parts == 1)
@@ -869,7 +870,7 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
                     int32_t max_blocks_per_seq, const int32_t* context_lens,
                     int32_t max_context_len, int32_t num_seqs, int32_t num_heads,
                     int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks, float scale,
-                    void* workspace, size_t workspace_bytes, int32_t dtype, pa_stream_t stream) {
+                    void* workspace, size_t workspace_bytes, int32_t dtype, pa_stream_t stream, int64_t q_row = 0) {
   clear_error();
   PA_REQUIRE(dtype_ok(dtype) || dtype == PA_DTYPE_FP8_E4M3, PA_ERR_INVALID_ARG,
              "pa_decode: unknown dtype %d", dtype);
@@ -915,6 +916,9 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
     ws_o = (float*)workspace;
     ws_ml = ws_o + (size_t)num_seqs * num_heads * np * head_dim;
   }
+  if (q_row == 0) q_row = (int64_t)num_heads * head_dim;
+  PA_REQUIRE(q_row >= (int64_t)num_heads * head_dim, PA_ERR_INVALID_ARG,
+             "pa_decode: q row stride %lld below num_heads * head_dim", (long long)q_row);
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   if (mfma) {
@@ -925,7 +929,7 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   KERNEL<DD, NW><<<grid, 64 * NW, 0, s>>>(                                                    \
       o, qq, (const TC*)k_cache, (const TC*)v_cache, block_tables, max_blocks_per_seq,        \
       context_lens, num_heads, num_kv_heads, G, num_blocks, scale_log2, np, part_len, ws_o,   \
-      ws_ml)
+      ws_ml, q_row)
 #define PA_LAUNCH_MFMA(KERNEL, TC, DD)                                                        \
   do {                                                                                        \
     if (merge_waves == 2)                                                                     \
@@ -960,14 +964,14 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
       decode_generic_kernel<uint16_t, Fp8><<<grid, 256, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const Fp8*)k_cache, (const Fp8*)v_cache,
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
-          num_blocks, scale_log2, np, ws_o, ws_ml, nullptr);
+          num_blocks, scale_log2, np, ws_o, ws_ml, nullptr, q_row);
     else if (dtype == PA_DTYPE_BF16)
       decode_generic_kernel<uint16_t><<<grid, 256, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
-          num_blocks, scale_log2, np, ws_o, ws_ml, nullptr);
+          num_blocks, scale_log2, np, ws_o, ws_ml, nullptr, q_row);
     else if (f32_group) {
-#define PA_LAUNCH_F32(DD)                                                                     decode_f32_group_kernel<DD><<<dim3(np, num_kv_heads, num_seqs), 1024, 0, s>>>(                   (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,                  block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, num_blocks,       scale_log2, np, ws_o, ws_ml, kv_scales)
+#define PA_LAUNCH_F32(DD)                                                                     decode_f32_group_kernel<DD><<<dim3(np, num_kv_heads, num_seqs), 1024, 0, s>>>(                   (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,                  block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, num_blocks,       scale_log2, np, ws_o, ws_ml, kv_scales, q_row)
       switch (head_dim) {
         case 16: PA_LAUNCH_F32(16); break;
         case 32: PA_LAUNCH_F32(32); break;
@@ -981,7 +985,7 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
       decode_generic_kernel<float><<<grid, 256, 0, s>>>(
           (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
-          num_blocks, scale_log2, np, ws_o, ws_ml, kv_scales);
+          num_blocks, scale_log2, np, ws_o, ws_ml, kv_scales, q_row);
   }
   int32_t rc = check_launch("pa_decode");
   if (rc != PA_OK || np == 1 || merge_waves > 1) return rc;
@@ -1026,3 +1030,17 @@ extern "C" int32_t pa_decode_quantized(void* out, const void* q, const float* k_
                      context_lens, max_context_len, num_seqs, num_heads, num_kv_heads, head_dim,
                      num_blocks, scale, workspace, workspace_bytes, PA_DTYPE_F32, stream);
 }
+
+namespace pa {
+int32_t decode_strided(void* out, const void* q, int64_t q_row, const void* k_cache,
+                       const void* v_cache, const int32_t* block_tables,
+                       int32_t max_blocks_per_seq, const int32_t* context_lens,
+                       int32_t max_context_len, int32_t num_seqs, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks, float scale,
+                       void* workspace, size_t workspace_bytes, int32_t dtype,
+                       pa_stream_t stream) {
+  return decode_impl(out, q, k_cache, v_cache, nullptr, block_tables, max_blocks_per_seq,
+                     context_lens, max_context_len, num_seqs, num_heads, num_kv_heads, head_dim,
+                     num_blocks, scale, workspace, workspace_bytes, dtype, stream, q_row);
+}
+}  // namespace pa

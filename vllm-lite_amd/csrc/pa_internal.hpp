@@ -17,4 +17,21 @@ PA_HIDDEN int32_t launch_quant_read(const float* k_cache, const float* v_cache,
                                     const float* scales, const int32_t* block_ids, int seq_len,
                                     int H, int D, float* out_k, float* out_v, hipStream_t stream);
 
+// pa_decode / pa_prefill with q rows q_row elements apart (a view of a fused
+// QKV projection output); pa_batch_attention's path.
+PA_HIDDEN int32_t decode_strided(void* out, const void* q, int64_t q_row, const void* k_cache,
+                                 const void* v_cache, const int32_t* block_tables,
+                                 int32_t max_blocks_per_seq, const int32_t* context_lens,
+                                 int32_t max_context_len, int32_t num_seqs, int32_t num_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                                 float scale, void* workspace, size_t workspace_bytes,
+                                 int32_t dtype, hipStream_t stream);
+PA_HIDDEN int32_t prefill_strided(void* out, const void* q, int64_t q_row, const void* k_cache,
+                                  const void* v_cache, const int32_t* block_tables,
+                                  int32_t max_blocks_per_seq, const int32_t* cu_q_lens,
+                                  const int32_t* past_lens, int32_t num_seqs, int32_t total_q,
+                                  int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t num_blocks, float scale,
+                                  int32_t dtype, hipStream_t stream);
+
 }  // namespace pa

@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "pa_common.hpp"
+#include "pa_internal.hpp"
 
 namespace pa {
 namespace {
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
-    int num_blocks, float scale_log2) {
+    int num_blocks, float scale_log2, int64_t q_row) {
   constexpr int KS = D / 32;
   constexpr int DT = D / 16;
   constexpr int ROWS = 16 * NT;  // query rows per wavefront
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
     for (int s = 0; s < KS; ++s) {
       if (row < qlen)
         qv[nt][s] = *reinterpret_cast<const bf16x8*>(
-            q + ((int64_t)(q_begin + row) * Hq + h) * D + 32 * s + 8 * j);
+            q + (int64_t)(q_begin + row) * q_row + (int64_t)h * D + 32 * s + 8 * j);
       else
         qv[nt][s] = bf16x8{};
     }
@@ -242,7 +243,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const TC* __restrict__ kc,
     const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
-    int num_blocks, float scale_log2, int B, int tiles_per_seq, int head_groups) {
+    int num_blocks, float scale_log2, int B, int tiles_per_seq, int head_groups, int64_t q_row) {
   constexpr int KS = D / 32;   // QK reduction steps
   constexpr int DT = D / 16;   // PV output tiles
   // Cache elements: bf16 (TC = uint16_t) or FP8-E4M3 (TC = uint8_t), the
@@ -345,7 +346,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     for (int s = 0; s < KS; ++s) {
       if (rows_active && row < qlen) {
         const bf16x8 raw = *reinterpret_cast<const bf16x8*>(
-            q + ((int64_t)(q_begin + row) * Hq + head) * D + 32 * s + 8 * j);
+            q + (int64_t)(q_begin + row) * q_row + (int64_t)head * D + 32 * s + 8 * j);
 #pragma unroll
         for (int i = 0; i < 8; ++i) qv[nt][s][i] = (__bf16)((float)raw[i] * scale_log2);
       } else {
@@ -728,7 +729,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
     T* __restrict__ out, const T* __restrict__ q, const TC* __restrict__ kc,
     const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
-    int D, int num_blocks, float scale_log2, const float* __restrict__ kv_scales) {
+    int D, int num_blocks, float scale_log2, const float* __restrict__ kv_scales, int64_t q_row) {
   // kv_scales: per-block scales of a quantised (int8-in-f32) cache, or null
   __shared__ float qs[512];
   __shared__ float ps[64];
@@ -738,7 +739,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
   if (row >= cu_q[seq + 1] - q_begin) return;
   const int G = Hq / Hkv, kvh = h / G;
   const int pos = past_lens[seq] + row;
-  const int64_t qoff = ((int64_t)(q_begin + row) * Hq + h) * D;
+  const int64_t qoff = (int64_t)(q_begin + row) * q_row + (int64_t)h * D;
   for (int d = lane; d < D; d += 64) qs[d] = Elem<T>::load(q + qoff + d);
   float acc[8];
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
@@ -789,7 +790,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;
   for (int i = 0; i * 64 + lane < D; ++i)
-    Elem<T>::store(out + qoff + i * 64 + lane, acc[i] * inv);
+    Elem<T>::store(out + ((int64_t)(q_begin + row) * Hq + h) * D + i * 64 + lane, acc[i] * inv);
 }
 
 }  // namespace
@@ -821,7 +822,7 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
                      const int32_t* past_lens, int32_t num_seqs, int32_t total_q,
                      int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
                      int32_t head_dim, int32_t num_blocks, float scale, int32_t dtype,
-                     pa_stream_t stream) {
+                     pa_stream_t stream, int64_t q_row = 0) {
   clear_error();
   PA_REQUIRE(dtype_ok(dtype) || dtype == PA_DTYPE_FP8_E4M3, PA_ERR_INVALID_ARG,
              "pa_prefill: unknown dtype %d", dtype);
@@ -835,6 +836,9 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
   if (num_seqs == 0 || total_q == 0 || max_q_len == 0) return PA_OK;
   PA_REQUIRE(out && q && k_cache && v_cache && block_tables && cu_q_lens && past_lens,
              PA_ERR_INVALID_ARG, "pa_prefill: null pointer");
+  if (q_row == 0) q_row = (int64_t)num_heads * head_dim;
+  PA_REQUIRE(q_row >= (int64_t)num_heads * head_dim, PA_ERR_INVALID_ARG,
+             "pa_prefill: q row stride %lld below num_heads * head_dim", (long long)q_row);
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   const bool fp8 = dtype == PA_DTYPE_FP8_E4M3;
@@ -859,7 +863,7 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
   prefill_tiled_kernel<DD, NT, TC><<<grid, 64 * (16 / NT), 0, s>>>(                           \
       o, qq, (const TC*)k_cache, (const TC*)v_cache, block_tables, max_blocks_per_seq,        \
       cu_q_lens, past_lens, num_heads, num_kv_heads, num_blocks, scale_log2, num_seqs,        \
-      tiles_per_seq, head_groups)
+      tiles_per_seq, head_groups, q_row)
     if (fp8) {
       if (head_dim == 128)
         PA_LAUNCH_TILED(128, uint8_t);
@@ -883,7 +887,7 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
 #define PA_LAUNCH_PREFILL(DD)                                                                 \
   prefill_mfma_kernel<DD, NT><<<grid, 64 * kWaves, 0, s>>>(                                   \
       o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,       \
-      num_kv_heads, num_blocks, scale_log2)
+      num_kv_heads, num_blocks, scale_log2, q_row)
     PA_LAUNCH_PREFILL(256);
 #undef PA_LAUNCH_PREFILL
   } else {
@@ -892,17 +896,17 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
       prefill_generic_kernel<uint16_t, Fp8><<<grid, 64, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const Fp8*)k_cache, (const Fp8*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2, nullptr);
+          head_dim, num_blocks, scale_log2, nullptr, q_row);
     else if (dtype == PA_DTYPE_BF16)
       prefill_generic_kernel<uint16_t><<<grid, 64, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2, nullptr);
+          head_dim, num_blocks, scale_log2, nullptr, q_row);
     else
       prefill_generic_kernel<float><<<grid, 64, 0, s>>>(
           (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2, kv_scales);
+          head_dim, num_blocks, scale_log2, kv_scales, q_row);
   }
   return check_launch("pa_prefill");
 }
@@ -936,3 +940,17 @@ extern "C" int32_t pa_prefill_quantized(void* out, const void* q, const float* k
                       cu_q_lens, past_lens, num_seqs, total_q, max_q_len, num_heads, num_kv_heads,
                       head_dim, num_blocks, scale, PA_DTYPE_F32, stream);
 }
+
+namespace pa {
+int32_t prefill_strided(void* out, const void* q, int64_t q_row, const void* k_cache,
+                        const void* v_cache, const int32_t* block_tables,
+                        int32_t max_blocks_per_seq, const int32_t* cu_q_lens,
+                        const int32_t* past_lens, int32_t num_seqs, int32_t total_q,
+                        int32_t max_q_len, int32_t num_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t num_blocks, float scale, int32_t dtype,
+                        pa_stream_t stream) {
+  return prefill_impl(out, q, k_cache, v_cache, nullptr, block_tables, max_blocks_per_seq,
+                      cu_q_lens, past_lens, num_seqs, total_q, max_q_len, num_heads, num_kv_heads,
+                      head_dim, num_blocks, scale, dtype, stream, q_row);
+}
+}  // namespace pa

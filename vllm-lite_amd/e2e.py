@@ -22,7 +22,7 @@ larger batches (prefill chunks) and the long-K down projection, for which
 hipBLASLt's split-K GEMM is faster (9.5 vs 14.9 us measured), run in
 hipBLASLt (torch.nn.functional.linear).  With RMSNorm and weights packed with
 the norm weights folded in (Weights.pack()), a decode step runs the fused
-layer of Engine._forward_fused: six launches per layer.
+layer of Engine._forward_fused: five launches per layer.
 The norm is chosen explicitly by ModelConfig.norm: "rms" (RMSNorm, what the
 benchmark configuration states) or "layer" (the zero-bias LayerNorm the
 reference's CausalLm constructs for these models,
@@ -100,7 +100,8 @@ class Weights:
         nq = self.wo[0].shape[1]
         ln1 = self.ln1 if fold_rms else [None] * n
         ln2 = self.ln2 if fold_rms else [None] * n
-        blocks = {"q": [(x[:nq], g) for x, g in zip(self.wqkv, ln1)],
+        blocks = {"qkv": [(x, g) for x, g in zip(self.wqkv, ln1)],
+                  "q": [(x[:nq], g) for x, g in zip(self.wqkv, ln1)],
                   "kv": [(x[nq:], g) for x, g in zip(self.wqkv, ln1)],
                   "o": [(x, None) for x in self.wo],
                   "gu": [(x, g) for x, g in zip(self.wgu, ln2)]}
@@ -158,7 +159,7 @@ class Engine:
             return pk[name][layer] if name in pk else None
 
         if (skinny and pk.get("rms_folded") and c.norm == "rms" and
-                all(name in pk for name in ("q", "kv", "o", "gu", "lm_head"))):
+                all(name in pk for name in ("qkv", "o", "gu", "lm_head"))):
             return self._forward_fused(tokens, logit_rows)
 
         x = F.embedding(tokens, w.embed)          # residual stream [T, hidden]
@@ -190,22 +191,23 @@ class Engine:
 
     def _forward_fused(self, tokens, logit_rows):
         """Decode-step forward with the RMSNorms folded into the projections:
-        per layer Q and K|V (pa_linear normalising its input rows, ln1 folded
-        into the packed weights), attention, O added into the residual stream
-        in place, gate|up + SwiGLU (ln2 folded), down added into the residual
-        stream by hipBLASLt (beta = 1); the final norm is folded into the LM
-        head.  Six launches per layer instead of nine."""
+        per layer the fused QKV projection (pa_linear normalising its input
+        rows, ln1 folded into the packed weight; attention reads q, k, v as
+        strided views of its rows), attention, O added into the residual
+        stream in place, gate|up + SwiGLU (ln2 folded), down added into the
+        residual stream by hipBLASLt (beta = 1); the final norm is folded into
+        the LM head.  Five launches per layer instead of nine."""
         c, w, pk = self.cfg, self.w, self.w.packed
         t = tokens.shape[0]
         hq, hkv, d = c.heads, c.kv_heads, c.head_dim
         nq = hq * d
         x = F.embedding(tokens, w.embed)  # residual stream [T, hidden]
         for layer in range(c.layers):
-            bqkv = w.bqkv[layer]
-            q = ops.linear(x, pk["q"][layer], bqkv[:nq], rms_eps=c.eps).view(t, hq, d)
-            kv = ops.linear(x, pk["kv"][layer], bqkv[nq:], rms_eps=c.eps)
-            k = kv[:, :hkv * d].view(t, hkv, d)
-            v = kv[:, hkv * d:].view(t, hkv, d)
+            # one QKV projection; q, k, v are strided views of its rows
+            qkv = ops.linear(x, pk["qkv"][layer], w.bqkv[layer], rms_eps=c.eps)
+            q = qkv[:, :nq].view(t, hq, d)
+            k = qkv[:, nq:nq + hkv * d].view(t, hkv, d)
+            v = qkv[:, nq + hkv * d:].view(t, hkv, d)
             attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq, self.scale)
             ops.linear(attn.view(t, nq), pk["o"][layer], out=x, add_to_out=True)
             act = ops.linear(x, pk["gu"][layer], act=ops.ACT_SILU_MUL, rms_eps=c.eps)

@@ -228,8 +228,8 @@ class StepBatch:
 
     def attention(self, cache, layer, q, key, value, inv_freq=None, scale=None):
         """q [T, Hq, D] (rotated in place with inv_freq), key / value
-        [T, Hkv, D] (rows may be strided views of a fused projection) ->
-        out [T, Hq, D]."""
+        [T, Hkv, D] (rows of all three may be strided views of a fused
+        projection) -> out [T, Hq, D]."""
         t, hq, d = q.shape
         if t != self.num_tokens():
             raise ValueError(f"batch has {self.num_tokens()} tokens, q has {t}")
@@ -239,8 +239,6 @@ class StepBatch:
             if x.dtype != cache.dtype or x.device != cache.device or x.stride(2) != 1 or \
                     x.stride(1) != d:
                 raise ValueError("q / key / value rows must be [H, D] in the cache dtype")
-        if q.stride(0) != hq * d:
-            raise ValueError("q must be contiguous")
         if inv_freq is not None and (inv_freq.dtype != torch.float32 or
                                      inv_freq.shape != (d // 2,)):
             raise ValueError("inv_freq must be float32 [D/2]")
