@@ -842,10 +842,14 @@ int num_partitions(int max_ctx, int part_len) {
 // Small batches of short contexts (fewer than 512 items at 256 tokens, at
 // most 1024 tokens) take 128-token partitions, up to 8 per (kv head,
 // sequence), which one workgroup merges in LDS.
-int choose_partition(int num_seqs, int num_kv_heads, int max_ctx, int head_dim) {
+int choose_partition(int num_seqs, int num_kv_heads, int max_ctx, int head_dim, int elem_bytes) {
   const long long units = (long long)num_seqs * num_kv_heads;
   auto items = [&](int p) { return units * ((max_ctx + p - 1) / p); };
-  if (max_ctx <= 8192 && items(2048) >= 1024) return 2048;
+  // one-byte (FP8) caches: half the length, so the same contexts give twice
+  // the wavefronts (measured on the config-2 shape: 91.2 us at 2048, 84.7 us
+  // at 1024; a streaming probe: 5.7 TB/s with 1024 wavefronts, 6.75 with 2048)
+  const int long_part = elem_bytes == 1 ? 1024 : 2048;
+  if (max_ctx <= 8192 && items(long_part) >= 1024) return long_part;
   if (items(512) >= 1024) return 512;
   if (items(kPart) < 512 && max_ctx <= 1024 && head_dim <= 128) return kPart / 2;
   return kPart;
@@ -895,7 +899,8 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   const bool f32_group = dtype == PA_DTYPE_F32 && G <= kF32MaxG && head_dim <= 256 &&
                          256 % head_dim == 0 && head_dim % 16 == 0;
   const int part_len =
-      mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len, head_dim) : kPart;
+      mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len, head_dim, fp8 ? 1 : 2)
+           : kPart;
   const int np = num_partitions(max_context_len, part_len);
   PA_REQUIRE(np <= 1024, PA_ERR_UNSUPPORTED,
              "pa_decode: context of %d tokens needs %d > 1024 partitions", max_context_len, np);
