@@ -72,11 +72,25 @@ enum { PA_LINEAR_RMS_IN = 1, PA_LINEAR_ADD_OUT = 2 };
  *   PA_LINEAR_ADD_OUT  out is the residual stream and is updated in place,
  *                      out[r][n] = bf16(out[r][n] + bf16(y[r][n])) (the
  *                      decoder block's residual add); not with SwiGLU.
+ * workspace: NULL, or pa_linear_workspace_size() bytes (256-byte aligned)
+ * whose first bytes hold counters that must be ZERO before the first call
+ * that uses it (e.g. hipMemset once after allocating it); every call leaves
+ * them zero again.  With it, long-K projections over few output tiles (the
+ * MLP down projection of a decode step) split K over several workgroups per
+ * tile, the last to finish summing the partial tiles in a fixed order (the
+ * result does not depend on their timing).  Calls that may run at the same
+ * time need distinct workspaces.  Without it one workgroup takes each tile.
  * Built for rows <= 64, where the weights dominate the traffic; the weights
  * are re-read once per 32 rows.  bf16 only (PA_ERR_UNSUPPORTED otherwise). */
 int32_t pa_linear(void* out, const void* x, const void* weight, const void* bias, int32_t rows,
                   int32_t out_features, int32_t in_features, int32_t act, int32_t packed,
-                  int32_t flags, float eps, int32_t dtype, pa_stream_t stream);
+                  int32_t flags, float eps, void* workspace, size_t workspace_bytes,
+                  int32_t dtype, pa_stream_t stream);
+
+/* Workspace bytes pa_linear's K split uses for this shape (0: none; the call
+ * then needs no workspace).  No reference counterpart. */
+size_t pa_linear_workspace_size(int32_t rows, int32_t out_features, int32_t in_features,
+                                int32_t act);
 
 /* Repacks a row-major bf16 weight [rows, cols] (rows a multiple of 16, cols
  * of 32) into the fragment order pa_linear reads with packed = 1: every
@@ -88,6 +102,14 @@ int32_t pa_linear(void* out, const void* x, const void* weight, const void* bias
  * load-time layout step for the weights pa_linear streams. */
 int32_t pa_linear_pack(void* packed, const void* weight, const void* col_scale, int32_t rows,
                        int32_t cols, int32_t dtype, pa_stream_t stream);
+
+/* Greedy sampling's argmax_logits (crates/traits/src/sampling.rs:439-453) on
+ * every row of a logit matrix: out[r] = the first column holding the row's
+ * largest value, comparing with `>` from -inf, so NaN never wins and a row
+ * with no value above -inf (or cols == 0) gives 0.  logits [rows, cols] with
+ * row_stride elements between rows (0 = cols); out [rows] int64 (device). */
+int32_t pa_argmax(int64_t* out, const void* logits, int32_t rows, int32_t cols,
+                  int64_t row_stride, int32_t dtype, pa_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -43,6 +43,8 @@ def load():
         lib.oracle_expand_kv.restype = None
         lib.oracle_block_hash.argtypes = [p, i64]
         lib.oracle_block_hash.restype = C.c_uint64
+        lib.oracle_argmax_logits.argtypes = [p, i64]
+        lib.oracle_argmax_logits.restype = i64
         lib.oracle_attention.argtypes = [p, p, p, i32, i32, i32, i32, i32, i32, f32, i32, p]
         lib.oracle_paged_attention.argtypes = [p, p, p, p, i32, p, p, i32, i32, i32, i32, i32,
                                                f32, i32, i32, i32, p]
@@ -179,6 +181,15 @@ def expand_kv(x, num_q_heads):
 def block_hash(data):
     data = np.ascontiguousarray(data, dtype=np.float32).ravel()
     return int(load().oracle_block_hash(_p(data), data.size))
+
+
+def argmax_logits(logits):
+    """Greedy token of each row of logits [rows, vocab] (last axis), int64."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    rows = x.reshape(-1, x.shape[-1]) if x.ndim > 1 else x.reshape(1, -1)
+    lib = load()
+    out = np.array([lib.oracle_argmax_logits(_p(r), r.size) for r in rows], np.int64)
+    return out.reshape(x.shape[:-1]) if x.ndim > 1 else out[0]
 
 
 # ---- attention -------------------------------------------------------------

@@ -36,6 +36,9 @@
  *   oracle_rope_inv_freq / oracle_rope -> closed forms (identity at
  *          position 0, cos/sin at position 1, rotation direction, per-type
  *          frequency tables).
+ *   oracle_argmax_logits    -> the reference's sampling.rs:468-490 known
+ *          answers (first of equal maxima, negatives, empty, one element)
+ *          and numpy's argmax on NaN-free rows.
  *   oracle_fp8_encode / oracle_fp8_decode -> the reference's own test values,
  *          torch's independent float8_e4m3fn conversions wherever that
  *          format and the reference's coincide, exhaustive round trips and a
@@ -252,6 +255,21 @@ uint64_t oracle_block_hash(const float* data, int64_t n) {
     acc = acc * 31u + x;
   }
   return acc;
+}
+
+/* Greedy sampling. crates/traits/src/sampling.rs:439-453:
+ *   enumerate().fold((0, -inf), |(bi, bv), (i, v)| if v > bv {(i, v)} else {(bi, bv)})
+ * i.e. the first strict maximum; NaN never compares greater; an empty row or
+ * one with nothing above -inf keeps index 0. */
+int64_t oracle_argmax_logits(const float* x, int64_t n) {
+  int64_t bi = 0;
+  float bv = -INFINITY;
+  for (int64_t i = 0; i < n; ++i)
+    if (x[i] > bv) {
+      bi = i;
+      bv = x[i];
+    }
+  return bi;
 }
 
 /* ------------------------------------------------------------------------ */

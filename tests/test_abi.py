@@ -74,15 +74,27 @@ def test_argument_errors_without_gpu(lib):
     assert rc == -4 and b"workspace" in lib.pa_last_error()
     # pa_linear: f32, K not a multiple of 32, N not a multiple of 16, bias with SwiGLU
     p = C.c_void_p(16)
-    assert lib.pa_linear(p, p, p, null, 4, 64, 96, 0, 0, 0, 0.0, 0, null) == -3
-    assert lib.pa_linear(p, p, p, null, 4, 64, 80, 0, 0, 0, 0.0, 1, null) == -3
+    assert lib.pa_linear(p, p, p, null, 4, 64, 96, 0, 0, 0, 0.0, null, 0, 0, null) == -3
+    assert lib.pa_linear(p, p, p, null, 4, 64, 80, 0, 0, 0, 0.0, null, 0, 1, null) == -3
     assert b"multiple of 32" in lib.pa_last_error()
-    assert lib.pa_linear(p, p, p, null, 4, 40, 96, 0, 0, 0, 0.0, 1, null) == -3
-    assert lib.pa_linear(p, p, p, p, 4, 48, 96, 1, 0, 0, 0.0, 1, null) == -1
-    assert lib.pa_linear(null, null, null, null, 0, 64, 96, 0, 0, 0, 0.0, 1, null) == 0
-    assert lib.pa_linear(p, p, p, null, 4, 64, 96, 1, 0, 2, 0.0, 1, null) == -1  # add + SwiGLU
-    assert lib.pa_linear(p, p, p, null, 4, 64, 96, 0, 0, 1, 0.0, 1, null) == -1  # rms, eps 0
+    assert lib.pa_linear(p, p, p, null, 4, 40, 96, 0, 0, 0, 0.0, null, 0, 1, null) == -3
+    assert lib.pa_linear(p, p, p, p, 4, 48, 96, 1, 0, 0, 0.0, null, 0, 1, null) == -1
+    assert lib.pa_linear(null, null, null, null, 0, 64, 96, 0, 0, 0, 0.0, null, 0, 1, null) == 0
+    assert lib.pa_linear(p, p, p, null, 4, 64, 96, 1, 0, 2, 0.0, null, 0, 1, null) == -1  # add + SwiGLU
+    assert lib.pa_linear(p, p, p, null, 4, 64, 96, 0, 0, 1, 0.0, null, 0, 1, null) == -1  # rms, eps 0
+    # pa_linear's K split: long K over few tiles only; a workspace not 256-byte aligned
+    assert lib.pa_linear_workspace_size(32, 896, 4864, 0) > 0
+    assert lib.pa_linear_workspace_size(32, 896, 896, 0) == 0
+    assert lib.pa_linear_workspace_size(32, 151936, 896, 0) == 0
+    assert lib.pa_linear_workspace_size(0, 896, 4864, 0) == 0
+    assert lib.pa_linear(p, p, p, null, 32, 896, 4864, 0, 0, 0, 0.0, C.c_void_p(16), 1 << 30, 1,
+                         null) == -1
     assert lib.pa_linear_pack(p, C.c_void_p(32), null, 24, 64, 1, null) == -3  # rows not a multiple of 16
+    # argmax: unknown dtype, row stride below cols, null pointer; no rows is a no-op
+    assert lib.pa_argmax(p, p, 2, 8, 0, 9, null) == -1
+    assert lib.pa_argmax(p, p, 2, 8, 4, 1, null) == -1
+    assert lib.pa_argmax(null, p, 2, 8, 0, 1, null) == -1
+    assert lib.pa_argmax(null, null, 0, 8, 0, 1, null) == 0
     # read_kv: table cannot hold seq_len
     rc = lib.pa_read_kv(null, null, null, 1, 17, 2, 4, 4, null, null, 0, null)
     assert rc == -2

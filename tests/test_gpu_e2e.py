@@ -112,7 +112,7 @@ def ref_logits(cfg, w, tokens, inv_freq):
 
 @pytest.mark.parametrize("norm,packed", [("rms", False), ("rms", "plain"), ("rms", True),
                                          ("layer", True)])
-def test_engine_matches_fp32_forward(pa, norm, packed):
+def test_engine_matches_fp32_forward(pa, oracle, norm, packed):
     from vllm_lite_amd import e2e
     cfg = e2e.ModelConfig(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=32, inter=512,
                           vocab=1008, rope_theta=1e4, norm=norm)
@@ -133,6 +133,10 @@ def test_engine_matches_fp32_forward(pa, norm, packed):
     toks = torch.tensor([x for p in prompts for x in p], dtype=torch.int64, device=DEV)
     last = torch.tensor(np.cumsum(lens) - 1, device=DEV)
     got = [eng.forward(toks, last)]
+    # the engine's greedy choice (pa_argmax over the bf16 logits; rerunning
+    # the step rewrites the same cache entries) is argmax_logits of them
+    np.testing.assert_array_equal(eng.next_tokens(toks, last).cpu().numpy(),
+                                  oracle.argmax_logits(got[0].cpu().numpy()))
     steps = 5
     errs = []
     for step in range(steps + 1):

@@ -130,3 +130,48 @@ def test_linear_adds_into_residual(pa, packed):
     got = pa.linear(x, pa.ops.PackedWeight(w) if packed else w, out=out, add_to_out=True)
     assert got.data_ptr() == out.data_ptr()
     close(out, expect)
+
+
+@pytest.mark.parametrize("m,n,k,act,rms,add", [
+    (32, 896, 4864, 0, False, True),     # the decode step's down projection
+    (1, 896, 4864, 0, False, False),
+    (64, 896, 4864, 0, False, True),     # two row tiles
+    (20, 256, 2048, 0, True, False),     # RMS-in: partial sums of squares too
+    (8, 256, 4096, 1, True, False),      # SwiGLU epilogue after the split
+    (5, 48, 3072, 0, False, False),      # bias-free, 3 tiles
+])
+def test_linear_split_k(pa, m, n, k, act, rms, add):
+    # K split over workgroups (pa_linear's workspace): against fp32, twice in
+    # a row on one workspace, then again on fewer rows (a counter left
+    # non-zero would leave a tile's output unwritten or summed early); the
+    # split is independent of arrival order, so repeated calls agree bit for
+    # bit
+    ws = pa.ops.linear_workspace(64, n, k, act, DEV)
+    assert ws is not None and ws.numel() >= pa.ops.linear_workspace_size(m, n, k, act)
+    g = torch.Generator(device=DEV).manual_seed(m + n + k)
+    w = (torch.randn((2 if act else 1) * n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wp = pa.ops.PackedWeight(w)
+    for rows in (m, max(1, m // 3)):
+        x = torch.randn(rows, k, generator=g, device=DEV).to(torch.bfloat16)
+        xf = x.float()
+        if rms:
+            xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+        y = xf @ w.float().T
+        if act:
+            gg = y[:, :n].to(torch.bfloat16).float()
+            uu = y[:, n:].to(torch.bfloat16).float()
+            y = F.silu(gg) * uu
+        res = torch.randn(rows, n, generator=g, device=DEV).to(torch.bfloat16) if add else None
+        outs = []
+        for _ in range(2):
+            o = res.clone() if add else None
+            outs.append(pa.linear(x, wp, act=act, out=o, add_to_out=add,
+                                  rms_eps=1e-6 if rms else None, workspace=ws))
+        assert torch.equal(outs[0], outs[1])
+        ref = y + res.float() if add else y
+        # rms: the 1 / rms factor and the bf16 rounding of g, u add a few ulp
+        torch.testing.assert_close(outs[0].float(), ref, atol=3e-2 if (rms or add) else 2e-2,
+                                   rtol=3e-2 if rms else 1e-2)
+        nsplit = pa.ops.linear(x, wp, act=act, rms_eps=1e-6 if rms else None)
+        if not add:
+            torch.testing.assert_close(outs[0].float(), nsplit.float(), atol=2e-2, rtol=1e-2)

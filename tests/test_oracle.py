@@ -233,3 +233,30 @@ def test_quant_read_is_affine_plus_zero(oracle):
     assert np.signbit(kc[0, 0, 0, 0]) and kc[0, 0, 0, 0] == 0.0
     n, rk, rv = oracle.quant_read_kv(kc, vc, scales, [0], 1)
     assert rk[0, 0, 0].view(np.uint32) == 0 and rk[0, 0, 1] == np.float32(127.0) * scales[0]
+
+
+def test_argmax_logits_known_answers(oracle):
+    # crates/traits/src/sampling.rs:468-490
+    assert oracle.argmax_logits(np.array([1.0, 2.0, 3.0, 2.0, 1.0])) == 2
+    assert oracle.argmax_logits(np.array([-3.0, -1.0, -2.0])) == 1
+    assert oracle.argmax_logits(np.array([1.0, 1.0, 1.0, 1.0])) == 0
+    assert oracle.argmax_logits(np.zeros(0, np.float32)) == 0
+    assert oracle.argmax_logits(np.array([42.0])) == 0
+
+
+def test_argmax_logits_against_numpy(oracle):
+    # numpy's argmax takes the first maximum; with NaN mapped to -inf it is
+    # the reference's fold (NaN never compares greater, all -inf gives 0)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((40, 1000)).astype(np.float32)
+    x[1, 500] = x[1, 7] = x[1].max() + 1          # a tie: the first wins
+    x[2, :] = np.nan
+    x[3, :] = -np.inf
+    x[4, ::3] = np.nan
+    x[5, 0] = np.nan
+    x[6, :] = 0.0
+    x[6, 9] = -0.0                                 # -0 == +0: index 0 stays
+    x[7, 999] = np.inf
+    x[8] = np.round(x[8])                          # many ties
+    expect = np.argmax(np.where(np.isnan(x), -np.inf, x), axis=1)
+    np.testing.assert_array_equal(oracle.argmax_logits(x), expect)

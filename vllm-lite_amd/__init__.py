@@ -11,6 +11,7 @@ from . import _lib
 from .ops import (
     BLOCK_SIZE,
     PaError,
+    argmax,
     block_hash,
     decode,
     decode_workspace_size,
@@ -33,6 +34,7 @@ __all__ = [
     "PaError",
     "PagedKvCache",
     "StepBatch",
+    "argmax",
     "block_hash",
     "decode",
     "decode_workspace_size",

@@ -26,8 +26,11 @@ SIGNATURES = {
     "pa_rms_norm": (_i32, [_p, _p, _p, _p, _i32, _i32, _f32, _i32, _p]),
     "pa_layer_norm": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _f32, _i32, _p]),
     "pa_silu_mul": (_i32, [_p, _p, _i32, _i32, _i32, _p]),
-    "pa_linear": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p]),
+    "pa_linear": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, _sz,
+                         _i32, _p]),
+    "pa_linear_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
     "pa_linear_pack": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p]),
+    "pa_argmax": (_i32, [_p, _p, _i32, _i32, _i64, _i32, _p]),
     "pa_decode_quantized": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32,
                                    _i32, _i32, _f32, _p, _sz, _p]),
     "pa_prefill_quantized": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32,

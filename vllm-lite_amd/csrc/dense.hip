@@ -1,7 +1,8 @@
 // Dense-side kernels of an end-to-end decoder step (pa_dense.h): residual
-// add + RMSNorm or LayerNorm, and the SwiGLU activation.  All are HBM-bound
-// row passes.
+// add + RMSNorm or LayerNorm, the SwiGLU activation, skinny-M projections and
+// the greedy argmax over logit rows.  All are HBM-bound.
 #include <algorithm>
+#include <climits>
 
 #include "pa_common.hpp"
 #include "../../include/pa_dense.h"
@@ -126,13 +127,18 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(T* __restrict__ out,
 template <int EPI, int NT, bool PK, int U>
 __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const uint16_t* __restrict__ bias, int M, int N, int K, int kw, int flags, float eps) {
+    const uint16_t* __restrict__ bias, int M, int N, int K, int kw, int flags, float eps,
+    float* __restrict__ ws, int* __restrict__ counters) {
   static_assert(EPI != 2 || NT == 2, "SwiGLU pairs one gate and one up tile");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, j = lane >> 4;
   const int nsteps = K / 32;
-  const int s0 = wave * nsteps / kw, s1 = (wave + 1) * nsteps / kw;
+  // K split: workgroup z of gridDim.z takes steps [k0, k1), its wavefronts
+  // an equal share each
+  const int splits = gridDim.z;
+  const int k0 = blockIdx.z * nsteps / splits, k1 = (blockIdx.z + 1) * nsteps / splits;
+  const int s0 = k0 + wave * (k1 - k0) / kw, s1 = k0 + (wave + 1) * (k1 - k0) / kw;
   const int m0 = blockIdx.y * 32;
   const int n0 = blockIdx.x * (EPI == 2 ? 16 : 16 * NT);
   // Weight fragment of tile t (16 rows from row r0) at step s:
@@ -232,16 +238,72 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
   } else if (rms) {
     __syncthreads();
   }
+  float ssum[2] = {0.f, 0.f};  // sums of squares of batch rows c, 16 + c
+  if (rms) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      for (int v = 0; v < kw; ++v) ssum[q] += rss[v][q][c];
+  }
+  if (splits > 1) {
+    // Split K: the workgroup's partial tile (and sums of squares) goes to
+    // its record in the workspace; the last of the tile's `splits`
+    // workgroups to arrive (counted by a device-scope atomic) sums the
+    // records in split order, so the result does not depend on the arrival
+    // order, applies the epilogue and sets the counter back to zero for the
+    // next call.
+    // The records cross workgroups on other XCDs, whose L2s are not
+    // coherent with this one.  They are written and read as device-scope
+    // relaxed atomics (stores written through, loads that miss the
+    // non-coherent cache levels), and the stores have completed
+    // (vmcnt(0)) before the counter increment is issued; the reads are
+    // issued after the increment's result, on which they depend, has
+    // returned.  That orders them without the release / acquire fences,
+    // which would write back and invalidate this XCD's whole L2 (measured
+    // at ~5 us per call).
+    constexpr int RECF = 2 * NT * 256 + 32;  // floats per record
+    const int64_t tile = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    float* mine = ws + (tile * splits + blockIdx.z) * RECF;
+    auto put = [](float* p, float v) {
+      __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto get = [](const float* p) {
+      return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+#pragma unroll
+    for (int q = 0; q < 2 * NT; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) put(mine + (q * 64 + lane) * 4 + r, acc[q >> 1][q & 1][r]);
+    if (j == 0) {
+      put(mine + 2 * NT * 256 + c, ssum[0]);
+      put(mine + 2 * NT * 256 + 16 + c, ssum[1]);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int arrived = 0;
+    if (lane == 0)
+      arrived = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+    if (__builtin_amdgcn_readfirstlane(arrived) != splits - 1) return;
+#pragma unroll
+    for (int q = 0; q < 2 * NT; ++q) acc[q >> 1][q & 1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    ssum[0] = ssum[1] = 0.f;
+    for (int z = 0; z < splits; ++z) {
+      const float* rec = ws + (tile * splits + z) * RECF;
+#pragma unroll
+      for (int q = 0; q < 2 * NT; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[q >> 1][q & 1][r] += get(rec + (q * 64 + lane) * 4 + r);
+      ssum[0] += get(rec + 2 * NT * 256 + c);
+      ssum[1] += get(rec + 2 * NT * 256 + 16 + c);
+    }
+    if (lane == 0)
+      __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   // 1 / rms of the batch rows (1 without PA_LINEAR_RMS_IN); the norm weight
   // is folded into the packed weight's columns
   float inv[2] = {1.f, 1.f};
   if (rms) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      float t = 0.f;
-      for (int v = 0; v < kw; ++v) t += rss[v][q][c];
-      inv[q] = 1.0f / sqrtf(t / (float)K + eps);
-    }
+    for (int q = 0; q < 2; ++q) inv[q] = 1.0f / sqrtf(ssum[q] / (float)K + eps);
   }
   const bool add_out = (flags & PA_LINEAR_ADD_OUT) != 0;
 #pragma unroll
@@ -313,6 +375,92 @@ __global__ __launch_bounds__(256) void linear_pack_kernel(uint16_t* __restrict__
   }
 }
 
+
+// Greedy token choice over logit rows, argmax_logits's rule
+// (crates/traits/src/sampling.rs:439-453): the first index holding the
+// largest value; NaN never wins; a row with no value above -inf (or no
+// columns) gives 0.  One workgroup of 1024 threads per row.  A thread scans
+// its elements in increasing index order keeping the first strict maximum,
+// then (value, index) pairs are combined by larger value, ties to the
+// smaller index, across the wavefront by lane shuffles and across the
+// wavefronts in LDS.  VEC: elements per load (8 bf16 or 4 f32 = 16 bytes,
+// when the rows are 16-byte aligned; else 1).
+constexpr int kArgmaxThreads = 1024;
+template <typename T, int VEC>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int64_t* __restrict__ out,
+                                                                const T* __restrict__ x,
+                                                                int cols, int64_t row_stride) {
+  const T* row = x + (int64_t)blockIdx.x * row_stride;
+  float best = -INFINITY;
+  int bi = INT_MAX;
+  const int nv = cols / VEC;
+  constexpr int UN = 4;  // loads in flight per thread
+  for (int v0 = threadIdx.x; v0 < nv; v0 += UN * kArgmaxThreads) {
+    float e[UN][VEC];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int v = v0 + u * kArgmaxThreads;
+      if (v < nv) {
+        if constexpr (VEC == 1) {
+          e[u][0] = Elem<T>::load(row + v);
+        } else {
+          typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+          const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row) + v);
+          const uint32_t wd[4] = {w[0], w[1], w[2], w[3]};
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            if constexpr (sizeof(T) == 2)
+              e[u][i] = bf16_bits_to_f32((uint16_t)(wd[i / 2] >> (16 * (i & 1))));
+            else
+              e[u][i] = __uint_as_float(wd[i]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) e[u][i] = -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i)
+        if (e[u][i] > best) {
+          best = e[u][i];
+          bi = (v0 + u * kArgmaxThreads) * VEC + i;
+        }
+  }
+  // columns past the last whole vector (VEC > 1 and cols % VEC != 0 never
+  // happens: the host takes VEC = 1 then)
+  auto better = [](float v, int i, float bv, int bj) {
+    return v > bv || (v == bv && i < bj);
+  };
+#pragma unroll
+  for (int w = 32; w > 0; w >>= 1) {
+    const float ov = __shfl_xor(best, w, 64);
+    const int oi = __shfl_xor(bi, w, 64);
+    if (better(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float sv[kArgmaxThreads / 64];
+  __shared__ int si[kArgmaxThreads / 64];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgmaxThreads / 64; ++w)
+      if (better(sv[w], si[w], best, bi)) {
+        best = sv[w];
+        bi = si[w];
+      }
+    out[blockIdx.x] = bi == INT_MAX ? 0 : bi;
+  }
+}
+
 }  // namespace
 }  // namespace pa
 
@@ -376,10 +524,65 @@ extern "C" int32_t pa_silu_mul(void* out, const void* gate_up, int32_t rows, int
   return check_launch("pa_silu_mul");
 }
 
+namespace {
+// Launch shape of pa_linear.
+//   nt: weight tiles per wavefront: 4 for wide outputs (each X fragment then
+//       feeds 4 tiles), 1 where 2 would leave fewer than ~512 wavefronts,
+//       else 2.
+//   splits: workgroups sharing a tile's K range (needs the workspace): for
+//       long K (>= 2048) and fewer than 128 tiles, enough to give ~256
+//       workgroups, at most 8 and at least 16 steps each.
+//   kw: wavefronts per workgroup splitting its K range: NT = 1 runs up to 16,
+//       with one stage of 8 steps when the range is short and stages of 4
+//       otherwise; NT > 1 up to 8 wavefronts of about 8 steps (two stages of 4).
+struct LinearPlan {
+  int nt, kw, stage, splits;
+  dim3 grid;
+};
+LinearPlan linear_plan(int rows, int n, int k, int act, bool can_split) {
+  LinearPlan p{2, 1, 4, 1, dim3(1)};
+  const int nsteps = k / 32;
+  const int kw0 = std::max(1, std::min(8, (nsteps + 7) / 8));
+  if (act != PA_ACT_SILU_MUL) {
+    if ((n + 63) / 64 >= 1024) p.nt = 4;
+    else if ((long long)((n + 31) / 32) * kw0 < 512) p.nt = 1;
+  }
+  const int cols = act == PA_ACT_SILU_MUL ? 16 : 16 * p.nt;
+  const long long tiles = (long long)((n + cols - 1) / cols) * ((rows + 31) / 32);
+  if (can_split && nsteps >= 64 && tiles < 128)
+    p.splits = (int)std::max(1LL, std::min({8LL, 256 / tiles, (long long)nsteps / 16}));
+  const int steps = (nsteps + p.splits - 1) / p.splits;  // per workgroup
+  p.kw = std::max(1, std::min(8, (steps + 7) / 8));
+  if (p.nt == 1) {
+    if (steps <= 64)
+      p.stage = 8;
+    else
+      p.kw = std::min(16, (steps + 7) / 8);
+  }
+  p.grid = dim3((n + cols - 1) / cols, (rows + 31) / 32, p.splits);
+  return p;
+}
+// Workspace bytes of a split plan: one counter per tile (256-byte aligned
+// block), then one record per (tile, split) of 2 NT x 64 partial f32x4 plus
+// 32 sums of squares.
+size_t linear_ws_bytes(const LinearPlan& p) {
+  if (p.splits <= 1) return 0;
+  const size_t tiles = (size_t)p.grid.x * p.grid.y;
+  const size_t counters = (tiles * sizeof(int) + 255) / 256 * 256;
+  return counters + tiles * p.splits * (2 * p.nt * 256 + 32) * sizeof(float);
+}
+}  // namespace
+
+extern "C" size_t pa_linear_workspace_size(int32_t rows, int32_t out_features,
+                                           int32_t in_features, int32_t act) {
+  if (rows <= 0 || out_features <= 0 || in_features < 32) return 0;
+  return linear_ws_bytes(linear_plan(rows, out_features, in_features, act, true));
+}
+
 extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const void* bias,
                              int32_t rows, int32_t out_features, int32_t in_features, int32_t act,
-                             int32_t packed, int32_t flags, float eps, int32_t dtype,
-                             pa_stream_t stream) {
+                             int32_t packed, int32_t flags, float eps, void* workspace,
+                             size_t workspace_bytes, int32_t dtype, pa_stream_t stream) {
   clear_error();
   PA_REQUIRE(dtype == PA_DTYPE_BF16, PA_ERR_UNSUPPORTED, "pa_linear: dtype %d (bf16 only)", dtype);
   PA_REQUIRE(act == PA_ACT_NONE || act == PA_ACT_SILU_MUL, PA_ERR_INVALID_ARG,
@@ -403,28 +606,21 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   PA_REQUIRE(((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out) % 16 == 0, PA_ERR_INVALID_ARG,
              "pa_linear: x, weight and out must be 16-byte aligned");
   PA_REQUIRE((rows + 31) / 32 <= 65535, PA_ERR_UNSUPPORTED, "pa_linear: %d rows", rows);
-  // Weight tiles per wavefront: 4 for wide outputs (each X fragment then
-  // feeds 4 tiles), 1 where 2 would leave fewer than ~512 wavefronts, else 2.
-  // K split: NT = 1 runs up to 16 wavefronts per workgroup, with one stage of
-  // 8 steps when K is short and stages of 4 otherwise; NT > 1 up to 8
-  // wavefronts of about 8 steps (two stages of 4).
-  const int nsteps = in_features / 32;
-  int kw = std::max(1, std::min(8, (nsteps + 7) / 8));
-  int nt = 2;
-  if (act != PA_ACT_SILU_MUL) {
-    if ((out_features + 63) / 64 >= 1024) nt = 4;
-    else if ((long long)((out_features + 31) / 32) * kw < 512) nt = 1;
-  }
-  int stage = 4;
-  if (nt == 1) {
-    if (nsteps <= 64) {
-      stage = 8;
-    } else {
-      kw = std::min(16, (nsteps + 7) / 8);
-    }
-  }
-  const int cols = act == PA_ACT_SILU_MUL ? 16 : 16 * nt;
-  const dim3 grid((out_features + cols - 1) / cols, (rows + 31) / 32);
+  // The split plan when the workspace holds it, else one workgroup per tile.
+  LinearPlan plan = linear_plan(rows, out_features, in_features, act, true);
+  const size_t ws_need = linear_ws_bytes(plan);
+  if (ws_need == 0 || !workspace || workspace_bytes < ws_need)
+    plan = linear_plan(rows, out_features, in_features, act, false);
+  else
+    PA_REQUIRE((uintptr_t)workspace % 256 == 0, PA_ERR_INVALID_ARG,
+               "pa_linear: workspace must be 256-byte aligned");
+  const int nt = plan.nt, kw = plan.kw, stage = plan.stage;
+  const dim3 grid = plan.grid;
+  int* counters = (int*)workspace;
+  float* ws = plan.splits > 1
+                  ? (float*)((char*)workspace +
+                             ((size_t)grid.x * grid.y * sizeof(int) + 255) / 256 * 256)
+                  : nullptr;
   hipStream_t s = (hipStream_t)stream;
   auto* o = (uint16_t*)out;
   auto* xx = (const uint16_t*)x;
@@ -432,9 +628,9 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   auto* bb = (const uint16_t*)bias;
 #define PA_LAUNCH_LINEAR_U(EPI, NT, UU)                                                       \
   (packed ? linear_skinny_kernel<EPI, NT, true, UU><<<grid, 64 * kw, 0, s>>>(                  \
-                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps)               \
+                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps, ws, counters) \
           : linear_skinny_kernel<EPI, NT, false, UU><<<grid, 64 * kw, 0, s>>>(                 \
-                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps))
+                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps, ws, counters))
 #define PA_LAUNCH_LINEAR(EPI, NT)                                                             \
   (NT == 1 && stage == 8 ? PA_LAUNCH_LINEAR_U(EPI, 1, 8) : PA_LAUNCH_LINEAR_U(EPI, NT, 4))
   if (act == PA_ACT_SILU_MUL)
@@ -464,4 +660,36 @@ extern "C" int32_t pa_linear_pack(void* packed, const void* weight, const void* 
   linear_pack_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
       (uint16_t*)packed, (const uint16_t*)weight, (const uint16_t*)col_scale, rows, cols);
   return check_launch("pa_linear_pack");
+}
+
+extern "C" int32_t pa_argmax(int64_t* out, const void* logits, int32_t rows, int32_t cols,
+                             int64_t row_stride, int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype_ok(dtype), PA_ERR_INVALID_ARG, "pa_argmax: unknown dtype %d", dtype);
+  PA_REQUIRE(rows >= 0 && cols >= 0, PA_ERR_INVALID_ARG, "pa_argmax: bad sizes");
+  if (row_stride == 0) row_stride = cols;
+  PA_REQUIRE(row_stride >= cols, PA_ERR_INVALID_ARG,
+             "pa_argmax: row stride %lld below cols %d", (long long)row_stride, cols);
+  if (rows == 0) return PA_OK;
+  PA_REQUIRE(out && (logits || cols == 0), PA_ERR_INVALID_ARG, "pa_argmax: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int esz = dtype == PA_DTYPE_BF16 ? 2 : 4;
+  const bool vec = (uintptr_t)logits % 16 == 0 && (row_stride * esz) % 16 == 0 &&
+                   (cols * esz) % 16 == 0;
+  if (dtype == PA_DTYPE_BF16) {
+    if (vec)
+      argmax_kernel<uint16_t, 8><<<rows, kArgmaxThreads, 0, s>>>(out, (const uint16_t*)logits,
+                                                                 cols, row_stride);
+    else
+      argmax_kernel<uint16_t, 1><<<rows, kArgmaxThreads, 0, s>>>(out, (const uint16_t*)logits,
+                                                                 cols, row_stride);
+  } else {
+    if (vec)
+      argmax_kernel<float, 4><<<rows, kArgmaxThreads, 0, s>>>(out, (const float*)logits, cols,
+                                                              row_stride);
+    else
+      argmax_kernel<float, 1><<<rows, kArgmaxThreads, 0, s>>>(out, (const float*)logits, cols,
+                                                              row_stride);
+  }
+  return check_launch("pa_argmax");
 }

@@ -18,11 +18,12 @@ StepBatch per engine step, and per layer
 Projections of batches of at most SKINNY_ROWS rows (decode steps, the LM head
 over the last tokens) run in pa_linear over weights repacked once at load
 time (pa_linear_pack: every MFMA operand fragment one contiguous kilobyte);
-larger batches (prefill chunks) and the long-K down projection, for which
-hipBLASLt's split-K GEMM is faster (9.5 vs 14.9 us measured), run in
-hipBLASLt (torch.nn.functional.linear).  With RMSNorm and weights packed with
-the norm weights folded in (Weights.pack()), a decode step runs the fused
-layer of Engine._forward_fused: five launches per layer.
+larger batches (prefill chunks) run in hipBLASLt (torch.nn.functional.linear),
+and so does the long-K down projection of the unfused path.  With RMSNorm and
+weights packed with the norm weights folded in (Weights.pack()), a decode step
+runs the fused layer of Engine._forward_fused: five launches per layer, the
+down projection split over K (pa_linear's workspace) and added into the
+residual stream in its epilogue.
 The norm is chosen explicitly by ModelConfig.norm: "rms" (RMSNorm, what the
 benchmark configuration states) or "layer" (the zero-bias LayerNorm the
 reference's CausalLm constructs for these models,
@@ -104,7 +105,8 @@ class Weights:
                   "q": [(x[:nq], g) for x, g in zip(self.wqkv, ln1)],
                   "kv": [(x[nq:], g) for x, g in zip(self.wqkv, ln1)],
                   "o": [(x, None) for x in self.wo],
-                  "gu": [(x, g) for x, g in zip(self.wgu, ln2)]}
+                  "gu": [(x, g) for x, g in zip(self.wgu, ln2)],
+                  "down": [(x, None) for x in self.wd]}
         p = {name: [ops.PackedWeight(x, col_scale=g) for x, g in ws]
              for name, ws in blocks.items() if all(fits(x) for x, _ in ws)}
         if fits(self.embed):
@@ -139,10 +141,26 @@ class Engine:
         if cfg.norm not in ("rms", "layer"):
             raise ValueError(f"unknown norm {cfg.norm!r}")
         self._norm = ops.rms_norm if cfg.norm == "rms" else ops.layer_norm
+        # pa_linear's K split of the down projection (the one long-K
+        # projection), sized for every skinny batch; zeroed once here, every
+        # call leaves it zeroed
+        ws = max(ops.linear_workspace_size(r, cfg.hidden, cfg.inter)
+                 for r in range(1, SKINNY_ROWS + 1))
+        self.linear_ws = (torch.zeros(ws, dtype=torch.uint8, device=self.device)
+                          if ws else None)
 
     def forward(self, tokens, logit_rows):
         """One step over the prepared batch: tokens [T] (int64, device) ->
         logits of the rows logit_rows [R, vocab] (f32)."""
+        return self._logits(tokens, logit_rows).float()
+
+    def next_tokens(self, tokens, logit_rows):
+        """Greedy next token of each row of logit_rows (int64 [R]): pa_argmax
+        over the bf16 logits, argmax_logits's rule."""
+        return ops.argmax(self._logits(tokens, logit_rows))
+
+    def _logits(self, tokens, logit_rows):
+        """forward's logits in the model dtype (bf16)."""
         c, w = self.cfg, self.w
         t = tokens.shape[0]
         hq, hkv, d = c.heads, c.kv_heads, c.head_dim
@@ -186,17 +204,17 @@ class Engine:
         self._norm(x, w.norm, c.eps, add=add, out=h)
         rows = h[logit_rows]
         if rows.shape[0] <= SKINNY_ROWS and ops.linear_supports(rows, w.embed):
-            return ops.linear(rows, pk.get("lm_head", w.embed)).float()
-        return F.linear(rows, w.embed).float()
+            return ops.linear(rows, pk.get("lm_head", w.embed))
+        return F.linear(rows, w.embed)
 
     def _forward_fused(self, tokens, logit_rows):
         """Decode-step forward with the RMSNorms folded into the projections:
         per layer the fused QKV projection (pa_linear normalising its input
         rows, ln1 folded into the packed weight; attention reads q, k, v as
         strided views of its rows), attention, O added into the residual
-        stream in place, gate|up + SwiGLU (ln2 folded), down added into the
-        residual stream by hipBLASLt (beta = 1); the final norm is folded into
-        the LM head.  Five launches per layer instead of nine."""
+        stream in place, gate|up + SwiGLU (ln2 folded), down (K split over
+        workgroups) added into the residual stream; the final norm is folded
+        into the LM head.  Five launches per layer instead of nine."""
         c, w, pk = self.cfg, self.w, self.w.packed
         t = tokens.shape[0]
         hq, hkv, d = c.heads, c.kv_heads, c.head_dim
@@ -211,9 +229,13 @@ class Engine:
             attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq, self.scale)
             ops.linear(attn.view(t, nq), pk["o"][layer], out=x, add_to_out=True)
             act = ops.linear(x, pk["gu"][layer], act=ops.ACT_SILU_MUL, rms_eps=c.eps)
-            x.addmm_(act, w.wd[layer].t())
+            if "down" in pk:
+                ops.linear(act, pk["down"][layer], out=x, add_to_out=True,
+                           workspace=self.linear_ws)
+            else:
+                x.addmm_(act, w.wd[layer].t())
         rows = x[logit_rows].contiguous()
-        return ops.linear(rows, pk["lm_head"], rms_eps=c.eps).float()
+        return ops.linear(rows, pk["lm_head"], rms_eps=c.eps)
 
     def generate(self, prompts, max_new):
         """Greedy generation for every prompt (lists of token ids).  Returns
@@ -233,7 +255,7 @@ class Engine:
             tokens = torch.tensor([x for p in prompts for x in p], dtype=torch.int64,
                                   device=self.device)
             last = torch.tensor([sum(lens[:i + 1]) - 1 for i in range(b)], device=self.device)
-            nxt = self.forward(tokens, last).argmax(-1)
+            nxt = self.next_tokens(tokens, last)
             out = [nxt]
             torch.cuda.synchronize(self.device)
             t1 = time.perf_counter()
@@ -244,13 +266,13 @@ class Engine:
                 self.batch.prepare(self.cache, [1] * b, [n + step - 1 for n in lens], blocks)
                 if not self.graph or step == 1:
                     # eager (also the warm-up of every launch the graph records)
-                    nxt = self.forward(nxt, rows).argmax(-1)
+                    nxt = self.next_tokens(nxt, rows)
                 else:
                     if graph is None:
                         static_tok = nxt.clone()
                         graph = torch.cuda.CUDAGraph()
                         with torch.cuda.graph(graph):
-                            static_out = self.forward(static_tok, rows).argmax(-1)
+                            static_out = self.next_tokens(static_tok, rows)
                     else:
                         static_tok.copy_(nxt)
                     graph.replay()

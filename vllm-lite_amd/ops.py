@@ -338,6 +338,25 @@ def silu_mul(gate_up, out=None):
     return out
 
 
+def argmax(logits, out=None):
+    """pa_argmax: greedy token ids of logit rows [rows, vocab] (bf16 or f32,
+    unit stride along the vocab) -> int64 [rows]; the first index of the
+    largest value, NaN never chosen, 0 for a row with nothing above -inf
+    (argmax_logits, crates/traits/src/sampling.rs:439-453)."""
+    if not logits.is_cuda:
+        raise ValueError("argmax: expected a device tensor")
+    if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):
+        raise ValueError("argmax: logits must be [rows, vocab] with unit column stride")
+    rows, cols = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    lib = _lib.load()
+    _check("pa_argmax", lib.pa_argmax(_ptr(out), _ptr(logits), rows, cols,
+                                      logits.stride(0) if rows > 1 else cols,
+                                      _dtype_code(logits), _stream(logits)))
+    return out
+
+
 ACT_NONE, ACT_SILU_MUL = 0, 1
 LINEAR_RMS_IN, LINEAR_ADD_OUT = 1, 2
 
@@ -370,12 +389,30 @@ class PackedWeight:
             _dtype_code(weight), _stream(weight)))
 
 
-def linear(x, weight, bias=None, act=ACT_NONE, out=None, rms_eps=None, add_to_out=False):
+def linear_workspace_size(rows, n, k, act=ACT_NONE):
+    """pa_linear_workspace_size: bytes of pa_linear's K-split workspace for
+    this shape (0: the shape does not split)."""
+    return _lib.load().pa_linear_workspace_size(rows, n, k, act)
+
+
+def linear_workspace(rows, n, k, act=ACT_NONE, device="cuda"):
+    """A zeroed workspace for pa_linear's K split at this shape (uint8 device
+    tensor), or None when the shape does not split.  One workspace serves
+    any number of calls that run one after another (each leaves its
+    counters zero), e.g. every layer of a model, if it is sized for the
+    largest of them."""
+    nbytes = linear_workspace_size(rows, n, k, act)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
+def linear(x, weight, bias=None, act=ACT_NONE, out=None, rms_eps=None, add_to_out=False,
+           workspace=None):
     """pa_linear: x [rows, K] bf16, weight [N, K] (or the fused gate|up
     [2 N, K] with act=ACT_SILU_MUL), row-major or a PackedWeight -> out
     [rows, N] bf16.  rms_eps: RMS-normalise the rows of x on the fly (the
     norm weight folded into a PackedWeight's col_scale); add_to_out: out is
-    the residual stream, updated in place with the result."""
+    the residual stream, updated in place with the result; workspace: from
+    linear_workspace (K split over several workgroups per tile) or None."""
     packed = isinstance(weight, PackedWeight)
     wt = weight.data if packed else weight
     _dev(x, wt)
@@ -391,11 +428,17 @@ def linear(x, weight, bias=None, act=ACT_NONE, out=None, rms_eps=None, add_to_ou
         if add_to_out:
             raise ValueError("add_to_out needs out")
         out = torch.empty(rows, n, dtype=x.dtype, device=x.device)
+    if workspace is not None:
+        _dev(workspace)
+        if workspace.dtype != torch.uint8:
+            raise ValueError("workspace: expected a uint8 tensor from linear_workspace")
     flags = (LINEAR_RMS_IN if rms_eps is not None else 0) | (LINEAR_ADD_OUT if add_to_out else 0)
     lib = _lib.load()
     _check("pa_linear", lib.pa_linear(_ptr(out), _ptr(x), _ptr(wt),
                                       _ptr(bias) if bias is not None else None, rows, n, k, act,
                                       1 if packed else 0, flags,
                                       float(rms_eps) if rms_eps is not None else 0.0,
+                                      _ptr(workspace) if workspace is not None else None,
+                                      workspace.numel() if workspace is not None else 0,
                                       _dtype_code(x), _stream(x)))
     return out
