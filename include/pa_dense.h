@@ -103,6 +103,37 @@ size_t pa_linear_workspace_size(int32_t rows, int32_t out_features, int32_t in_f
 int32_t pa_linear_pack(void* packed, const void* weight, const void* col_scale, int32_t rows,
                        int32_t cols, int32_t dtype, pa_stream_t stream);
 
+/* The decode step's QKV projection with RoPE and the KV-cache write fused
+ * into its epilogue: pa_linear (bf16, act none, optional PA_LINEAR_RMS_IN and
+ * bias) over a weight packed by pa_linear_pack_qkv, followed in the same pass
+ * by what pa_rope_reshape_and_cache does to its output
+ * (crates/model/src/components/attention/rope_gqa.rs:280-302,
+ * crates/model/src/components/positional/rope.rs:335-568):
+ *   out [rows, (num_heads + 2 num_kv_heads) head_dim]: the projection, q and k
+ *       columns rotated by position (inv_freq [head_dim / 2], positions [rows]),
+ *       v columns as projected; identical to pa_linear followed by
+ *       pa_rope_reshape_and_cache on the q / k / v views of its output;
+ *   k_cache / v_cache: token r's rotated k and its v written to slot
+ *       slot_mapping[r] (skipped when outside [0, num_blocks * 16)).
+ * head_dim and in_features multiples of 32; flags 0 or PA_LINEAR_RMS_IN.
+ * weight, bias: the fused QKV weight [(Hq + 2 Hkv) head_dim, in_features]
+ * (bias in the original row order).  No reference counterpart as one call. */
+int32_t pa_linear_rope_cache(void* out, const void* x, const void* weight, const void* bias,
+                             int32_t rows, int32_t num_heads, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t in_features, int32_t flags, float eps,
+                             const int64_t* positions, const int64_t* slot_mapping,
+                             const float* inv_freq, void* k_cache, void* v_cache,
+                             int32_t num_blocks, int32_t dtype, pa_stream_t stream);
+
+/* pa_linear_pack for pa_linear_rope_cache's weight: the fused QKV weight
+ * [(num_heads + 2 num_kv_heads) head_dim, cols], with the rows of each query
+ * and key head reordered so that the two members (i, i + head_dim / 2) of
+ * each rotation pair land in the same wavefront; col_scale as pa_linear_pack.
+ * No reference counterpart: a load-time layout step. */
+int32_t pa_linear_pack_qkv(void* packed, const void* weight, const void* col_scale,
+                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t cols, int32_t dtype, pa_stream_t stream);
+
 /* Greedy sampling's argmax_logits (crates/traits/src/sampling.rs:439-453) on
  * every row of a logit matrix: out[r] = the first column holding the row's
  * largest value, comparing with `>` from -inf, so NaN never wins and a row

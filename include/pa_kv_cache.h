@@ -133,6 +133,18 @@ int32_t pa_batch_set_capacity(pa_batch* batch, int32_t max_context_len);
 /* 1 when every sequence is a single-token decode step. */
 int32_t pa_batch_is_decode(const pa_batch* batch);
 
+/* The prepared batch's fused QKV projection of one layer with RoPE and the
+ * KV-cache write in its epilogue: pa_linear_rope_cache with the batch's
+ * positions and slots and the layer's caches (bf16 cache, rows = the batch's
+ * token count).  out [T, (Hq + 2 Hkv) D]: rotated q (and k), v; pass its q
+ * view to pa_batch_attention with key = value = NULL.  weight from
+ * pa_linear_pack_qkv; flags 0 or PA_LINEAR_RMS_IN (x's rows normalised on
+ * the fly, the norm weight folded into the packed weight). */
+int32_t pa_batch_qkv_rope_cache(pa_batch* batch, pa_kv_cache* cache, int32_t layer,
+                                int32_t num_heads, void* out, const void* x, const void* weight,
+                                const void* bias, int32_t in_features, int32_t flags, float eps,
+                                const float* inv_freq, pa_stream_t stream);
+
 /* One layer's attention for the prepared batch: writes the step's K / V
  * into the cache (rotating K, and q in place, when inv_freq is non-NULL),
  * then attends with pa_decode (all-decode batch) or pa_prefill (anything
@@ -141,6 +153,8 @@ int32_t pa_batch_is_decode(const pa_batch* batch);
  *   [T, Hkv, D], each with a token stride in elements (0 = contiguous; q, k
  *   and v may be views of one fused QKV projection output), inv_freq [D/2]
  *   device f32 or NULL, scale = attn_factor / sqrt(D).
+ * key == value == NULL (and inv_freq NULL): the step's K / V are already in
+ * the cache and q is final (pa_batch_qkv_rope_cache ran); attention only.
  * Allocates (once, grown on demand) the decode workspace. */
 int32_t pa_batch_attention(pa_batch* batch, pa_kv_cache* cache, int32_t layer, int32_t num_heads,
                            void* q, int64_t q_stride, const void* key, int64_t key_stride,

@@ -82,6 +82,15 @@ def test_argument_errors_without_gpu(lib):
     assert lib.pa_linear(null, null, null, null, 0, 64, 96, 0, 0, 0, 0.0, null, 0, 1, null) == 0
     assert lib.pa_linear(p, p, p, null, 4, 64, 96, 1, 0, 2, 0.0, null, 0, 1, null) == -1  # add + SwiGLU
     assert lib.pa_linear(p, p, p, null, 4, 64, 96, 0, 0, 1, 0.0, null, 0, 1, null) == -1  # rms, eps 0
+    # pa_linear_rope_cache / pa_linear_pack_qkv: f32, head_dim not a multiple of 32,
+    # the residual-add flag
+    assert lib.pa_linear_rope_cache(p, p, p, null, 4, 8, 2, 64, 128, 0, 0.0, p, p, p, p, p, 8,
+                                    0, null) == -3
+    assert lib.pa_linear_rope_cache(p, p, p, null, 4, 8, 2, 48, 128, 0, 0.0, p, p, p, p, p, 8,
+                                    1, null) == -3
+    assert lib.pa_linear_rope_cache(p, p, p, null, 4, 8, 2, 64, 128, 2, 0.0, p, p, p, p, p, 8,
+                                    1, null) == -1
+    assert lib.pa_linear_pack_qkv(p, C.c_void_p(32), null, 8, 2, 48, 128, 1, null) == -3
     # pa_linear's K split: long K over few tiles only; a workspace not 256-byte aligned
     assert lib.pa_linear_workspace_size(32, 896, 4864, 0) > 0
     assert lib.pa_linear_workspace_size(32, 896, 896, 0) == 0

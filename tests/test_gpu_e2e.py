@@ -170,3 +170,26 @@ def test_graph_replay_matches_eager(pa):
     eager, _ = e2e.Engine(cfg, w, 96, DEV, graph=False).generate(prompts, 12)
     graphed, _ = e2e.Engine(cfg, w, 96, DEV, graph=True).generate(prompts, 12)
     assert torch.equal(eager, graphed)
+
+
+def test_fused_qkv_rope_step_matches_unfused(pa):
+    # the QKV projection with RoPE and the KV write in its epilogue gives the
+    # same logits, bit for bit, as the projection followed by the separate
+    # RoPE + KV-write kernel (same bf16 values, same rotation)
+    from vllm_lite_amd import e2e
+    cfg = e2e.ModelConfig(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=32, inter=512,
+                          vocab=1008, rope_theta=1e4)
+    w = e2e.Weights(cfg, seed=11, device=DEV)
+    w.pack()
+    assert "qkv_rope" in w.packed
+    rng = np.random.default_rng(5)
+    prompts = [list(rng.integers(0, cfg.vocab, n)) for n in (9, 17, 3)]
+    runs = []
+    for fused in (True, False):
+        if not fused:
+            del w.packed["qkv_rope"]
+        eng = e2e.Engine(cfg, w, 64, DEV, graph=False)
+        gen, _ = eng.generate(prompts, 6)
+        runs.append(gen)
+    assert torch.equal(runs[0], runs[1])
+

@@ -175,3 +175,55 @@ def test_linear_split_k(pa, m, n, k, act, rms, add):
         nsplit = pa.ops.linear(x, wp, act=act, rms_eps=1e-6 if rms else None)
         if not add:
             torch.testing.assert_close(outs[0].float(), nsplit.float(), atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("rows,hq,hkv,d,k", [(32, 14, 2, 64, 896), (5, 32, 8, 128, 256),
+                                             (40, 4, 4, 64, 64), (1, 8, 2, 32, 128)])
+@pytest.mark.parametrize("rms,with_bias", [(True, True), (False, False)])
+def test_linear_rope_cache_matches_unfused(pa, rows, hq, hkv, d, k, rms, with_bias):
+    # pa_linear_rope_cache == pa_linear on the row-major-packed weight, then
+    # pa_rope_reshape_and_cache on the q / k / v views of its output: the
+    # same bf16 projection values, the same rotation, the same cache writes
+    # (bit for bit), one slot outside the pool skipped, untouched slots zero
+    n = (hq + 2 * hkv) * d
+    g = torch.Generator(device=DEV).manual_seed(rows * 3 + hq + d + k)
+    x = torch.randn(rows, k, generator=g, device=DEV).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.05).to(torch.bfloat16)
+    bias = (torch.randn(n, generator=g, device=DEV) * 0.1).to(torch.bfloat16) if with_bias \
+        else None
+    gamma = (1 + 0.1 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16) if rms \
+        else None
+    nb = 8
+    positions = torch.randint(0, 4000, (rows,), generator=g, device=DEV)
+    slots = torch.randperm(nb * 16, generator=g, device=DEV)[:rows].clone()
+    slots[rows // 2] = -1 if rows > 1 else slots[0]
+    inv_freq = torch.from_numpy(pa.rope_inv_freq(d, 1e6)).to(DEV)
+    eps = 1e-6 if rms else None
+
+    kc0 = torch.zeros(nb, hkv, 16, d, dtype=torch.bfloat16, device=DEV)
+    vc0 = torch.zeros(nb, hkv, d, 16, dtype=torch.bfloat16, device=DEV)
+    ref = pa.linear(x, pa.ops.PackedWeight(w, col_scale=gamma), bias, rms_eps=eps)
+    q = ref[:, :hq * d].view(rows, hq, d)
+    kk = ref[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
+    vv = ref[:, (hq + hkv) * d:].view(rows, hkv, d)
+    pa.rope_reshape_and_cache(q, kk, vv, kc0, vc0, slots, positions, inv_freq)
+
+    kc1 = torch.zeros_like(kc0)
+    vc1 = torch.zeros_like(vc0)
+    wq = pa.ops.PackedWeight(w, col_scale=gamma, rope_heads=(hq, hkv, d))
+    got = pa.ops.linear_rope_cache(x, wq, bias, positions, slots, inv_freq, kc1, vc1,
+                                   rms_eps=eps)
+    # q rotated in place by the unfused path; k columns of ref are unrotated
+    # there (rotated on their way into the cache), v as projected
+    assert torch.equal(got[:, :hq * d], ref[:, :hq * d])
+    assert torch.equal(got[:, (hq + hkv) * d:], ref[:, (hq + hkv) * d:])
+    assert torch.equal(kc1, kc0) and torch.equal(vc1, vc0)
+    # the rotated k columns of the output are what went into the cache
+    kg = got[:, hq * d:(hq + hkv) * d].view(rows, hkv, d)
+    for r in range(rows):
+        s = int(slots[r])
+        if s >= 0:
+            assert torch.equal(kg[r], kc1[s // 16, :, s % 16, :])
+            assert torch.equal(vv[r], vc1[s // 16, :, :, s % 16])
+    with pytest.raises(ValueError):
+        pa.linear(x, wq)   # a rope-packed weight is not a plain packed weight

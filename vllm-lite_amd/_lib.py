@@ -31,6 +31,9 @@ SIGNATURES = {
     "pa_linear_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
     "pa_linear_pack": (_i32, [_p, _p, _p, _i32, _i32, _i32, _p]),
     "pa_argmax": (_i32, [_p, _p, _i32, _i32, _i64, _i32, _p]),
+    "pa_linear_rope_cache": (_i32, [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                                    _p, _p, _p, _p, _p, _i32, _i32, _p]),
+    "pa_linear_pack_qkv": (_i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p]),
     "pa_decode_quantized": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32,
                                    _i32, _i32, _f32, _p, _sz, _p]),
     "pa_prefill_quantized": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32,
@@ -61,6 +64,8 @@ SIGNATURES = {
     "pa_batch_num_tokens": (_i32, [_p]),
     "pa_batch_set_capacity": (_i32, [_p, _i32]),
     "pa_batch_is_decode": (_i32, [_p]),
+    "pa_batch_qkv_rope_cache": (_i32, [_p, _p, _i32, _i32, _p, _p, _p, _p, _i32, _i32, _f32,
+                                       _p, _p]),
     "pa_batch_attention": (_i32, [_p, _p, _i32, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _f32,
                                   _p, _p]),
 }

@@ -17,6 +17,7 @@
 #include <cstring>
 #include <vector>
 
+#include "../../include/pa_dense.h"
 #include "../../include/pa_kv_cache.h"
 #include "pa_common.hpp"
 
@@ -204,10 +205,15 @@ extern "C" int32_t pa_batch_attention(pa_batch* b, pa_kv_cache* cache, int32_t l
   const int dtype = pa_kv_cache_dtype(cache);
   PA_REQUIRE(num_heads > 0 && num_heads % hkv == 0, PA_ERR_INVALID_ARG,
              "pa_batch_attention: num_heads %d not a multiple of num_kv_heads %d", num_heads, hkv);
-  PA_REQUIRE(q && key && value && out, PA_ERR_INVALID_ARG, "pa_batch_attention: null tensor");
+  PA_REQUIRE(q && out && (key != nullptr) == (value != nullptr), PA_ERR_INVALID_ARG,
+             "pa_batch_attention: null tensor");
+  PA_REQUIRE(key || !inv_freq, PA_ERR_INVALID_ARG,
+             "pa_batch_attention: inv_freq without key / value (rotated where written)");
   const int64_t* slots = (const int64_t*)b->slots.ptr;
-  int32_t rc;
-  if (inv_freq) {
+  int32_t rc = PA_OK;
+  if (!key) {
+    // the step's K / V were written by pa_batch_qkv_rope_cache
+  } else if (inv_freq) {
     rc = pa_rope_reshape_and_cache(q, q_stride, key, key_stride, value, value_stride, kc, vc,
                                    slots, (const int64_t*)b->positions.ptr, inv_freq,
                                    b->num_tokens, num_heads, hkv, d, b->num_blocks, dtype,
@@ -235,4 +241,28 @@ extern "C" int32_t pa_batch_attention(pa_batch* b, pa_kv_cache* cache, int32_t l
                              b->max_blocks, (const int32_t*)b->cu_q.ptr,
                              (const int32_t*)b->past.ptr, b->num_seqs, b->num_tokens, b->max_q,
                              num_heads, hkv, d, b->num_blocks, scale, dtype, stream);
+}
+
+extern "C" int32_t pa_batch_qkv_rope_cache(pa_batch* b, pa_kv_cache* cache, int32_t layer,
+                                           int32_t num_heads, void* out, const void* x,
+                                           const void* weight, const void* bias,
+                                           int32_t in_features, int32_t flags, float eps,
+                                           const float* inv_freq, pa_stream_t stream) {
+  pa::clear_error();
+  PA_REQUIRE(b && cache, PA_ERR_INVALID_ARG, "pa_batch_qkv_rope_cache: null batch or cache");
+  void* kc = pa_kv_cache_key_ptr(cache, layer);
+  void* vc = pa_kv_cache_value_ptr(cache, layer);
+  PA_REQUIRE(kc && vc, PA_ERR_OUT_OF_BOUNDS, "layer_idx %d out of bounds for %d layers", layer,
+             pa_kv_cache_num_layers(cache));
+  PA_REQUIRE(pa_kv_cache_num_blocks(cache) == b->num_blocks, PA_ERR_INVALID_ARG,
+             "pa_batch_qkv_rope_cache: batch prepared for %d blocks, cache has %d",
+             b->num_blocks, pa_kv_cache_num_blocks(cache));
+  const int hkv = pa_kv_cache_num_heads(cache), d = pa_kv_cache_head_dim(cache);
+  PA_REQUIRE(num_heads > 0 && num_heads % hkv == 0, PA_ERR_INVALID_ARG,
+             "pa_batch_qkv_rope_cache: num_heads %d not a multiple of num_kv_heads %d",
+             num_heads, hkv);
+  return pa_linear_rope_cache(out, x, weight, bias, b->num_tokens, num_heads, hkv, d,
+                              in_features, flags, eps, (const int64_t*)b->positions.ptr,
+                              (const int64_t*)b->slots.ptr, inv_freq, kc, vc, b->num_blocks,
+                              pa_kv_cache_dtype(cache), stream);
 }

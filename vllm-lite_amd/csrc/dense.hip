@@ -124,12 +124,28 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(T* __restrict__ out,
 //          path, whose projection output is bf16).
 // Weight tiles of the last column block that lie past N (N a multiple of 16)
 // read row n0 and are not stored.
+// Epilogue 3 (the decode step's QKV projection with RoPE and the KV-cache
+// write fused in): per token row m its position and cache slot, the
+// inverse-frequency table, the layer's caches ([NB, Hkv, 16, D] keys,
+// token-minor [NB, Hkv, D, 16] values) and the head layout of the output
+// columns (Hq query heads, then Hkv key heads, then Hkv value heads of D).
+struct RopeCacheArgs {
+  const int64_t* positions;
+  const int64_t* slots;
+  const float* inv_freq;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t num_slots;
+  int Hq, Hkv, D;
+};
+
 template <int EPI, int NT, bool PK, int U>
 __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ bias, int M, int N, int K, int kw, int flags, float eps,
-    float* __restrict__ ws, int* __restrict__ counters) {
+    float* __restrict__ ws, int* __restrict__ counters, const RopeCacheArgs ra) {
   static_assert(EPI != 2 || NT == 2, "SwiGLU pairs one gate and one up tile");
+  static_assert(EPI != 3 || NT == 2, "RoPE pairs the two halves of a head in two tiles");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, j = lane >> 4;
@@ -202,6 +218,24 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
     }
   };
   if (s0 < s1) load(s0, a[0], b[0]);
+  // Epilogue 3: the rotation angles of this lane's pairs (batch rows c and
+  // 16 + c, pairs i = f0 + 4 j + r), computed by wavefront 0 while its first
+  // loads are in flight.
+  float rsn[2][4], rcs[2][4];
+  if constexpr (EPI == 3) {
+    const int head = n0 / ra.D;
+    if (wave == 0 && head < ra.Hq + ra.Hkv) {
+      const int f0 = 8 * ((n0 % ra.D) / 16);
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        const int m = min(m0 + 16 * bb + c, M - 1);
+        const float pos = (float)ra.positions[m];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sincosf(pos * ra.inv_freq[f0 + 4 * j + r], &rsn[bb][r], &rcs[bb][r]);
+      }
+    }
+  }
   for (int s = s0; s < s1; s += 2 * U) {
     if (s + U < s1) load(s + U, a[1], b[1]);
     mma(s, a[0], b[0]);
@@ -320,6 +354,64 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
       }
       *reinterpret_cast<uint64_t*>(out + (int64_t)m * N + n0 + 4 * j) =
           *reinterpret_cast<const uint64_t*>(o4);
+    } else if constexpr (EPI == 3) {
+      // Packed by linear_pack_kernel with rope pairs: within a query or key
+      // head the two tiles hold head rows 16 p .. +15 and D / 2 + 16 p .. +15
+      // (p = the tile pair), so this lane holds both members (i, i + D / 2)
+      // of the rotation pairs i = 16 p + 4 j + r of batch row m.  Value
+      // heads keep their row order.  Rounded to bf16 as the unfused
+      // projection output, then rotated as rope_cache_kernel does.
+      const int D = ra.D;
+      const int head = n0 / D, u = (n0 % D) / 16;
+      const bool rot = head < ra.Hq + ra.Hkv;
+      const int f0 = rot ? 8 * u : 16 * u;                   // head row of tile 0
+      const int f1 = rot ? D / 2 + 8 * u : 16 * u + 16;      // head row of tile 1
+      float y[2][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float a0 = acc[0][bb][r] * inv[bb], a1 = acc[1][bb][r] * inv[bb];
+        if (bias) {
+          a0 += bf16_bits_to_f32(bias[head * D + f0 + 4 * j + r]);
+          a1 += bf16_bits_to_f32(bias[head * D + f1 + 4 * j + r]);
+        }
+        y[0][r] = bf16_bits_to_f32(f32_to_bf16_bits(a0));
+        y[1][r] = bf16_bits_to_f32(f32_to_bf16_bits(a1));
+      }
+      if (rot) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float sn = rsn[bb][r], cs = rcs[bb][r];
+          const float x1 = y[0][r], x2 = y[1][r];
+          y[0][r] = x1 * cs - x2 * sn;
+          y[1][r] = x2 * cs + x1 * sn;
+        }
+      }
+      uint16_t o4[2][4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o4[t][r] = f32_to_bf16_bits(y[t][r]);
+      uint16_t* orow = out + (int64_t)m * N + head * D + 4 * j;
+      *reinterpret_cast<uint64_t*>(orow + f0) = *reinterpret_cast<const uint64_t*>(o4[0]);
+      *reinterpret_cast<uint64_t*>(orow + f1) = *reinterpret_cast<const uint64_t*>(o4[1]);
+      const int64_t slot = ra.slots[m];
+      if (head >= ra.Hq && slot >= 0 && slot < ra.num_slots) {
+        const int64_t blk = slot / kBlock;
+        const int off = (int)(slot % kBlock);
+        if (rot) {
+          uint16_t* kd = ra.k_cache + ((blk * ra.Hkv + (head - ra.Hq)) * kBlock + off) * D + 4 * j;
+          *reinterpret_cast<uint64_t*>(kd + f0) = *reinterpret_cast<const uint64_t*>(o4[0]);
+          *reinterpret_cast<uint64_t*>(kd + f1) = *reinterpret_cast<const uint64_t*>(o4[1]);
+        } else {
+          uint16_t* vd =
+              ra.v_cache + ((blk * ra.Hkv + (head - ra.Hq - ra.Hkv)) * D + 4 * j) * kBlock + off;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            vd[(f0 + r) * kBlock] = o4[0][r];
+            vd[(f1 + r) * kBlock] = o4[1][r];
+          }
+        }
+      }
     } else {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -353,7 +445,8 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
 __global__ __launch_bounds__(256) void linear_pack_kernel(uint16_t* __restrict__ dst,
                                                           const uint16_t* __restrict__ src,
                                                           const uint16_t* __restrict__ col_scale,
-                                                          int N, int K) {
+                                                          int N, int K, int rope_d,
+                                                          int rope_rows) {
   const int64_t total = (int64_t)N * K / 8;
   const int nsteps = K / 32;
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < total;
@@ -363,8 +456,18 @@ __global__ __launch_bounds__(256) void linear_pack_kernel(uint16_t* __restrict__
     const int64_t tile = frag / nsteps;
     const int step = (int)(frag % nsteps);
     const int64_t row = tile * 16 + (lane & 15);
+    // With rope pairs (rope_d = head_dim, the first rope_rows rows being
+    // query and key heads): packed tile 2 p + h of a head takes the head's
+    // rows h * D / 2 + 16 p .. +15, so tiles 2 p and 2 p + 1 hold the two
+    // halves of the rotation pairs 16 p .. 16 p + 15.
+    int64_t src_row = row;
+    if (row < rope_rows) {
+      const int64_t hd = row / rope_d;
+      const int u = (int)(row % rope_d) / 16;
+      src_row = hd * rope_d + (u & 1) * (rope_d / 2) + (u >> 1) * 16 + (lane & 15);
+    }
     const int col = step * 32 + 8 * (lane >> 4);
-    uint4 v = *reinterpret_cast<const uint4*>(src + row * K + col);
+    uint4 v = *reinterpret_cast<const uint4*>(src + src_row * K + col);
     if (col_scale) {
       uint16_t* e = reinterpret_cast<uint16_t*>(&v);
 #pragma unroll
@@ -628,9 +731,11 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   auto* bb = (const uint16_t*)bias;
 #define PA_LAUNCH_LINEAR_U(EPI, NT, UU)                                                       \
   (packed ? linear_skinny_kernel<EPI, NT, true, UU><<<grid, 64 * kw, 0, s>>>(                  \
-                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps, ws, counters) \
+                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps, ws, counters,  \
+                RopeCacheArgs{})                                                              \
           : linear_skinny_kernel<EPI, NT, false, UU><<<grid, 64 * kw, 0, s>>>(                 \
-                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps, ws, counters))
+                o, xx, ww, bb, rows, out_features, in_features, kw, flags, eps, ws, counters,  \
+                RopeCacheArgs{}))
 #define PA_LAUNCH_LINEAR(EPI, NT)                                                             \
   (NT == 1 && stage == 8 ? PA_LAUNCH_LINEAR_U(EPI, 1, 8) : PA_LAUNCH_LINEAR_U(EPI, NT, 4))
   if (act == PA_ACT_SILU_MUL)
@@ -658,8 +763,32 @@ extern "C" int32_t pa_linear_pack(void* packed, const void* weight, const void* 
   const int64_t pieces = (int64_t)rows * cols / 8;
   const int blocks = (int)std::min<int64_t>((pieces + 255) / 256, 65536);
   linear_pack_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
-      (uint16_t*)packed, (const uint16_t*)weight, (const uint16_t*)col_scale, rows, cols);
+      (uint16_t*)packed, (const uint16_t*)weight, (const uint16_t*)col_scale, rows, cols, 1, 0);
   return check_launch("pa_linear_pack");
+}
+
+extern "C" int32_t pa_linear_pack_qkv(void* packed, const void* weight, const void* col_scale,
+                                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                      int32_t cols, int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype == PA_DTYPE_BF16, PA_ERR_UNSUPPORTED,
+             "pa_linear_pack_qkv: dtype %d (bf16 only)", dtype);
+  PA_REQUIRE(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && cols > 0, PA_ERR_INVALID_ARG,
+             "pa_linear_pack_qkv: bad sizes");
+  PA_REQUIRE(head_dim % 32 == 0 && cols % 32 == 0, PA_ERR_UNSUPPORTED,
+             "pa_linear_pack_qkv: head_dim %d and cols %d must be multiples of 32", head_dim,
+             cols);
+  PA_REQUIRE(packed && weight && packed != weight, PA_ERR_INVALID_ARG,
+             "pa_linear_pack_qkv: null or aliased pointers");
+  PA_REQUIRE(((uintptr_t)packed | (uintptr_t)weight) % 16 == 0, PA_ERR_INVALID_ARG,
+             "pa_linear_pack_qkv: pointers must be 16-byte aligned");
+  const int rows = (num_heads + 2 * num_kv_heads) * head_dim;
+  const int64_t pieces = (int64_t)rows * cols / 8;
+  const int blocks = (int)std::min<int64_t>((pieces + 255) / 256, 65536);
+  linear_pack_kernel<<<blocks, 256, 0, (hipStream_t)stream>>>(
+      (uint16_t*)packed, (const uint16_t*)weight, (const uint16_t*)col_scale, rows, cols,
+      head_dim, (num_heads + num_kv_heads) * head_dim);
+  return check_launch("pa_linear_pack_qkv");
 }
 
 extern "C" int32_t pa_argmax(int64_t* out, const void* logits, int32_t rows, int32_t cols,
@@ -692,4 +821,49 @@ extern "C" int32_t pa_argmax(int64_t* out, const void* logits, int32_t rows, int
                                                               row_stride);
   }
   return check_launch("pa_argmax");
+}
+
+extern "C" int32_t pa_linear_rope_cache(void* out, const void* x, const void* weight,
+                                        const void* bias, int32_t rows, int32_t num_heads,
+                                        int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t in_features, int32_t flags, float eps,
+                                        const int64_t* positions, const int64_t* slot_mapping,
+                                        const float* inv_freq, void* k_cache, void* v_cache,
+                                        int32_t num_blocks, int32_t dtype, pa_stream_t stream) {
+  clear_error();
+  PA_REQUIRE(dtype == PA_DTYPE_BF16, PA_ERR_UNSUPPORTED,
+             "pa_linear_rope_cache: dtype %d (bf16 only)", dtype);
+  PA_REQUIRE(rows >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
+                 in_features > 0 && num_blocks > 0,
+             PA_ERR_INVALID_ARG, "pa_linear_rope_cache: bad sizes");
+  PA_REQUIRE(head_dim % 32 == 0 && in_features % 32 == 0, PA_ERR_UNSUPPORTED,
+             "pa_linear_rope_cache: head_dim %d and in_features %d must be multiples of 32",
+             head_dim, in_features);
+  PA_REQUIRE((flags & ~PA_LINEAR_RMS_IN) == 0, PA_ERR_INVALID_ARG,
+             "pa_linear_rope_cache: flags %d (only PA_LINEAR_RMS_IN)", flags);
+  PA_REQUIRE(!(flags & PA_LINEAR_RMS_IN) || eps > 0.f, PA_ERR_INVALID_ARG,
+             "pa_linear_rope_cache: eps must be positive");
+  if (rows == 0) return PA_OK;
+  PA_REQUIRE(out && x && weight && positions && slot_mapping && inv_freq && k_cache && v_cache,
+             PA_ERR_INVALID_ARG, "pa_linear_rope_cache: null pointer");
+  PA_REQUIRE(((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)k_cache) % 16 == 0,
+             PA_ERR_INVALID_ARG, "pa_linear_rope_cache: x, weight, out and k_cache must be "
+             "16-byte aligned");
+  PA_REQUIRE((rows + 31) / 32 <= 65535, PA_ERR_UNSUPPORTED, "pa_linear_rope_cache: %d rows",
+             rows);
+  const int n = (num_heads + 2 * num_kv_heads) * head_dim;
+  // K split over the wavefronts as pa_linear splits it for this shape (up
+  // to the 8 wavefronts this instance launches with), so the f32 sums, and
+  // so the bf16 outputs, are those of pa_linear
+  // K split over the wavefronts as pa_linear splits it for this shape (up
+  // to the 8 wavefronts this instance launches with), so the f32 sums, and
+  // so the bf16 outputs, are those of pa_linear
+  const int kw = std::min(8, linear_plan(rows, n, in_features, PA_ACT_NONE, false).kw);
+  const RopeCacheArgs ra{positions, slot_mapping, inv_freq, (uint16_t*)k_cache,
+                         (uint16_t*)v_cache, (int64_t)num_blocks * kBlock, num_heads,
+                         num_kv_heads, head_dim};
+  linear_skinny_kernel<3, 2, true, 4><<<dim3(n / 32, (rows + 31) / 32), 64 * kw, 0, (hipStream_t)stream>>>(
+      (uint16_t*)out, (const uint16_t*)x, (const uint16_t*)weight, (const uint16_t*)bias, rows,
+      n, in_features, kw, flags, eps, nullptr, nullptr, ra);
+  return check_launch("pa_linear_rope_cache");
 }

@@ -68,6 +68,7 @@ class Weights:
     """Random weights of the configuration (bf16 on the device)."""
 
     def __init__(self, cfg, seed=4, device="cuda", dtype=torch.bfloat16):
+        self.cfg = cfg
         g = torch.Generator(device=device).manual_seed(seed)
 
         def w(*shape):
@@ -109,6 +110,13 @@ class Weights:
                   "down": [(x, None) for x in self.wd]}
         p = {name: [ops.PackedWeight(x, col_scale=g) for x, g in ws]
              for name, ws in blocks.items() if all(fits(x) for x, _ in ws)}
+        if fold_rms and self.cfg.head_dim % 32 == 0 and self.cfg.hidden % 32 == 0:
+            # the fused QKV weight for pa_linear_rope_cache (RoPE and the KV
+            # write in the projection's epilogue)
+            c = self.cfg
+            p["qkv_rope"] = [ops.PackedWeight(x, col_scale=g,
+                                              rope_heads=(c.heads, c.kv_heads, c.head_dim))
+                             for x, g in zip(self.wqkv, ln1)]
         if fits(self.embed):
             p["lm_head"] = ops.PackedWeight(self.embed, col_scale=self.norm if fold_rms else None)
         p["rms_folded"] = fold_rms
@@ -221,12 +229,21 @@ class Engine:
         nq = hq * d
         x = F.embedding(tokens, w.embed)  # residual stream [T, hidden]
         for layer in range(c.layers):
-            # one QKV projection; q, k, v are strided views of its rows
-            qkv = ops.linear(x, pk["qkv"][layer], w.bqkv[layer], rms_eps=c.eps)
-            q = qkv[:, :nq].view(t, hq, d)
-            k = qkv[:, nq:nq + hkv * d].view(t, hkv, d)
-            v = qkv[:, nq + hkv * d:].view(t, hkv, d)
-            attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq, self.scale)
+            if "qkv_rope" in pk:
+                # one QKV projection with RoPE and the KV write in its
+                # epilogue; attention reads q as a strided view of its rows
+                qkv = self.batch.qkv_rope_cache(self.cache, layer, x, pk["qkv_rope"][layer],
+                                                w.bqkv[layer], self.inv_freq, rms_eps=c.eps)
+                q = qkv[:, :nq].view(t, hq, d)
+                attn = self.batch.attention(self.cache, layer, q, None, None, None, self.scale)
+            else:
+                # one QKV projection; q, k, v are strided views of its rows
+                qkv = ops.linear(x, pk["qkv"][layer], w.bqkv[layer], rms_eps=c.eps)
+                q = qkv[:, :nq].view(t, hq, d)
+                k = qkv[:, nq:nq + hkv * d].view(t, hkv, d)
+                v = qkv[:, nq + hkv * d:].view(t, hkv, d)
+                attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq,
+                                            self.scale)
             ops.linear(attn.view(t, nq), pk["o"][layer], out=x, add_to_out=True)
             act = ops.linear(x, pk["gu"][layer], act=ops.ACT_SILU_MUL, rms_eps=c.eps)
             if "down" in pk:

@@ -226,16 +226,46 @@ class StepBatch:
     def is_decode(self):
         return bool(self._lib.pa_batch_is_decode(self._h))
 
+    def qkv_rope_cache(self, cache, layer, x, weight, bias, inv_freq, rms_eps=None):
+        """pa_batch_qkv_rope_cache: the step's fused QKV projection of x
+        [T, K] with RoPE and the KV-cache write in its epilogue; weight a
+        PackedWeight with rope_heads.  Returns [T, (Hq + 2 Hkv) D]; pass its
+        q view to attention() with key = value = None."""
+        if weight.rope_heads is None:
+            raise ValueError("qkv_rope_cache takes a PackedWeight with rope_heads")
+        hq, hkv, d = weight.rope_heads
+        t, k = x.shape
+        if t != self.num_tokens() or hkv != cache.num_heads or d != cache.head_dim:
+            raise ValueError("x / weight do not match the batch and cache")
+        if x.dtype != cache.dtype or not x.is_contiguous() or x.device != cache.device:
+            raise ValueError("x must be contiguous, on the cache's device and dtype")
+        if inv_freq.dtype != torch.float32 or inv_freq.shape != (d // 2,):
+            raise ValueError("inv_freq must be float32 [D/2]")
+        out = torch.empty(t, weight.shape[0], dtype=x.dtype, device=x.device)
+        _check("pa_batch_qkv_rope_cache", self._lib.pa_batch_qkv_rope_cache(
+            self._h, cache._h, layer, hq, C.c_void_p(out.data_ptr()), C.c_void_p(x.data_ptr()),
+            C.c_void_p(weight.data.data_ptr()),
+            C.c_void_p(bias.data_ptr()) if bias is not None else None, k,
+            1 if rms_eps is not None else 0, float(rms_eps) if rms_eps is not None else 0.0,
+            C.c_void_p(inv_freq.data_ptr()), cache._stream()))
+        return out
+
     def attention(self, cache, layer, q, key, value, inv_freq=None, scale=None):
         """q [T, Hq, D] (rotated in place with inv_freq), key / value
         [T, Hkv, D] (rows of all three may be strided views of a fused
-        projection) -> out [T, Hq, D]."""
+        projection) -> out [T, Hq, D].  key = value = None: the step's K / V
+        are already in the cache and q is final (qkv_rope_cache)."""
         t, hq, d = q.shape
         if t != self.num_tokens():
             raise ValueError(f"batch has {self.num_tokens()} tokens, q has {t}")
-        if key.shape != (t, cache.num_heads, d) or value.shape != key.shape:
+        if (key is None) != (value is None) or (key is None and inv_freq is not None):
+            raise ValueError("key and value both or neither; no inv_freq without them")
+        if key is not None and (key.shape != (t, cache.num_heads, d) or
+                                value.shape != key.shape):
             raise ValueError("key / value must be [T, Hkv, D]")
         for x in (q, key, value):
+            if x is None:
+                continue
             if x.dtype != cache.dtype or x.device != cache.device or x.stride(2) != 1 or \
                     x.stride(1) != d:
                 raise ValueError("q / key / value rows must be [H, D] in the cache dtype")
@@ -247,7 +277,9 @@ class StepBatch:
         out = torch.empty_like(q)
         _check("pa_batch_attention", self._lib.pa_batch_attention(
             self._h, cache._h, layer, hq, C.c_void_p(q.data_ptr()), q.stride(0),
-            C.c_void_p(key.data_ptr()), key.stride(0), C.c_void_p(value.data_ptr()),
-            value.stride(0), C.c_void_p(inv_freq.data_ptr()) if inv_freq is not None else None,
+            C.c_void_p(key.data_ptr()) if key is not None else None,
+            key.stride(0) if key is not None else 0,
+            C.c_void_p(value.data_ptr()) if value is not None else None,
+            value.stride(0) if value is not None else 0, C.c_void_p(inv_freq.data_ptr()) if inv_freq is not None else None,
             float(scale), C.c_void_p(out.data_ptr()), cache._stream()))
         return out

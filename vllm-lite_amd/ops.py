@@ -372,9 +372,12 @@ def linear_supports(x, weight):
 class PackedWeight:
     """A bf16 weight [N, K] repacked by pa_linear_pack (see pa_dense.h); pass
     it to linear() in place of the row-major tensor.  col_scale [K] (bf16):
-    folded into the columns (a norm weight in front of the projection)."""
+    folded into the columns (a norm weight in front of the projection).
+    rope_heads=(num_heads, num_kv_heads, head_dim): the fused QKV weight
+    packed by pa_linear_pack_qkv for linear_rope_cache (rotation pairs in
+    one wavefront); linear() does not take it."""
 
-    def __init__(self, weight, col_scale=None):
+    def __init__(self, weight, col_scale=None, rope_heads=None):
         _dev(weight)
         if not weight.is_contiguous():
             raise ValueError("pa_linear_pack takes a contiguous weight")
@@ -384,9 +387,56 @@ class PackedWeight:
         self.shape = tuple(weight.shape)
         self.dtype = weight.dtype
         self.data = torch.empty_like(weight)
-        _check("pa_linear_pack", _lib.load().pa_linear_pack(
-            _ptr(self.data), _ptr(weight), _ptr(col_scale), weight.shape[0], weight.shape[1],
-            _dtype_code(weight), _stream(weight)))
+        self.rope_heads = tuple(rope_heads) if rope_heads is not None else None
+        lib = _lib.load()
+        if rope_heads is None:
+            _check("pa_linear_pack", lib.pa_linear_pack(
+                _ptr(self.data), _ptr(weight), _ptr(col_scale), weight.shape[0],
+                weight.shape[1], _dtype_code(weight), _stream(weight)))
+        else:
+            hq, hkv, d = rope_heads
+            if weight.shape[0] != (hq + 2 * hkv) * d:
+                raise ValueError(f"weight {self.shape} is not a fused QKV weight of "
+                                 f"{hq} + 2 x {hkv} heads of {d}")
+            _check("pa_linear_pack_qkv", lib.pa_linear_pack_qkv(
+                _ptr(self.data), _ptr(weight), _ptr(col_scale), hq, hkv, d, weight.shape[1],
+                _dtype_code(weight), _stream(weight)))
+
+
+def linear_rope_cache(x, weight, bias, positions, slot_mapping, inv_freq, k_cache, v_cache,
+                      rms_eps=None, out=None):
+    """pa_linear_rope_cache: the fused QKV projection of x [rows, K] with q and
+    k rotated (positions [rows] int64, inv_freq [D/2] f32) and each token's
+    k / v written to its slot (slot_mapping [rows] int64) of the caches
+    (k_cache [NB, Hkv, 16, D], token-minor v_cache [NB, Hkv, D, 16], bf16).
+    weight: PackedWeight(w_qkv, rope_heads=(Hq, Hkv, D)).  Returns out
+    [rows, (Hq + 2 Hkv) D] (rotated q and k, v)."""
+    if not isinstance(weight, PackedWeight) or weight.rope_heads is None:
+        raise ValueError("linear_rope_cache takes a PackedWeight with rope_heads")
+    hq, hkv, d = weight.rope_heads
+    _dev(x, weight.data, positions, slot_mapping, inv_freq, k_cache, v_cache)
+    rows, k = x.shape
+    if weight.shape[1] != k:
+        raise ValueError(f"weight {weight.shape} does not match x {tuple(x.shape)}")
+    if positions.shape != (rows,) or slot_mapping.shape != (rows,) or \
+            positions.dtype != torch.int64 or slot_mapping.dtype != torch.int64:
+        raise ValueError("positions / slot_mapping must be int64 [rows]")
+    if k_cache.shape[1:] != (hkv, BLOCK_SIZE, d) or v_cache.shape != (k_cache.shape[0], hkv, d,
+                                                                       BLOCK_SIZE):
+        raise ValueError("caches must be [NB, Hkv, 16, D] and [NB, Hkv, D, 16]")
+    if bias is not None:
+        _dev(bias)
+        if bias.shape != (weight.shape[0],):
+            raise ValueError("bias must be [(Hq + 2 Hkv) D]")
+    if out is None:
+        out = torch.empty(rows, weight.shape[0], dtype=x.dtype, device=x.device)
+    _check("pa_linear_rope_cache", _lib.load().pa_linear_rope_cache(
+        _ptr(out), _ptr(x), _ptr(weight.data), _ptr(bias), rows, hq, hkv, d, k,
+        LINEAR_RMS_IN if rms_eps is not None else 0,
+        float(rms_eps) if rms_eps is not None else 0.0, _ptr(positions), _ptr(slot_mapping),
+        _ptr(inv_freq), _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], _dtype_code(x),
+        _stream(x)))
+    return out
 
 
 def linear_workspace_size(rows, n, k, act=ACT_NONE):
@@ -414,6 +464,8 @@ def linear(x, weight, bias=None, act=ACT_NONE, out=None, rms_eps=None, add_to_ou
     the residual stream, updated in place with the result; workspace: from
     linear_workspace (K split over several workgroups per tile) or None."""
     packed = isinstance(weight, PackedWeight)
+    if packed and weight.rope_heads is not None:
+        raise ValueError("a weight packed with rope_heads is for linear_rope_cache")
     wt = weight.data if packed else weight
     _dev(x, wt)
     rows, k = x.shape
