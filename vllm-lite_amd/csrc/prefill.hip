@@ -263,7 +263,13 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // 1 KB chunk i of a K tile and of a V tile lie in the same cache block
   // (i / CPB), and a wavefront's chunks stay within one block
   static_assert(RPI * CPB == kBlock && CPB % DMA_PER_WAVE == 0, "one block per wavefront copy");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2][NBUF][TILE_BYTES];
+  // Compute tiles are bf16 for both cache types: an FP8 tile is copied
+  // into the staging area `stage` (its own layout, below) and converted to
+  // bf16 once per workgroup at the tile boundary, so the per-step fragment
+  // reads and the inner loop are those of the bf16 kernel.
+  constexpr int CT_BYTES = KT * D * 2;  // one bf16 K (or V) compute tile
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2][NBUF][CT_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage[FP8 ? 2 : 1][FP8 ? TILE_BYTES : 16];
 
   const int lane = threadIdx.x & 63;
   const int wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -394,7 +400,8 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // ch ^ kswz(r).  The rows one QK operand read touches (see qk) differ in
   // bits 0-1 and 3-4, which kswz spreads over distinct chunk positions.
   auto kswz = [](int r) -> int {
-    return CPR >= 16 ? (r & 3) | (((r >> 3) & 3) << 2) : (r & 3) | (((r >> 3) & 1) << 2);
+    constexpr int CPR2 = D * 2 / 16;  // 16-byte chunks per bf16 K row
+    return CPR2 >= 16 ? (r & 3) | (((r >> 3) & 3) << 2) : (r & 3) | (((r >> 3) & 1) << 2);
   };
   // V row swizzle: the two 16-byte halves of dim row d are swapped when
   // bit 2 of d is set.  (Measured read rates of the operand pattern, per CU:
@@ -436,10 +443,14 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       const int i = wave_s * DMA_PER_WAVE + i0;
       __builtin_amdgcn_global_load_lds(
           (const void*)(kbase + koff[i0]),
-          (__attribute__((address_space(3))) void*)(&smem[0][buf][i * 1024]), 16, 0, 0);
+          (__attribute__((address_space(3))) void*)(FP8 ? &stage[0][i * 1024]
+                                                        : &smem[0][buf][i * 1024]),
+          16, 0, 0);
       __builtin_amdgcn_global_load_lds(
           (const void*)(vbase + voff[i0]),
-          (__attribute__((address_space(3))) void*)(&smem[1][buf][i * 1024]), 16, 0, 0);
+          (__attribute__((address_space(3))) void*)(FP8 ? &stage[1][i * 1024]
+                                                        : &smem[1][buf][i * 1024]),
+          16, 0, 0);
     }
   };
   // A tile that reaches past the last key, or holds a block id outside the
@@ -451,18 +462,40 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   auto zero_stale = [&](int kt, int buf, int valid) -> bool {
     const bool special = kt * KT + KT > key_end || valid != (1 << (KT / kBlock)) - 1;
     if (!special) return false;
-    TC* vz = reinterpret_cast<TC*>(&smem[1][buf][0]);
+    uint16_t* vz = reinterpret_cast<uint16_t*>(&smem[1][buf][0]);
     for (int e = threadIdx.x; e < KT * D; e += blockDim.x) {
       const int key = e / D, d = e % D;
       const int b = key / kBlock, t16 = key % kBlock;
       const bool ok = kt * KT + key < key_end && ((valid >> b) & 1);
       if (!ok) {
-        const int half = FP8 ? t16 / 8 : (t16 / 8) ^ vswz(d);
+        const int half = (t16 / 8) ^ vswz(d);
         vz[(b * D + d) * kBlock + half * 8 + t16 % 8] = 0;
       }
     }
     __syncthreads();
     return true;
+  };
+  // FP8: converts the staged tile (copy layout: K row r's 8-byte unit u at
+  // unit position u ^ fsw(r), V dim rows of 16 bytes) into bf16 compute
+  // buffer `buf` (the bf16 layouts and swizzles above), exactly (every
+  // E4M3 value is a bf16 value).  All threads of the workgroup; the caller
+  // puts barriers around it.
+  auto convert_tile = [&](int buf) {
+    if constexpr (FP8) {
+      for (int e = threadIdx.x; e < KT * D / 8; e += blockDim.x) {
+        const int r = e / (D / 8), u = e % (D / 8);
+        const uint2 w = *reinterpret_cast<const uint2*>(&stage[0][r * D + (u ^ fsw(r)) * 8]);
+        *reinterpret_cast<bf16x8*>(&smem[0][buf][r * (D * 2) + (u ^ kswz(r)) * 16]) =
+            fp8x8_to_bf16(w.x, w.y);
+      }
+      for (int e = threadIdx.x; e < KT * D / 8; e += blockDim.x) {
+        const int bd = e / 2, h = e % 2;  // bd = block * D + dim
+        const int d = bd % D;
+        const uint2 w = *reinterpret_cast<const uint2*>(&stage[1][bd * 16 + 8 * h]);
+        *reinterpret_cast<bf16x8*>(&smem[1][buf][bd * 32 + (h ^ vswz(d)) * 16]) =
+            fp8x8_to_bf16(w.x, w.y);
+      }
+    }
   };
   // Sᵀ for the 32 keys of step ST of the tile in buffer `buf`.  MFMA tile
   // kk's row i holds key 8 (i / 4) + 4 kk + i % 4 of the step, so the lane
@@ -476,13 +509,8 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       const int r = ST * 32 + 8 * (c >> 2) + 4 * kk + (c & 3);
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        if constexpr (FP8) {
-          const uint2 w = *reinterpret_cast<const uint2*>(ks + r * D + ((4 * s + j) ^ fsw(r)) * 8);
-          ka[kk][s] = fp8x8_to_bf16(w.x, w.y);
-        } else {
-          const int ch = (4 * s + j) ^ kswz(r);
-          ka[kk][s] = *reinterpret_cast<const bf16x8*>(ks + r * (D * 2) + ch * 16);
-        }
+        const int ch = (4 * s + j) ^ kswz(r);
+        ka[kk][s] = *reinterpret_cast<const bf16x8*>(ks + r * (D * 2) + ch * 16);
       }
     }
   };
@@ -502,9 +530,16 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   bool tile_special;        // current tile needs key masking
   int valid_cur;            // validity bits of the current tile's 4 blocks
   int32_t id_ahead = 0;     // this wavefront's block id of the tile two ahead
-  // Prologue: tiles 0 and 1 in flight, wait for tile 0.
+  // Prologue: tiles 0 and 1 in flight, wait for tile 0.  (FP8: tile 0 is
+  // staged, converted, and only then is tile 1 copied into the staging area.)
   issue_tile(fetch_id(0), 0);
-  if (n_kt > 1) {
+  if constexpr (FP8) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    convert_tile(0);
+    __syncthreads();
+    if (n_kt > 1) issue_tile(fetch_id(1), 1);
+  } else if (n_kt > 1) {
     issue_tile(fetch_id(1), 1);
     __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DMA_PER_WAVE) & 0xF) | (((2 * DMA_PER_WAVE) >> 4) << 14));
   } else {
@@ -536,20 +571,11 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     // the softmax covers their latency.
     bf16x8 va[DT];
     {
-      if constexpr (FP8) {
-        const uint8_t* vrow = &smem[1][buf][0] + ((2 * ST + (j >> 1)) * D + c) * 16 + 8 * (j & 1);
+      const uint8_t* vrow = &smem[1][buf][0] + (2 * ST + (j >> 1)) * (D * 32) + c * 32;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const uint2 w = *reinterpret_cast<const uint2*>(vrow + dt * 16 * 16);
-          va[dt] = fp8x8_to_bf16(w.x, w.y);
-        }
-      } else {
-        const uint8_t* vrow = &smem[1][buf][0] + (2 * ST + (j >> 1)) * (D * 32) + c * 32;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int d = 16 * dt + c;
-          va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 + (((j & 1) ^ vswz(d)) * 16));
-        }
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = 16 * dt + c;
+        va[dt] = *reinterpret_cast<const bf16x8*>(vrow + dt * 16 * 32 + (((j & 1) ^ vswz(d)) * 16));
       }
     }
     // K fragments of the next step, read now so the softmax prep below
@@ -571,6 +597,12 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
+        if constexpr (FP8) {
+          // tile kt + 1 staged: convert it, then the staging area is free
+          // for tile kt + 2
+          convert_tile(next);
+          __syncthreads();
+        }
         if (kt + 2 < n_kt) issue_tile(id_ahead, ahead);
       }
       qk_load(next, IC<0>{}, ka);
