@@ -801,6 +801,23 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
   const int ctx = min(context_lens[seq], mbs * kBlock);
   const int np = min(min(num_parts, (ctx + part_len - 1) / part_len), 1024);
   const int64_t row0 = (int64_t)row * num_parts;
+  // Wavefront w sums the partitions w, w + 4, ... of dims lane and lane + 64
+  // (head_dim <= 128: the common case, in chunks of kRU partitions whose
+  // loads are all in flight together; the first chunk is loaded before the
+  // max / sum pass so the two round trips overlap).
+  constexpr int kRU = 8;
+  const bool two = D <= 128;
+  float v0[kRU], v1[kRU];
+  auto load_chunk = [&](int p0) {
+#pragma unroll
+    for (int u = 0; u < kRU; ++u) {
+      const int p = p0 + 4 * u;
+      const float* src = ws_o + (row0 + min(p, np - 1)) * D;
+      v0[u] = lane < D ? src[lane] : 0.f;
+      v1[u] = lane + 64 < D ? src[lane + 64] : 0.f;
+    }
+  };
+  if (two && np > 0) load_chunk(wave);
   float M = -INFINITY;
   for (int p = tid; p < np; p += 256) M = fmaxf(M, ws_ml[2 * (row0 + p)]);
   for (int w = 32; w > 0; w >>= 1) M = fmaxf(M, __shfl_xor(M, w, 64));
@@ -818,10 +835,27 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
   __syncthreads();
   L = ml[1][0] + ml[1][1] + ml[1][2] + ml[1][3];
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  for (int d = lane; d < D; d += 64) {
-    float acc = 0.f;
-    for (int p = wave; p < np; p += 4) acc += wsh[p] * ws_o[(row0 + p) * D + d];
-    red[wave][d] = acc;
+  if (two) {
+    float a0 = 0.f, a1 = 0.f;
+    for (int p0 = wave; p0 < np; p0 += 4 * kRU) {
+      if (p0 != wave) load_chunk(p0);
+#pragma unroll
+      for (int u = 0; u < kRU; ++u) {
+        const int p = p0 + 4 * u;
+        if (p < np) {
+          a0 += wsh[p] * v0[u];
+          a1 += wsh[p] * v1[u];
+        }
+      }
+    }
+    if (lane < D) red[wave][lane] = a0;
+    if (lane + 64 < D) red[wave][lane + 64] = a1;
+  } else {
+    for (int d = lane; d < D; d += 64) {
+      float acc = 0.f;
+      for (int p = wave; p < np; p += 4) acc += wsh[p] * ws_o[(row0 + p) * D + d];
+      red[wave][d] = acc;
+    }
   }
   __syncthreads();
   for (int d = tid; d < D; d += 256)
