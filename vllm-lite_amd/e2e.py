@@ -21,9 +21,10 @@ time (pa_linear_pack: every MFMA operand fragment one contiguous kilobyte);
 larger batches (prefill chunks) run in hipBLASLt (torch.nn.functional.linear),
 and so does the long-K down projection of the unfused path.  With RMSNorm and
 weights packed with the norm weights folded in (Weights.pack()), a decode step
-runs the fused layer of Engine._forward_fused: five launches per layer, the
-down projection split over K (pa_linear's workspace) and added into the
-residual stream in its epilogue.
+runs the fused layer of Engine._forward_fused: five launches per layer (the
+QKV projection with RoPE and the KV write in its epilogue, attention, O, gate|up
++ SwiGLU, and the down projection split over K by pa_linear's workspace), the
+residual adds in the O and down epilogues.
 The norm is chosen explicitly by ModelConfig.norm: "rms" (RMSNorm, what the
 benchmark configuration states) or "layer" (the zero-bias LayerNorm the
 reference's CausalLm constructs for these models,
@@ -217,12 +218,15 @@ class Engine:
 
     def _forward_fused(self, tokens, logit_rows):
         """Decode-step forward with the RMSNorms folded into the projections:
-        per layer the fused QKV projection (pa_linear normalising its input
-        rows, ln1 folded into the packed weight; attention reads q, k, v as
-        strided views of its rows), attention, O added into the residual
-        stream in place, gate|up + SwiGLU (ln2 folded), down (K split over
-        workgroups) added into the residual stream; the final norm is folded
-        into the LM head.  Five launches per layer instead of nine."""
+        per layer the fused QKV projection (normalising its input rows, ln1
+        folded into the packed weight) with RoPE and the KV-cache write in
+        its epilogue (pa_batch_qkv_rope_cache; without a "qkv_rope" pack, the
+        projection, then RoPE + the KV write in the attention call),
+        attention reading q as a strided view of its rows, O added into the
+        residual stream in place, gate|up + SwiGLU (ln2 folded), down (K
+        split over workgroups) added into the residual stream; the final
+        norm is folded into the LM head.  Five launches per layer instead of
+        nine."""
         c, w, pk = self.cfg, self.w, self.w.packed
         t = tokens.shape[0]
         hq, hkv, d = c.heads, c.kv_heads, c.head_dim
