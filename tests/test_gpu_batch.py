@@ -102,3 +102,20 @@ def test_prepare_rejects_bad_tables(pa):
     with pytest.raises(pa.PaError, match="multiple"):
         batch.attention(cache, 0, torch.zeros(17, 3, 64, dtype=torch.bfloat16, device=DEV),
                         kv, kv)
+    # attention only (the step's K / V already written): no inv_freq then, and
+    # key and value both or neither
+    inv = torch.ones(32, dtype=torch.float32, device=DEV)
+    with pytest.raises(ValueError):
+        batch.attention(cache, 0, q, None, None, inv)
+    with pytest.raises(ValueError):
+        batch.attention(cache, 0, q, kv, None)
+    import ctypes as C
+    lib = pa._lib.load()
+    out = torch.empty_like(q)
+    rc = lib.pa_batch_attention(batch._h, cache._h, 0, 4, C.c_void_p(q.data_ptr()), 0, None, 0,
+                                None, 0, C.c_void_p(inv.data_ptr()), 0.125,
+                                C.c_void_p(out.data_ptr()), cache._stream())
+    assert rc == -1 and b"inv_freq" in lib.pa_last_error()
+    # the attention-only call itself runs (zero caches: zero output)
+    out = batch.attention(cache, 0, q, None, None)
+    assert out.shape == q.shape and not torch.isnan(out.float()).any()
