@@ -269,7 +269,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // reads and the inner loop are those of the bf16 kernel.
   constexpr int CT_BYTES = KT * D * 2;  // one bf16 K (or V) compute tile
   __shared__ __attribute__((aligned(1024))) uint8_t smem[2][NBUF][CT_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t stage[FP8 ? 2 : 1][FP8 ? TILE_BYTES : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage[FP8 ? 2 : 1][2][FP8 ? TILE_BYTES : 16];
 
   const int lane = threadIdx.x & 63;
   const int wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -443,12 +443,12 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       const int i = wave_s * DMA_PER_WAVE + i0;
       __builtin_amdgcn_global_load_lds(
           (const void*)(kbase + koff[i0]),
-          (__attribute__((address_space(3))) void*)(FP8 ? &stage[0][i * 1024]
+          (__attribute__((address_space(3))) void*)(FP8 ? &stage[buf & 1][0][i * 1024]
                                                         : &smem[0][buf][i * 1024]),
           16, 0, 0);
       __builtin_amdgcn_global_load_lds(
           (const void*)(vbase + voff[i0]),
-          (__attribute__((address_space(3))) void*)(FP8 ? &stage[1][i * 1024]
+          (__attribute__((address_space(3))) void*)(FP8 ? &stage[buf & 1][1][i * 1024]
                                                         : &smem[1][buf][i * 1024]),
           16, 0, 0);
     }
@@ -475,23 +475,24 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     __syncthreads();
     return true;
   };
-  // FP8: converts the staged tile (copy layout: K row r's 8-byte unit u at
-  // unit position u ^ fsw(r), V dim rows of 16 bytes) into bf16 compute
-  // buffer `buf` (the bf16 layouts and swizzles above), exactly (every
-  // E4M3 value is a bf16 value).  All threads of the workgroup; the caller
-  // puts barriers around it.
-  auto convert_tile = [&](int buf) {
+  // FP8: converts the tile staged in slot `slot` (copy layout: K row r's
+  // 8-byte unit u at unit position u ^ fsw(r), V dim rows of 16 bytes) into
+  // bf16 compute buffer `buf` (the bf16 layouts and swizzles above), exactly
+  // (every E4M3 value is a bf16 value).  All threads of the workgroup.
+  // Tile t is staged in slot t % 2 (issue_tile's `buf` is the slot for FP8)
+  // and converted one tile boundary before its first use.
+  auto convert_tile = [&](int buf, int slot) {
     if constexpr (FP8) {
       for (int e = threadIdx.x; e < KT * D / 8; e += blockDim.x) {
         const int r = e / (D / 8), u = e % (D / 8);
-        const uint2 w = *reinterpret_cast<const uint2*>(&stage[0][r * D + (u ^ fsw(r)) * 8]);
+        const uint2 w = *reinterpret_cast<const uint2*>(&stage[slot][0][r * D + (u ^ fsw(r)) * 8]);
         *reinterpret_cast<bf16x8*>(&smem[0][buf][r * (D * 2) + (u ^ kswz(r)) * 16]) =
             fp8x8_to_bf16(w.x, w.y);
       }
       for (int e = threadIdx.x; e < KT * D / 8; e += blockDim.x) {
         const int bd = e / 2, h = e % 2;  // bd = block * D + dim
         const int d = bd % D;
-        const uint2 w = *reinterpret_cast<const uint2*>(&stage[1][bd * 16 + 8 * h]);
+        const uint2 w = *reinterpret_cast<const uint2*>(&stage[slot][1][bd * 16 + 8 * h]);
         *reinterpret_cast<bf16x8*>(&smem[1][buf][bd * 32 + (h ^ vswz(d)) * 16]) =
             fp8x8_to_bf16(w.x, w.y);
       }
@@ -529,16 +530,18 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
 
   bool tile_special;        // current tile needs key masking
   int valid_cur;            // validity bits of the current tile's 4 blocks
-  int32_t id_ahead = 0;     // this wavefront's block id of the tile two ahead
-  // Prologue: tiles 0 and 1 in flight, wait for tile 0.  (FP8: tile 0 is
-  // staged, converted, and only then is tile 1 copied into the staging area.)
+  int32_t id_ahead = 0;     // this wavefront's block id of the tile two (FP8: three) ahead
+  // Prologue: tiles 0 and 1 in flight, wait for tile 0.  (FP8: tiles 0 and
+  // 1 staged and converted, then tile 2 copied into slot 0.)
   issue_tile(fetch_id(0), 0);
   if constexpr (FP8) {
+    if (n_kt > 1) issue_tile(fetch_id(1), 1);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    convert_tile(0);
+    convert_tile(0, 0);
+    if (n_kt > 1) convert_tile(1, 1);
     __syncthreads();
-    if (n_kt > 1) issue_tile(fetch_id(1), 1);
+    if (n_kt > 2) issue_tile(fetch_id(2), 0);
   } else if (n_kt > 1) {
     issue_tile(fetch_id(1), 1);
     __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * DMA_PER_WAVE) & 0xF) | (((2 * DMA_PER_WAVE) >> 4) << 14));
@@ -584,7 +587,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     if constexpr (ST == 0) {
       qk_load(buf, IC<1>{}, ka);
       // this wavefront's block of the tile two ahead, a step before its copy
-      if (kt + 2 < n_kt) id_ahead = fetch_id(kt + 2);
+      if (kt + (FP8 ? 3 : 2) < n_kt) id_ahead = fetch_id(kt + (FP8 ? 3 : 2));
     } else {
       // Tile boundary, at the start of a tile's second step: the next tile
       // has landed (all waves), the buffer two tiles ahead is free again
@@ -598,12 +601,15 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if constexpr (FP8) {
-          // tile kt + 1 staged: convert it, then the staging area is free
-          // for tile kt + 2
-          convert_tile(next);
-          __syncthreads();
+          // FP8: tile kt + 2 (staged since the last boundary) into the free
+          // compute buffer, visible to all at the next boundary's barrier;
+          // its staging slot's previous tile (kt + 1) was converted a tile
+          // ago, so tile kt + 3 is copied into it
+          if (kt + 2 < n_kt) convert_tile(ahead, (kt + 2) & 1);
+          if (kt + 3 < n_kt) issue_tile(id_ahead, (kt + 3) & 1);
+        } else {
+          if (kt + 2 < n_kt) issue_tile(id_ahead, ahead);
         }
-        if (kt + 2 < n_kt) issue_tile(id_ahead, ahead);
       }
       qk_load(next, IC<0>{}, ka);
     }
