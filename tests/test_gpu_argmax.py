@@ -56,6 +56,14 @@ def test_argmax_strided_rows(pa, oracle, dtype):
         np.testing.assert_array_equal(pa.argmax(fd[:, lo:lo + n]).cpu().numpy(), expect)
 
 
+def test_argmax_expanded_rows(pa, oracle):
+    # a broadcast view (row stride 0) is read as the rows it shows
+    row = (torch.randn(1, 3000, generator=torch.Generator().manual_seed(2)) * 3)
+    x = row.to(DEV).expand(5, 3000)
+    expect = oracle.argmax_logits(row.expand(5, 3000).numpy())
+    np.testing.assert_array_equal(pa.argmax(x).cpu().numpy(), expect)
+
+
 def test_argmax_empty_vocab_and_rows(pa):
     x = torch.empty(4, 0, dtype=torch.bfloat16, device=DEV)
     np.testing.assert_array_equal(pa.argmax(x).cpu().numpy(), np.zeros(4, np.int64))

@@ -348,6 +348,8 @@ def argmax(logits, out=None):
     if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):
         raise ValueError("argmax: logits must be [rows, vocab] with unit column stride")
     rows, cols = logits.shape
+    if rows > 1 and logits.stride(0) < cols:
+        logits = logits.contiguous()  # rows that overlap (e.g. an expanded view)
     if out is None:
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)
     lib = _lib.load()
