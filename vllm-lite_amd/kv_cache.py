@@ -267,8 +267,9 @@ class StepBatch:
             if x is None:
                 continue
             if x.dtype != cache.dtype or x.device != cache.device or x.stride(2) != 1 or \
-                    x.stride(1) != d:
-                raise ValueError("q / key / value rows must be [H, D] in the cache dtype")
+                    x.stride(1) != d or (t > 1 and x.stride(0) < x.shape[1] * d):
+                raise ValueError("q / key / value rows must be [H, D] in the cache dtype, "
+                                 "token rows not overlapping")
         if inv_freq is not None and (inv_freq.dtype != torch.float32 or
                                      inv_freq.shape != (d // 2,)):
             raise ValueError("inv_freq must be float32 [D/2]")

@@ -68,6 +68,14 @@ def _cache_dims(k_cache, v_cache):
     return nb, h, d
 
 
+def _rows_ok(x, h, d):
+    """Token rows [H, D] of x [T, H, D]: contiguous within a row, and rows
+    that do not overlap (a token stride of at least H * D; the C ABI reads a
+    stride of 0 as "contiguous")."""
+    return (x.stride(2) == 1 and x.stride(1) == d and
+            (x.shape[0] <= 1 or x.stride(0) >= h * d))
+
+
 def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
     """Scatter key/value [T, H, D] into the caches at slot_mapping [T] (int64)."""
     _dev(k_cache, v_cache, slot_mapping)
@@ -77,8 +85,8 @@ def reshape_and_cache(key, value, k_cache, v_cache, slot_mapping):
         raise ValueError("key/value must be [T, H, D] matching the cache; slot_mapping [T]")
     if slot_mapping.dtype != torch.int64 or key.dtype != k_cache.dtype or value.dtype != k_cache.dtype:
         raise ValueError("dtype mismatch")
-    if key.stride(2) != 1 or key.stride(1) != d or value.stride(2) != 1 or value.stride(1) != d:
-        raise ValueError("key/value rows must be contiguous [H, D]")
+    if not (_rows_ok(key, h, d) and _rows_ok(value, h, d)):
+        raise ValueError("key/value rows must be contiguous [H, D], not overlapping")
     lib = _lib.load()
     _check("pa_reshape_and_cache", lib.pa_reshape_and_cache(
         _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), t, h, d, nb,
@@ -108,8 +116,8 @@ def reshape_and_cache_fp8(key, value, k_cache, v_cache, slot_mapping):
         raise ValueError("key/value must be [T, H, D] matching the cache; slot_mapping [T]")
     if slot_mapping.dtype != torch.int64 or value.dtype != key.dtype:
         raise ValueError("dtype mismatch")
-    if key.stride(2) != 1 or key.stride(1) != d or value.stride(2) != 1 or value.stride(1) != d:
-        raise ValueError("key/value rows must be contiguous [H, D]")
+    if not (_rows_ok(key, h, d) and _rows_ok(value, h, d)):
+        raise ValueError("key/value rows must be contiguous [H, D], not overlapping")
     lib = _lib.load()
     _check("pa_reshape_and_cache_fp8", lib.pa_reshape_and_cache_fp8(
         _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), t, h, d, nb,
@@ -276,8 +284,9 @@ def rope_reshape_and_cache(q, key, value, k_cache, v_cache, slot_mapping, positi
             inv_freq.dtype != torch.float32:
         raise ValueError("positions / slot_mapping int64, inv_freq float32")
     for x in (q, key, value):
-        if x.dtype != k_cache.dtype or not x.is_cuda or x.stride(2) != 1 or x.stride(1) != d:
-            raise ValueError("q/key/value rows must be contiguous [H, D] in the cache dtype")
+        if x.dtype != k_cache.dtype or not x.is_cuda or not _rows_ok(x, x.shape[1], d):
+            raise ValueError("q/key/value rows must be contiguous [H, D] in the cache dtype, "
+                             "not overlapping")
     lib = _lib.load()
     _check("pa_rope_reshape_and_cache", lib.pa_rope_reshape_and_cache(
         _ptr(q), q.stride(0), _ptr(key), key.stride(0), _ptr(value), value.stride(0),
