@@ -227,3 +227,37 @@ def test_linear_rope_cache_matches_unfused(pa, rows, hq, hkv, d, k, rms, with_bi
             assert torch.equal(vv[r], vc1[s // 16, :, :, s % 16])
     with pytest.raises(ValueError):
         pa.linear(x, wq)   # a rope-packed weight is not a plain packed weight
+
+
+def test_linear_split_k_graph_replays(pa):
+    # the K split in a captured graph: three calls on one workspace per
+    # replay; each replay (new inputs copied in between, eager work and a
+    # synchronisation in between) equals the eager result bit for bit
+    m, n, k = 32, 896, 4864
+    g = torch.Generator(device=DEV).manual_seed(9)
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wp = pa.ops.PackedWeight(w)
+    ws = pa.ops.linear_workspace(m, n, k, device=DEV)
+    x = torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16)
+    res = torch.zeros(m, n, dtype=torch.bfloat16, device=DEV)
+
+    def step():
+        for _ in range(3):
+            pa.linear(x, wp, out=res, add_to_out=True, workspace=ws)
+
+    step()  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for i in range(3):
+        x.copy_(torch.randn(m, k, generator=g, device=DEV).to(torch.bfloat16))
+        start = torch.randn(m, n, generator=g, device=DEV).to(torch.bfloat16)
+        res.copy_(start)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = res.clone()
+        res.copy_(start)
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(got, res), i
