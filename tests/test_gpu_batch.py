@@ -21,11 +21,30 @@ STEPS = [
 ]
 
 
+# long contexts over few sequences (the engine's decode shape): several
+# partitions per (sequence, kv head) merged in the workgroup, two decode
+# steps in a row
+LONG_STEPS = [
+    {0: 700, 1: 1000, 2: 333, 3: 129},
+    {0: 1, 1: 1, 2: 1, 3: 1},
+    {0: 1, 1: 1, 2: 1, 3: 1},
+]
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("rope", [True, False])
 def test_engine_loop(pa, oracle, dtype, rope):
-    rng = np.random.default_rng(11 + rope)
-    layers, hq, hkv, d, nb = 2, 8, 2, 128, 48
+    run_loop(pa, oracle, dtype, rope, STEPS, 128, 48)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_engine_loop_long_decode(pa, oracle, d):
+    run_loop(pa, oracle, "bf16", True, LONG_STEPS, d, 160)
+
+
+def run_loop(pa, oracle, dtype, rope, steps, d, nb):
+    rng = np.random.default_rng(11 + rope + d)
+    layers, hq, hkv = 2, 8, 2
     tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
     cache = pa.PagedKvCache(layers, hkv, d, nb, tdt, DEV)
     pool = list(rng.permutation(nb))
@@ -35,7 +54,7 @@ def test_engine_loop(pa, oracle, dtype, rope):
              for _ in range(layers)]
     ref_v = [np.zeros_like(ref_k[0]) for _ in range(layers)]
     batch = pa.StepBatch()
-    for step in STEPS:
+    for step in steps:
         seqs = list(step)
         for s in seqs:
             computed.setdefault(s, 0)
@@ -77,7 +96,7 @@ def test_engine_loop(pa, oracle, dtype, rope):
             got = to_np(out.float()) if dtype == "bf16" else to_np(out)
             if dtype == "bf16":
                 want = oracle.bf16_to_f32(want)
-            assert_close(got, want, *tol, f"step {STEPS.index(step)} layer {layer}")
+            assert_close(got, want, *tol, f"step {steps.index(step)} layer {layer}")
             if not rope:
                 # the cache holds exactly what the oracle wrote
                 assert np.array_equal(to_np(cache.key_cache(layer)), ref_k[layer])
