@@ -117,7 +117,11 @@ void pa_batch_destroy(pa_batch* batch);
  * Token rows of q / k / v / out are the sequences' tokens in order.
  * Validates every table entry against num_blocks (PA_ERR_OUT_OF_BOUNDS) and
  * that each table covers num_computed + num_tokens tokens.  Uploads the
- * index arrays on `stream` and synchronises it before returning. */
+ * index arrays on `stream` without waiting for them (the caller's host
+ * arrays may be reused on return): the launches that read the batch
+ * (pa_batch_attention, pa_batch_qkv_rope_cache) must be on the same stream.
+ * A prepare waits only for the uploads of the prepare two calls back, so
+ * the host can prepare step n + 1 while the device runs step n. */
 int32_t pa_batch_prepare(pa_batch* batch, int32_t num_seqs, const int32_t* num_tokens,
                          const int32_t* num_computed, const int64_t* block_ids,
                          const int32_t* block_counts, int32_t num_blocks, pa_stream_t stream);

@@ -31,7 +31,12 @@ struct DevBuf {
   size_t bytes = 0;
   int32_t ensure(size_t need) {
     if (need <= bytes) return PA_OK;
-    if (ptr) (void)hipFree(ptr);
+    // queued work may still read the old array (uploads and launches are
+    // stream-ordered, the host does not wait for them)
+    if (ptr) {
+      (void)hipDeviceSynchronize();
+      (void)hipFree(ptr);
+    }
     ptr = nullptr;
     bytes = 0;
     if (hipMalloc(&ptr, need) != hipSuccess) {
@@ -54,11 +59,21 @@ struct pa_batch {
   bool decode = false;
   // device arrays
   DevBuf positions, slots, tables, cu_q, past, ctx_lens, workspace;
-  // pinned staging
-  void* stage = nullptr;
-  size_t stage_bytes = 0;
+  // pinned staging, two slots used in turn: a prepare waits (on the event
+  // recorded after its uploads) only for the uploads of the prepare two
+  // calls back, so the host can prepare the next step while the device
+  // still runs the current one
+  void* stage[2] = {nullptr, nullptr};
+  size_t stage_bytes[2] = {0, 0};
+  hipEvent_t uploaded[2] = {nullptr, nullptr};
+  bool pending[2] = {false, false};
+  int slot = 0;
   ~pa_batch() {
-    if (stage) (void)hipHostFree(stage);
+    for (int i = 0; i < 2; ++i) {
+      if (pending[i]) (void)hipEventSynchronize(uploaded[i]);
+      if (uploaded[i]) (void)hipEventDestroy(uploaded[i]);
+      if (stage[i]) (void)hipHostFree(stage[i]);
+    }
   }
 };
 
@@ -136,15 +151,40 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
   const size_t b_pos = pos.size() * 8, b_slot = slot.size() * 8, b_tab = table.size() * 4,
                b_cu = cu.size() * 4, b_past = past.size() * 4, b_ctx = ctxl.size() * 4;
   const size_t total = b_pos + b_slot + b_tab + b_cu + b_past + b_ctx;
-  if (total > b->stage_bytes) {
-    if (b->stage) (void)hipHostFree(b->stage);
-    b->stage = nullptr;
-    b->stage_bytes = 0;
-    if (hipHostMalloc(&b->stage, total, hipHostMallocDefault) != hipSuccess) {
+  const int sl = b->slot;
+  if (b->pending[sl]) {  // this slot's previous uploads have been read
+    if (hipEventSynchronize(b->uploaded[sl]) != hipSuccess) {
+      pa::set_error("pa_batch_prepare: waiting for an earlier upload failed");
+      return PA_ERR_HIP;
+    }
+    b->pending[sl] = false;
+  }
+  if (!b->uploaded[sl] &&
+      hipEventCreateWithFlags(&b->uploaded[sl], hipEventDisableTiming) != hipSuccess) {
+    pa::set_error("pa_batch_prepare: event creation failed");
+    return PA_ERR_HIP;
+  }
+  if (total > b->stage_bytes[sl]) {
+    if (b->stage[sl]) (void)hipHostFree(b->stage[sl]);
+    b->stage[sl] = nullptr;
+    b->stage_bytes[sl] = 0;
+    if (hipHostMalloc(&b->stage[sl], total, hipHostMallocDefault) != hipSuccess) {
       pa::set_error("pa_batch_prepare: pinned staging of %zu bytes failed", total);
       return PA_ERR_HIP;
     }
-    b->stage_bytes = total;
+    b->stage_bytes[sl] = total;
+  }
+  // A device array that must grow is replaced: wait for the work queued
+  // on the stream (it may still read the old one) first.
+  const bool grow = std::max<size_t>(b_pos, 8) > b->positions.bytes ||
+                    std::max<size_t>(b_slot, 8) > b->slots.bytes ||
+                    std::max<size_t>(b_tab, 4) > b->tables.bytes || b_cu > b->cu_q.bytes ||
+                    std::max<size_t>(b_past, 4) > b->past.bytes ||
+                    std::max<size_t>(b_ctx, 4) > b->ctx_lens.bytes;
+  hipStream_t s = (hipStream_t)stream;
+  if (grow && hipStreamSynchronize(s) != hipSuccess) {
+    pa::set_error("pa_batch_prepare: stream synchronisation failed");
+    return PA_ERR_HIP;
   }
   int32_t rc = PA_OK;
   if ((rc = b->positions.ensure(std::max<size_t>(b_pos, 8))) ||
@@ -153,8 +193,7 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
       (rc = b->past.ensure(std::max<size_t>(b_past, 4))) ||
       (rc = b->ctx_lens.ensure(std::max<size_t>(b_ctx, 4))))
     return rc;
-  char* st = (char*)b->stage;
-  hipStream_t s = (hipStream_t)stream;
+  char* st = (char*)b->stage[sl];
   struct Part {
     const void* src;
     size_t bytes;
@@ -172,10 +211,12 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
     }
     off += p.bytes;
   }
-  if (hipStreamSynchronize(s) != hipSuccess) {
-    pa::set_error("pa_batch_prepare: stream synchronisation failed");
+  if (hipEventRecord(b->uploaded[sl], s) != hipSuccess) {
+    pa::set_error("pa_batch_prepare: event record failed");
     return PA_ERR_HIP;
   }
+  b->pending[sl] = true;
+  b->slot = sl ^ 1;
   b->num_seqs = num_seqs;
   b->num_tokens = T;
   b->max_blocks = max_blocks;
