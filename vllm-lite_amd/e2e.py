@@ -160,7 +160,8 @@ class Engine:
 
     def forward(self, tokens, logit_rows):
         """One step over the prepared batch: tokens [T] (int64, device) ->
-        logits of the rows logit_rows [R, vocab] (f32)."""
+        logits of the rows logit_rows [R, vocab] (f32; None: every row, as
+        in a decode step)."""
         return self._logits(tokens, logit_rows).float()
 
     def next_tokens(self, tokens, logit_rows):
@@ -211,7 +212,7 @@ class Engine:
                 act = ops.silu_mul(F.linear(h, w.wgu[layer]))
             add = linear(act, w.wd[layer])
         self._norm(x, w.norm, c.eps, add=add, out=h)
-        rows = h[logit_rows]
+        rows = h if logit_rows is None else h[logit_rows]
         if rows.shape[0] <= SKINNY_ROWS and ops.linear_supports(rows, w.embed):
             return ops.linear(rows, pk.get("lm_head", w.embed))
         return F.linear(rows, w.embed)
@@ -255,7 +256,7 @@ class Engine:
                            workspace=self.linear_ws)
             else:
                 x.addmm_(act, w.wd[layer].t())
-        rows = x[logit_rows].contiguous()
+        rows = x if logit_rows is None else x[logit_rows].contiguous()
         return ops.linear(rows, pk["lm_head"], rms_eps=c.eps)
 
     def generate(self, prompts, max_new):
@@ -280,7 +281,7 @@ class Engine:
             out = [nxt]
             torch.cuda.synchronize(self.device)
             t1 = time.perf_counter()
-            rows = torch.arange(b, device=self.device)
+            rows = None  # decode steps: one token per sequence, every row's logits
             self.batch.set_capacity(max(lens) + max_new if self.graph else 0)
             graph = static_tok = static_out = None
             for step in range(1, max_new):
