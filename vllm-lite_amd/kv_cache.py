@@ -202,7 +202,8 @@ class StepBatch:
 
     def prepare(self, cache, num_tokens, num_computed, block_ids):
         """num_tokens / num_computed: per-sequence ints; block_ids: list of
-        per-sequence lists."""
+        per-sequence lists.  The uploads are queued on the current stream
+        (not waited for); the batch's launches must use the same stream."""
         n = len(num_tokens)
         if len(num_computed) != n or len(block_ids) != n:
             raise ValueError("per-sequence lists must have equal length")
