@@ -117,6 +117,24 @@ def test_config4_shared_prefix_long_context(pa, oracle):
     assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "config 4 pattern")
 
 
+def test_config4_full_batch(pa, oracle):
+    # BASELINE config 4 at full size: B 16, contexts log-uniform in
+    # [8192, 32768] (seed 3), the first 256 blocks (4096 tokens) of every
+    # table the same physical blocks, N(0, 1) K/V.  At this size the launch
+    # runs 512-token partitions and decode_reduce_kernel merges up to 64
+    # partitions per head.
+    rng = np.random.default_rng(3)
+    ctx = np.exp(rng.uniform(np.log(8192), np.log(32768), size=16)).astype(np.int32)
+    case = make_decode_case(rng, 16, 32, 8, 128, ctx, dtype="bf16", shared_prefix_blocks=256)
+    assert np.all(case["block_tables"][:, :256] == case["block_tables"][0, :256])
+    out = pa.decode(to_dev(case["q"]), to_dev(case["k_cache"]),
+                    to_dev(oracle.v_from_ref(case["v_cache_ref"])), to_dev(case["block_tables"]),
+                    to_dev(ctx), int(ctx.max()), scale=1 / math.sqrt(128))
+    got = oracle.bf16_to_f32(to_np(out))
+    assert_close(got, ref_f32(oracle, case, scale=1 / math.sqrt(128)), BF16_ATOL, BF16_RTOL,
+                 "config 4 full")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_split_equals_single_pass(pa, oracle, dtype):
     # A sequence long enough to split must match the same keys attended in

@@ -261,3 +261,24 @@ def test_linear_split_k_graph_replays(pa):
         step()
         torch.cuda.synchronize()
         assert torch.equal(got, res), i
+
+
+def test_linear_split_k_workspace_any_call_order(pa):
+    # One workspace shared by calls whose split plans differ (the engine's
+    # down projection at <= 32 rows: 56 tiles x 4 splits; at 33-64 rows:
+    # 112 tiles x 2 splits), in both orders and interleaved.  The counter
+    # region sits at a fixed place, so leftover partial sums of one plan
+    # never read as counters of the next; each call is checked against fp32
+    # and against the same call on a fresh workspace (bit for bit).
+    n, k = 896, 4864
+    g = torch.Generator(device=DEV).manual_seed(17)
+    w = (torch.randn(n, k, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    wp = pa.ops.PackedWeight(w)
+    ws = pa.ops.linear_workspace(64, n, k, device=DEV)
+    assert ws.numel() >= max(pa.ops.linear_workspace_size(r, n, k) for r in range(1, 65))
+    for rows in (7, 32, 33, 64, 20, 48, 1, 40, 40, 3):
+        x = torch.randn(rows, k, generator=g, device=DEV).to(torch.bfloat16)
+        got = pa.linear(x, wp, workspace=ws)
+        fresh = pa.linear(x, wp, workspace=pa.ops.linear_workspace(rows, n, k, device=DEV))
+        assert torch.equal(got, fresh), rows
+        torch.testing.assert_close(got.float(), x.float() @ w.float().T, atol=2e-2, rtol=1e-2)

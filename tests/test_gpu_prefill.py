@@ -143,3 +143,43 @@ def test_prefill_ids_outside_pool_are_absent_keys(pa, oracle, dtype, hq, hkv, d)
     assert np.isfinite(got).all()
     tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
     assert_close(got, ref, *tol, f"prefill with out-of-pool ids {dtype} {hq}/{hkv}x{d}")
+
+
+def test_config3_full_size(pa, oracle):
+    # BASELINE config 3 at full size: 4 x 2048 new tokens on past
+    # 0 / 512 / 1024 / 2048, 32 / 8 x 128, bf16; the persistent grid's
+    # rounds and snake order run exactly as in the benchmark.
+    #  (1) Sampled query rows against the oracle: row i of sequence s is a
+    #      one-row sequence with past P_s + i over the same table.  Rows on
+    #      every 64-row tile diagonal edge (i % 64 in {0, 63}), both 32-row
+    #      wavefront halves, the first and the last row, and random rows.
+    #  (2) Every row against pa_decode over context P_s + i + 1 (the decode
+    #      kernel is itself checked against the oracle): all 8192 x 32 rows.
+    rng = np.random.default_rng(2)
+    pasts, chunk = [0, 512, 1024, 2048], 2048
+    q, kc, vc, bt, cu, past = make_prefill_case(oracle, rng, pasts, [chunk] * 4, 32, 8, 128,
+                                                "bf16")
+    dk, dv, dbt = to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt)
+    out = pa.prefill(to_dev(q), dk, dv, dbt, to_dev(cu), to_dev(past), chunk)
+    got = oracle.bf16_to_f32(to_np(out))
+
+    rows = []  # (sequence, row)
+    for s in range(4):
+        pick = {0, 1, 31, 32, 33, 2047, 2046}
+        pick |= {i for i in range(chunk) if i % 64 in (0, 63) and i % 256 < 64}
+        pick |= set(rng.integers(0, chunk, 12).tolist())
+        rows += [(s, i) for i in sorted(pick)]
+    sel = np.array([cu[s] + i for s, i in rows])
+    q1 = q[sel]
+    bt1 = bt[[s for s, _ in rows]]
+    past1 = np.array([pasts[s] + i for s, i in rows], np.int32)
+    ref = oracle.paged_attention(oracle.as_f32(q1), oracle.as_f32(kc), oracle.as_f32(vc), bt1,
+                                 np.arange(len(rows) + 1), past1, scale=1 / math.sqrt(128))
+    assert_close(got[sel], ref, BF16_ATOL, BF16_RTOL, "config 3 full, sampled rows vs oracle")
+
+    seq = np.repeat(np.arange(4), chunk)
+    ctx = (np.asarray(pasts)[seq] + np.tile(np.arange(chunk), 4) + 1).astype(np.int32)
+    dec = pa.decode(to_dev(q), dk, dv,
+                    to_dev(bt[seq]), to_dev(ctx), int(ctx.max()))
+    assert_close(got, oracle.bf16_to_f32(to_np(dec)), 2e-2, 1e-2,
+                 "config 3 full, all rows vs pa_decode")

@@ -286,14 +286,16 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
     // order, applies the epilogue and sets the counter back to zero for the
     // next call.
     // The records cross workgroups on other XCDs, whose L2s are not
-    // coherent with this one.  They are written and read as device-scope
-    // relaxed atomics (stores written through, loads that miss the
-    // non-coherent cache levels), and the stores have completed
-    // (vmcnt(0)) before the counter increment is issued; the reads are
-    // issued after the increment's result, on which they depend, has
-    // returned.  That orders them without the release / acquire fences,
-    // which would write back and invalidate this XCD's whole L2 (measured
-    // at ~5 us per call).
+    // coherent with this one.  Publication follows the HIP memory model:
+    // the records are written as agent-scope relaxed atomics (stores
+    // written through past the non-coherent levels), the arrival is an
+    // agent-scope release RMW on the tile's counter, and the workgroup that
+    // observes the final count issues an agent-scope acquire fence before
+    // it reads the records.  The release orders this wavefront's record
+    // stores (program order within the wavefront, then the release at
+    // agent scope) before the increment; every earlier arrival's increment
+    // heads a release sequence the last RMW reads from, so the acquire
+    // fence makes all `splits` records visible.
     constexpr int RECF = 2 * NT * 256 + 32;  // floats per record
     const int64_t tile = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
     float* mine = ws + (tile * splits + blockIdx.z) * RECF;
@@ -311,12 +313,12 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
       put(mine + 2 * NT * 256 + c, ssum[0]);
       put(mine + 2 * NT * 256 + 16 + c, ssum[1]);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     int arrived = 0;
     if (lane == 0)
-      arrived = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED,
+      arrived = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELEASE,
                                        __HIP_MEMORY_SCOPE_AGENT);
     if (__builtin_amdgcn_readfirstlane(arrived) != splits - 1) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 #pragma unroll
     for (int q = 0; q < 2 * NT; ++q) acc[q >> 1][q & 1] = f32x4{0.f, 0.f, 0.f, 0.f};
     ssum[0] = ssum[1] = 0.f;
@@ -638,6 +640,11 @@ namespace {
 //   kw: wavefronts per workgroup splitting its K range: NT = 1 runs up to 16,
 //       with one stage of 8 steps when the range is short and stages of 4
 //       otherwise; NT > 1 up to 8 wavefronts of about 8 steps (two stages of 4).
+// Plans split K only for at most kMaxSplitTiles output tiles; their counters
+// fill the workspace's first kSplitCounterBytes.
+constexpr int kMaxSplitTiles = 127;
+constexpr size_t kSplitCounterBytes = 512;
+static_assert(kMaxSplitTiles * sizeof(int) <= kSplitCounterBytes, "counter region");
 struct LinearPlan {
   int nt, kw, stage, splits;
   dim3 grid;
@@ -652,7 +659,7 @@ LinearPlan linear_plan(int rows, int n, int k, int act, bool can_split) {
   }
   const int cols = act == PA_ACT_SILU_MUL ? 16 : 16 * p.nt;
   const long long tiles = (long long)((n + cols - 1) / cols) * ((rows + 31) / 32);
-  if (can_split && nsteps >= 64 && tiles < 128)
+  if (can_split && nsteps >= 64 && tiles <= kMaxSplitTiles)
     p.splits = (int)std::max(1LL, std::min({8LL, 256 / tiles, (long long)nsteps / 16}));
   const int steps = (nsteps + p.splits - 1) / p.splits;  // per workgroup
   p.kw = std::max(1, std::min(8, (steps + 7) / 8));
@@ -665,14 +672,15 @@ LinearPlan linear_plan(int rows, int n, int k, int act, bool can_split) {
   p.grid = dim3((n + cols - 1) / cols, (rows + 31) / 32, p.splits);
   return p;
 }
-// Workspace bytes of a split plan: one counter per tile (256-byte aligned
-// block), then one record per (tile, split) of 2 NT x 64 partial f32x4 plus
-// 32 sums of squares.
+// Workspace of a split plan: a counter region of fixed size (one int per
+// tile for the largest tile count that splits), then one record per (tile,
+// split) of 2 NT x 64 partial f32x4 plus 32 sums of squares.  The counter
+// region does not depend on the plan, so one workspace serves calls of
+// different shapes in any order: every counter is back at zero after a call.
 size_t linear_ws_bytes(const LinearPlan& p) {
   if (p.splits <= 1) return 0;
   const size_t tiles = (size_t)p.grid.x * p.grid.y;
-  const size_t counters = (tiles * sizeof(int) + 255) / 256 * 256;
-  return counters + tiles * p.splits * (2 * p.nt * 256 + 32) * sizeof(float);
+  return kSplitCounterBytes + tiles * p.splits * (2 * p.nt * 256 + 32) * sizeof(float);
 }
 }  // namespace
 
@@ -720,10 +728,7 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   const int nt = plan.nt, kw = plan.kw, stage = plan.stage;
   const dim3 grid = plan.grid;
   int* counters = (int*)workspace;
-  float* ws = plan.splits > 1
-                  ? (float*)((char*)workspace +
-                             ((size_t)grid.x * grid.y * sizeof(int) + 255) / 256 * 256)
-                  : nullptr;
+  float* ws = plan.splits > 1 ? (float*)((char*)workspace + kSplitCounterBytes) : nullptr;
   hipStream_t s = (hipStream_t)stream;
   auto* o = (uint16_t*)out;
   auto* xx = (const uint16_t*)x;
