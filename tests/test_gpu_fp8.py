@@ -182,3 +182,100 @@ def test_prefill_fp8_tiled_shapes(pa, oracle, hq, hkv, d, pasts, chunks):
                                  oracle.fp8_decode(vc), bt, cu, past)
     assert np.isfinite(got).all()
     assert_close(got, ref, BF16_ATOL, BF16_RTOL, f"fp8 prefill {hq}/{hkv}x{d}")
+
+
+def assert_same_specials(got, ref, what):
+    """NaN where the reference is NaN, the same signed infinities, and the
+    finite entries within the bf16 bar."""
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), (
+        f"{what}: NaN pattern differs ({np.isnan(got).sum()} vs {np.isnan(ref).sum()})")
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref)), f"{what}: +inf pattern"
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref)), f"{what}: -inf pattern"
+    fin = np.isfinite(ref)
+    assert_close(got[fin], ref[fin], BF16_ATOL, BF16_RTOL, what)
+
+
+def plant_codes(rng, kc, vc, bt, ctx, hkv, d):
+    """Writes the reference's special and off-OCP codes into visible cache
+    entries, one pattern per sequence (sequences 0-5), and NaN / inf codes
+    past the context of sequence 6.  kc / vc: reference-layout codes."""
+    def at(b, tok):
+        return bt[b, tok // 16], tok % 16
+    blk, off = at(0, ctx[0] // 3)
+    kc[blk, 1, off, 5] = 0x80                       # K NaN: every head of kv head 1
+    blk, off = at(1, ctx[1] - 1)
+    kc[blk, 0, off, 7] = 0x7C                       # K +inf: NaN where q[7] > 0
+    blk, off = at(2, 10)
+    vc[blk, hkv - 1, off, d - 1] = 0xFC             # V -inf in one dim
+    blk, off = at(3, ctx[3] // 2)
+    vc[blk, 0, off, 0] = 0x80                       # V NaN in one dim
+    blk, off = at(3, ctx[3] // 2 + 1)
+    vc[blk, 0, off, 1] = 0x7C                       # and V +inf in another
+    # off-OCP finite codes: subnormal-field codes in K, every one in V
+    sub = np.array([1, 2, 3, 4, 5, 6, 7, 0x81, 0x82, 0x83, 0x84, 0x85, 0x86, 0x87], np.uint8)
+    big = np.array([0x7F, 0xFF, 0x78, 0xF8, 0x7B, 0xFB, 0x7D, 0xFD, 0x7E, 0xFE], np.uint8)
+    for b, codes_k, codes_v in ((4, sub, np.concatenate([sub, big])), (5, sub, sub)):
+        n = int(ctx[b])
+        for tok in rng.choice(n, min(n, 40), replace=False):
+            blk, off = at(b, int(tok))
+            h = rng.integers(0, hkv)
+            kc[blk, h, off, rng.integers(0, d)] = rng.choice(codes_k)
+            vc[blk, h, off, rng.integers(0, d)] = rng.choice(codes_v)
+    n = int(ctx[6])
+    if n % 16:
+        blk = bt[6, (n - 1) // 16]
+        kc[blk, :, n % 16:, 0] = 0x80
+        vc[blk, :, n % 16:, 1] = 0x7C
+
+
+@pytest.mark.parametrize("B,ctx_hi", [(7, 3000), (64, 2048)])
+def test_decode_fp8_special_codes(pa, oracle, B, ctx_hi):
+    # The reference decodes 0x80 as NaN and 0x7C / 0xFC as +-inf, and
+    # 0x01-0x07 / 0x7F as finite values the OCP conversion reads otherwise
+    # (kv_cache_fp8.rs:188-212).  Attention over such codes equals the
+    # oracle's attention over the reference-decoded caches: NaN / inf where
+    # it has them, the finite entries within the bf16 bar, codes past the
+    # context ignored.  B 7: partitions merged by the reduce kernel; B 64:
+    # merged inside the workgroup.
+    rng = np.random.default_rng(B)
+    hq, hkv, d = 32, 8, 128
+    ctx = rng.integers(ctx_hi // 2, ctx_hi + 1, B).astype(np.int32)
+    ctx[6] = ctx_hi - 5
+    case, kc, vc = fp8_decode_case(oracle, rng, B, hq, hkv, d, ctx)
+    plant_codes(rng, kc, vc, case["block_tables"], ctx, hkv, d)
+    got, ref = run_fp8_decode(pa, oracle, case, kc, vc)
+    assert np.isnan(ref[0]).any() and np.isinf(ref[2]).any()
+    assert_same_specials(got, ref, f"fp8 decode specials B {B}")
+
+
+def test_prefill_fp8_special_codes(pa, oracle):
+    # The same codes under the chunked-prefill mask: a code among the past
+    # keys reaches every query row, one among the new keys only the rows at
+    # or after it.
+    rng = np.random.default_rng(77)
+    hq, hkv, d = 32, 8, 128
+    pasts, chunks = [100, 0, 64, 300, 17, 250, 33], [150, 200, 70, 20, 90, 64, 50]
+    B = len(pasts)
+    ctx = np.array([p + c for p, c in zip(pasts, chunks)], np.int32)
+    nblk = [(int(c) + 15) // 16 for c in ctx]
+    nb = sum(nblk) + 5
+    perm = rng.permutation(nb).astype(np.int32)
+    bt = np.zeros((B, max(nblk)), np.int32)
+    o = 0
+    for b in range(B):
+        bt[b, :nblk[b]] = perm[o:o + nblk[b]]
+        o += nblk[b]
+    kc = oracle.fp8_encode(rng.standard_normal((nb, hkv, 16, d), dtype=np.float32))
+    vc = oracle.fp8_encode(rng.standard_normal((nb, hkv, 16, d), dtype=np.float32))
+    plant_codes(rng, kc, vc, bt, ctx, hkv, d)
+    q = oracle.f32_to_bf16(rng.standard_normal((sum(chunks), hq, d), dtype=np.float32))
+    cu = np.concatenate([[0], np.cumsum(chunks)]).astype(np.int32)
+    past = np.asarray(pasts, np.int32)
+    out = pa.prefill(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt),
+                     to_dev(cu), to_dev(past), max(chunks))
+    got = oracle.bf16_to_f32(to_np(out))
+    ref = oracle.paged_attention(oracle.bf16_to_f32(q), oracle.fp8_decode(kc),
+                                 oracle.fp8_decode(vc), bt, cu, past)
+    assert np.isnan(ref).any() and np.isinf(ref).any() and np.isfinite(ref).any()
+    assert_same_specials(got, ref, "fp8 prefill specials")

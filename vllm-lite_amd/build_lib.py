@@ -21,17 +21,10 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", f"--offload-arch={ARCH}"]
 
 
-# The attention kernels mask every value that could be NaN (stale cache
-# slots) with a select before any max/exp, so they are built without NaN
-# semantics: fmaxf then maps to a bare v_max_f32 with no canonicalisation.
-NO_NAN_SOURCES = {"decode.hip", "prefill.hip"}
-
-
 def _compile(src):
     path = os.path.join(CSRC, src)
     obj = os.path.join(OBJ, src + ".o")
-    extra = ["-fno-honor-nans"] if src in NO_NAN_SOURCES else []
-    cmd = [HIPCC] + COMMON + DEVICE_FLAGS + extra + ["-c", path, "-o", obj]
+    cmd = [HIPCC] + COMMON + DEVICE_FLAGS + ["-c", path, "-o", obj]
     if src.endswith(".cpp"):
         cmd = [HIPCC, "-x", "hip"] + COMMON + DEVICE_FLAGS + ["-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -110,7 +110,9 @@ __device__ inline void merge_in_workgroup(uint16_t* __restrict__ out_group, cons
       num += a * so[w][hc][d];
       den += a * sml[w][hc][1];
     }
-    out_group[idx] = f32_to_bf16_bits(den > 0.f ? num / den : 0.f);
+    // den is 0 only for a row with no keys; a NaN den (a NaN score) must
+    // reach the output, so the test is != 0, not > 0
+    out_group[idx] = f32_to_bf16_bits(den != 0.f ? num / den : 0.f);
   }
 }
 
@@ -289,7 +291,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
   }
   if (c >= G) return;
   if (num_parts == 1) {
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    const float inv = lsum != 0.f ? 1.f / lsum : 0.f;
     uint16_t* orow = out + ((int64_t)seq * Hq + head) * D + 4 * j;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -314,10 +316,12 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
 // MFMA decode over FP8 caches (the reference's E4M3 codes, one byte per
 // element), q / out bf16.  Same work split, online softmax and epilogue as
 // decode_mfma_kernel; the operands are converted to bf16 in registers with
-// v_cvt_scalef32_pk_bf16_fp8 (scale 1).  That conversion reads OCP E4M3,
-// which gives the reference's value for every code its encoder produces from
-// finite input; only the NaN / inf codes (0x80, 0x7C, 0xFC) read as -0 and
-// +-384 here.
+// v_cvt_scalef32_pk_bf16_fp8 (scale 1), except for the rare 8-byte groups
+// that hold a code the OCP reading gets wrong for the reference, which take
+// an exact integer decode (fp8x8_to_bf16): every code, NaN (0x80) and +-inf
+// (0x7C / 0xFC) included, enters the MFMAs as the reference's value, and
+// NaN / inf propagate through the scores, the softmax and P·V as IEEE
+// arithmetic does in the reference.
 //
 // The lane layout is chosen so that every load is contiguous:
 //  * QK step s: lane (c, j) supplies K rows of tokens
@@ -427,17 +431,19 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
     for (int dt = 0; dt < DT; ++dt)
       st.v[dt] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(vr + dt * 16 * kBlock));
   };
-  auto compute = [&](Step& st) {
+  auto compute_step = [&](Step& st, auto exact_c) {
+    constexpr bool EXACT = decltype(exact_c)::value;
+    auto cvt = [](uint32_t lo, uint32_t hi) {
+      return EXACT ? fp8x8_to_bf16_exact(lo, hi) : fp8x8_to_bf16(lo, hi);
+    };
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const u32x4& w0 = st.k0[s / 2];
       const u32x4& w1 = st.k1[s / 2];
       const int h = 2 * (s & 1);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(w0[h], w0[h + 1]), qv[s], s0, 0,
-                                                   0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp8x8_to_bf16(w1[h], w1[h + 1]), qv[s], s1, 0,
-                                                   0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cvt(w0[h], w0[h + 1]), qv[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cvt(w1[h], w1[h + 1]), qv[s], s1, 0, 0, 0);
     }
     // x[i] <-> token tv0 + i of this lane's block (s0: i < 4, s1: i >= 4)
     float x[8];
@@ -483,7 +489,25 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          fp8x8_to_bf16((uint32_t)st.v[dt], (uint32_t)(st.v[dt] >> 32)), pb, o[dt], 0, 0, 0);
+          cvt((uint32_t)st.v[dt], (uint32_t)(st.v[dt] >> 32)), pb, o[dt], 0, 0, 0);
+  };
+  // Codes the hardware conversion reads differently from the reference
+  // (NaN / inf / off-OCP codes; never produced from finite input) are
+  // tracked per lane while the partition streams; a wavefront that met any
+  // recomputes its partition with the exact integer decode (rare, and kept
+  // out of the streaming loop so that loop's registers and code stay those
+  // of the plain conversion).
+  uint32_t exotic = 0;
+  auto compute = [&](Step& st) {
+#pragma unroll
+    for (int s = 0; s < KS / 2; ++s)
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        exotic |= fp8_exotic_bits(st.k0[s][h]) | fp8_exotic_bits(st.k1[s][h]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      exotic |= fp8_exotic_bits((uint32_t)st.v[dt]) | fp8_exotic_bits((uint32_t)(st.v[dt] >> 32));
+    compute_step(st, std::false_type{});
   };
 
   // The q loads complete here, once: a wait for them that the compiler placed
@@ -500,6 +524,17 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
     if (ib + 4 < nblk) load_step(ib + 4, sa);
     compute(sb);
   }
+  if (__builtin_amdgcn_ballot_w64((exotic & 0x80808080u) != 0)) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m = kNegBig;
+    lsum = 0.f;
+#pragma unroll 1
+    for (int ib = 0; ib < nblk; ib += 2) {
+      load_step(ib, sa);
+      compute_step(sa, std::true_type{});
+    }
+  }
 
   lsum += shfl_xor_f(lsum, 16);
   lsum += shfl_xor_f(lsum, 32);
@@ -509,7 +544,7 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
   }
   if (c >= G) return;
   if (num_parts == 1) {
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    const float inv = lsum != 0.f ? 1.f / lsum : 0.f;
     uint16_t* orow = out + ((int64_t)seq * Hq + head) * D + 4 * j;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -611,7 +646,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
       acc += ps[t] * (Elem<TC>::load(vc + (((int64_t)b * Hkv + kvh) * D + d) * kBlock + t % kBlock) * vs);
     }
     if (num_parts == 1) {
-      Elem<T>::store(out + ((int64_t)seq * Hq + h) * D + d, l > 0.f ? acc / l : 0.f);
+      Elem<T>::store(out + ((int64_t)seq * Hq + h) * D + d, l != 0.f ? acc / l : 0.f);
     } else {
       ws_o[(((int64_t)seq * Hq + h) * num_parts + part) * D + d] = acc;
     }
@@ -769,7 +804,7 @@ __global__ __launch_bounds__(1024) void decode_f32_group_kernel(
       const int64_t row = (int64_t)seq * Hq + kvh * G + g;
       if (num_parts == 1) {
         const float l = mls[g][1];
-        out[row * D + d] = l > 0.f ? acc / l : 0.f;
+        out[row * D + d] = l != 0.f ? acc / l : 0.f;
       } else {
         ws_o[(row * num_parts + part) * D + d] = acc;
         if (d == 0) {
@@ -834,7 +869,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
   if (lane == 0) ml[1][wave] = L;
   __syncthreads();
   L = ml[1][0] + ml[1][1] + ml[1][2] + ml[1][3];
-  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const float inv = L != 0.f ? 1.f / L : 0.f;
   if (two) {
     float a0 = 0.f, a1 = 0.f;
     for (int p0 = wave; p0 < np; p0 += 4 * kRU) {
@@ -903,6 +938,42 @@ extern "C" size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, 
 }
 
 namespace {
+// The launch configuration pa_decode picks for a call: kernel family,
+// partition length and count, and how many partitions one workgroup merges.
+struct DecodePlan {
+  bool mfma, f32_group;
+  int part_len, np, merge_waves;
+  size_t ws_bytes;  // workspace the launch needs (0: none)
+};
+DecodePlan decode_plan(int32_t dtype, bool quantized, int32_t num_seqs, int32_t num_heads,
+                       int32_t num_kv_heads, int32_t head_dim, int32_t max_context_len) {
+  DecodePlan p{};
+  const int G = num_heads / num_kv_heads;
+  const bool fp8 = dtype == PA_DTYPE_FP8_E4M3;
+  p.mfma = !quantized && (dtype == PA_DTYPE_BF16 || fp8) && G <= 16 &&
+           (head_dim == 64 || head_dim == 128 || head_dim == 256);
+  // f32: the group kernel for head dims that divide 256 (in 4-float steps)
+  // and groups of at most kF32MaxG heads, the generic kernel otherwise
+  p.f32_group = dtype == PA_DTYPE_F32 && G <= kF32MaxG && head_dim <= 256 &&
+                256 % head_dim == 0 && head_dim % 16 == 0;
+  p.part_len = p.mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len, head_dim,
+                                         fp8 ? 1 : 2)
+                      : kPart;
+  p.np = num_partitions(max_context_len, p.part_len);
+  // MFMA kernels: up to 4 partitions (8 for head_dim <= 128) are taken by one
+  // workgroup (one wavefront each) and merged in LDS, with no workspace and no
+  // reduce launch.
+  p.merge_waves = !p.mfma || p.np <= 1 ? 1
+                  : p.np == 2           ? 2
+                  : p.np <= 4           ? 4
+                  : (p.np <= 8 && head_dim <= 128) ? 8
+                                                   : 1;
+  p.ws_bytes = p.np > 1 && p.merge_waves == 1
+                   ? (size_t)num_seqs * num_heads * p.np * (head_dim + 2) * sizeof(float)
+                   : 0;
+  return p;
+}
+
 int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v_cache,
                     const float* kv_scales, const int32_t* block_tables,
                     int32_t max_blocks_per_seq, const int32_t* context_lens,
@@ -924,32 +995,18 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   if (num_seqs == 0 || max_context_len == 0) return PA_OK;
   PA_REQUIRE(out && q && k_cache && v_cache && block_tables && context_lens, PA_ERR_INVALID_ARG,
              "pa_decode: null pointer");
+  const DecodePlan plan = decode_plan(dtype, kv_scales != nullptr, num_seqs, num_heads,
+                                      num_kv_heads, head_dim, max_context_len);
   const int G = num_heads / num_kv_heads;
   const bool fp8 = dtype == PA_DTYPE_FP8_E4M3;
-  const bool mfma = !kv_scales && (dtype == PA_DTYPE_BF16 || fp8) && G <= 16 &&
-                    (head_dim == 64 || head_dim == 128 || head_dim == 256);
-  // f32: the group kernel for head dims that divide 256 (in 4-float steps)
-  // and groups of at most kF32MaxG heads, the generic kernel otherwise
-  const bool f32_group = dtype == PA_DTYPE_F32 && G <= kF32MaxG && head_dim <= 256 &&
-                         256 % head_dim == 0 && head_dim % 16 == 0;
-  const int part_len =
-      mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len, head_dim, fp8 ? 1 : 2)
-           : kPart;
-  const int np = num_partitions(max_context_len, part_len);
+  const bool mfma = plan.mfma, f32_group = plan.f32_group;
+  const int part_len = plan.part_len, np = plan.np, merge_waves = plan.merge_waves;
   PA_REQUIRE(np <= 1024, PA_ERR_UNSUPPORTED,
              "pa_decode: context of %d tokens needs %d > 1024 partitions", max_context_len, np);
-  // MFMA kernels: up to 4 partitions (8 for head_dim <= 128) are taken by one
-  // workgroup (one wavefront each) and merged in LDS, with no workspace and no
-  // reduce launch.
-  const int merge_waves = !mfma || np <= 1 ? 1
-                          : np == 2         ? 2
-                          : np <= 4         ? 4
-                          : (np <= 8 && head_dim <= 128) ? 8
-                                                         : 1;
   float* ws_o = nullptr;
   float* ws_ml = nullptr;
-  if (np > 1 && merge_waves == 1) {
-    const size_t need = (size_t)num_seqs * num_heads * np * (head_dim + 2) * sizeof(float);
+  if (plan.ws_bytes) {
+    const size_t need = plan.ws_bytes;
     PA_REQUIRE(workspace && workspace_bytes >= need, PA_ERR_WORKSPACE,
                "pa_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
     ws_o = (float*)workspace;
@@ -1083,3 +1140,4 @@ int32_t decode_strided(void* out, const void* q, int64_t q_row, const void* k_ca
                      num_blocks, scale, workspace, workspace_bytes, dtype, stream, q_row);
 }
 }  // namespace pa
+

@@ -20,15 +20,65 @@ typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
-// Eight FP8-E4M3 codes (little-endian bytes of lo, hi) to bf16, exactly
-// (every E4M3 value is a bf16 value), with the hardware's unscaled
-// conversion.
+// FP8-E4M3 codes in the reference's convention
+// (crates/model/src/components/kv_cache_fp8.rs:188-212) to bf16.
+//
+// fp8x8_to_bf16 converts eight codes (little-endian bytes of lo, hi) with
+// the hardware's unscaled conversion, which reads OCP E4M3.  That agrees
+// with the reference's decode on every code except those with exponent
+// field 0 and a nonzero byte (0x80 is NaN there, 0x01-0x07 / 0x81-0x87 read
+// 2^-7 (1 + m/8), not OCP subnormals) and those with exponent field 15
+// (0x7C / 0xFC are +-inf there, 0x7F / 0xFF read +-480, not NaN; the rest
+// agree).  Kernels OR fp8_exotic_bits over the words they convert and take
+// fp8x8_to_bf16_exact, the reference's decode, when bit 7 of any byte is set.
 __device__ inline bf16x8 fp8x8_to_bf16(uint32_t lo, uint32_t hi) {
   const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
   const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
   const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
   const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
   return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Bit 7 of each byte of the result is set where the hardware conversion
+// differs (or may differ) from the reference: exponent field 15, or
+// exponent field 0 with a nonzero byte.  The other bits are garbage, so
+// callers OR the results and test them against 0x80808080.  Per byte, with
+// y = b & 0x7F: y + 0x08 reaches bit 7 iff y >= 0x78 (exponent 15);
+// y + 0x78 iff y >= 8 (exponent above 0); y + 0x7F iff y >= 1.  No sum
+// carries into the next byte.
+__host__ __device__ inline uint32_t fp8_exotic_bits(uint32_t w) {
+  const uint32_t y = w & 0x7F7F7F7Fu;
+  const uint32_t e15 = y + 0x08080808u;
+  const uint32_t e_pos = y + 0x78787878u;
+  const uint32_t y_pos = y + 0x7F7F7F7Fu;
+  return e15 | (~e_pos & (y_pos | w));
+}
+
+// Two codes held in the low bytes of the 16-bit halves of x (bits 8-15 and
+// 24-31 zero) to two bf16s with the reference's decode, integer arithmetic
+// only: sign and (e, m) move into place with the exponent rebiased by
+// 127 - 7 = 120 (every such value is a bf16 value); (e, m) = 0 gives a
+// signed zero, except 0x80 which is NaN; 0x7C / 0xFC are +-inf.
+__host__ __device__ inline uint32_t fp8x2_ref_bf16x2(uint32_t x) {
+  const uint32_t lane1 = 0x00010001u;
+  const uint32_t m = x & 0x007F007Fu;
+  const uint32_t sgn = (x & 0x00800080u) << 8;
+  const uint32_t nz = ((m + 0x007F007Fu) >> 7) & lane1;               // m != 0
+  const uint32_t inf = (~((m ^ 0x007C007Cu) + 0x007F007Fu) >> 7) & lane1;  // m == 0x7C
+  const uint32_t nan = ~nz & (x >> 7) & lane1;                         // x == 0x80
+  uint32_t v = (((m << 4) + 0x3C003C00u) & (nz * 0xFFFFu)) | sgn;
+  v = (v & ~(inf * 0xFFFFu)) | ((sgn | 0x7F807F80u) & (inf * 0xFFFFu));
+  v = (v & ~(nan * 0xFFFFu)) | (0x7FC07FC0u & (nan * 0xFFFFu));
+  return v;
+}
+
+__device__ inline bf16x8 fp8x8_to_bf16_exact(uint32_t lo, uint32_t hi) {
+  typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+  const u32x4_t r = {fp8x2_ref_bf16x2(__builtin_amdgcn_perm(0u, lo, 0x0C010C00u)),
+                     fp8x2_ref_bf16x2(__builtin_amdgcn_perm(0u, lo, 0x0C030C02u)),
+                     fp8x2_ref_bf16x2(__builtin_amdgcn_perm(0u, hi, 0x0C010C00u)),
+                     fp8x2_ref_bf16x2(__builtin_amdgcn_perm(0u, hi, 0x0C030C02u))};
+  return __builtin_bit_cast(bf16x8, r);
 }
 
 // bf16 <-> f32 on raw 16-bit patterns (round to nearest even, NaN kept quiet).

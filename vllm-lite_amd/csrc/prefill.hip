@@ -191,7 +191,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
     l += shfl_xor_f(l, 32);
     const int row = row0 + 16 * nt + c;
     if (row >= qlen) continue;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const float inv = l != 0.f ? 1.f / l : 0.f;
     uint16_t* orow = out + ((int64_t)(q_begin + row) * Hq + h) * D + 4 * j;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -481,21 +481,47 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   // (every E4M3 value is a bf16 value).  All threads of the workgroup.
   // Tile t is staged in slot t % 2 (issue_tile's `buf` is the slot for FP8)
   // and converted one tile boundary before its first use.
+  // A wavefront whose units hold a code the hardware conversion reads
+  // differently from the reference (NaN / inf / off-OCP codes; never
+  // produced from finite input) converts them with the exact integer
+  // decode.  Each thread's units are read first, so their LDS reads are in
+  // flight together.
   auto convert_tile = [&](int buf, int slot) {
     if constexpr (FP8) {
-      for (int e = threadIdx.x; e < KT * D / 8; e += blockDim.x) {
+      constexpr int UPT = KT * D / 8 / (64 * W);  // 8-byte units per thread, K and V each
+      static_assert(UPT * 64 * W == KT * D / 8, "tile units per thread");
+      uint2 kw[UPT], vw[UPT];
+      uint32_t ex = 0;
+#pragma unroll
+      for (int i = 0; i < UPT; ++i) {
+        const int e = threadIdx.x + i * 64 * W;
         const int r = e / (D / 8), u = e % (D / 8);
-        const uint2 w = *reinterpret_cast<const uint2*>(&stage[slot][0][r * D + (u ^ fsw(r)) * 8]);
-        *reinterpret_cast<bf16x8*>(&smem[0][buf][r * (D * 2) + (u ^ kswz(r)) * 16]) =
-            fp8x8_to_bf16(w.x, w.y);
+        kw[i] = *reinterpret_cast<const uint2*>(&stage[slot][0][r * D + (u ^ fsw(r)) * 8]);
+        vw[i] = *reinterpret_cast<const uint2*>(&stage[slot][1][e * 8]);  // V dim rows
       }
-      for (int e = threadIdx.x; e < KT * D / 8; e += blockDim.x) {
-        const int bd = e / 2, h = e % 2;  // bd = block * D + dim
-        const int d = bd % D;
-        const uint2 w = *reinterpret_cast<const uint2*>(&stage[slot][1][bd * 16 + 8 * h]);
-        *reinterpret_cast<bf16x8*>(&smem[1][buf][bd * 32 + (h ^ vswz(d)) * 16]) =
-            fp8x8_to_bf16(w.x, w.y);
-      }
+#pragma unroll
+      for (int i = 0; i < UPT; ++i)
+        ex |= fp8_exotic_bits(kw[i].x) | fp8_exotic_bits(kw[i].y) | fp8_exotic_bits(vw[i].x) |
+              fp8_exotic_bits(vw[i].y);
+      auto store = [&](auto exact_c) {
+#pragma unroll
+        for (int i = 0; i < UPT; ++i) {
+          const int e = threadIdx.x + i * 64 * W;
+          const int r = e / (D / 8), u = e % (D / 8);
+          const int bd = e / 2, h = e % 2;  // V: bd = block * D + dim
+          const int d = bd % D;
+          *reinterpret_cast<bf16x8*>(&smem[0][buf][r * (D * 2) + (u ^ kswz(r)) * 16]) =
+              decltype(exact_c)::value ? fp8x8_to_bf16_exact(kw[i].x, kw[i].y)
+                                       : fp8x8_to_bf16(kw[i].x, kw[i].y);
+          *reinterpret_cast<bf16x8*>(&smem[1][buf][bd * 32 + (h ^ vswz(d)) * 16]) =
+              decltype(exact_c)::value ? fp8x8_to_bf16_exact(vw[i].x, vw[i].y)
+                                       : fp8x8_to_bf16(vw[i].x, vw[i].y);
+        }
+      };
+      if (__builtin_amdgcn_ballot_w64((ex & 0x80808080u) != 0))
+        store(std::true_type{});
+      else
+        store(std::false_type{});
     }
   };
   // Sᵀ for the 32 keys of step ST of the tile in buffer `buf`.  MFMA tile
@@ -743,7 +769,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     const float l = lacc[nt][0];
     const int row = r0 + 16 * nt + c;
     if (row >= qlen) continue;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const float inv = l != 0.f ? 1.f / l : 0.f;
     uint16_t* orow = out + ((int64_t)(q_begin + row) * Hq + head) * D + 4 * j;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -826,7 +852,7 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
       acc[i] = a;
     }
   }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float inv = l != 0.f ? 1.f / l : 0.f;
   for (int i = 0; i * 64 + lane < D; ++i)
     Elem<T>::store(out + ((int64_t)(q_begin + row) * Hq + h) * D + i * 64 + lane, acc[i] * inv);
 }
