@@ -213,6 +213,27 @@ int32_t pa_decode(void* out, const void* q, const void* k_cache, const void* v_c
                   float scale, void* workspace, size_t workspace_bytes, int32_t dtype,
                   pa_stream_t stream);
 
+/* pa_decode without a workspace argument and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops or harnesses
+ * that forbid hipMalloc).  Arguments and results are those of pa_decode;
+ * the split-K partial results go to a fixed device array inside the library
+ * (pa_decode_noalloc_scratch_bytes() bytes, 64 MiB, one per GPU, held until
+ * the process ends; its address is looked up once per device on the first
+ * call).  Sizes whose split needs more (pa_decode_workspace_size() bounds
+ * it) return PA_ERR_WORKSPACE without launching.  Calls on one GPU share the
+ * array: calls that may overlap (other streams, other threads) race. */
+int32_t pa_decode_noalloc(void* out, const void* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_tables, int32_t max_blocks_per_seq,
+                          const int32_t* context_lens, int32_t max_context_len,
+                          int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t num_blocks, float scale, int32_t dtype,
+                          pa_stream_t stream);
+
+/* Bytes of pa_decode_noalloc's fixed split-K scratch.  No reference
+ * counterpart. */
+size_t pa_decode_noalloc_scratch_bytes(void);
+
 /* pa_decode over a quantised PagedKvCache (int8 values in f32 caches with
  * one scale per block, pa_kv_cache_create_quantized): every K / V element
  * is read as value * block_scales[block], which is what the reference's

@@ -21,6 +21,9 @@ SIGNATURES = {
     "pa_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
     "pa_decode": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                          _p, _sz, _i32, _p]),
+    "pa_decode_noalloc": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32,
+                                 _i32, _f32, _i32, _p]),
+    "pa_decode_noalloc_scratch_bytes": (_sz, []),
     "pa_prefill": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                           _i32, _f32, _i32, _p]),
     "pa_rms_norm": (_i32, [_p, _p, _p, _p, _i32, _i32, _f32, _i32, _p]),

@@ -21,6 +21,7 @@
 //    processed per step (32 = the MFMA K dimension of the P·V product).
 //  * decode_generic_kernel (f32 or bf16, any D <= 512, any group size): a
 //    plain reference-grade kernel, one workgroup per query head.
+#include <mutex>
 #include <type_traits>
 
 #include "pa_common.hpp"
@@ -1141,3 +1142,71 @@ int32_t decode_strided(void* out, const void* q, int64_t q_row, const void* k_ca
 }
 }  // namespace pa
 
+// ---------------------------------------------------------------------------
+// pa_decode without a workspace argument: the split-K partial results go to
+// `scratch`, a fixed device array of this library (one copy per GPU, alive
+// until the process ends).  For callers that cannot allocate (HIP graph
+// capture, serving loops that forbid hipMalloc).  Nothing in it needs to
+// start at zero: every partition of every sequence writes its record before
+// decode_reduce_kernel reads it.  Calls that overlap on one GPU share the
+// array and race.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kDecodeScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (host code must use
+// it, never the array's name), looked up once per device.
+int32_t scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("pa_decode_noalloc: hipGetDevice failed (%s)", hipGetErrorString(e));
+    return PA_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("pa_decode_noalloc: hipGetSymbolAddress(scratch) failed on device %d (%s)", dev,
+                hipGetErrorString(e));
+      return PA_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PA_OK;
+}
+}  // namespace
+
+extern "C" size_t pa_decode_noalloc_scratch_bytes(void) { return kDecodeScratchBytes; }
+
+extern "C" int32_t pa_decode_noalloc(void* out, const void* q, const void* k_cache,
+                                     const void* v_cache, const int32_t* block_tables,
+                                     int32_t max_blocks_per_seq, const int32_t* context_lens,
+                                     int32_t max_context_len, int32_t num_seqs,
+                                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                     int32_t num_blocks, float scale, int32_t dtype,
+                                     pa_stream_t stream) {
+  clear_error();
+  if (num_seqs > 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
+      num_heads % num_kv_heads == 0 && max_context_len > 0) {
+    const DecodePlan plan = decode_plan(dtype, false, num_seqs, num_heads, num_kv_heads,
+                                        head_dim, max_context_len);
+    PA_REQUIRE(plan.ws_bytes <= kDecodeScratchBytes, PA_ERR_WORKSPACE,
+               "pa_decode_noalloc: %d sequences x %d heads at context %d need %zu bytes of "
+               "split-K scratch, above the fixed %zu (use pa_decode with a workspace)",
+               num_seqs, num_heads, max_context_len, plan.ws_bytes, kDecodeScratchBytes);
+  }
+  void* ws = nullptr;
+  const int32_t rc = scratch_ptr(&ws);
+  if (rc != PA_OK) return rc;
+  return decode_impl(out, q, k_cache, v_cache, nullptr, block_tables, max_blocks_per_seq,
+                     context_lens, max_context_len, num_seqs, num_heads, num_kv_heads, head_dim,
+                     num_blocks, scale, ws, kDecodeScratchBytes, dtype, stream);
+}
