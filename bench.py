@@ -220,17 +220,26 @@ class Workload:
 
 
 def measured_traffic(config):
-    """HBM bytes per launch of the dominant call as last measured with
-    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by the copy calibration),
-    from profiles/hbm_traffic.txt; None when that file has no entry."""
+    """HBM bytes per launch of the dominant call as measured with rocprofv3
+    --pmc FETCH_SIZE / WRITE_SIZE (scaled by the copy calibration), read from
+    profiles/hbm_traffic.txt, with where they come from: (bytes, source) or
+    (None, None) when that file has no entry.  The run does not measure
+    them itself (counters need a profiler pass of their own); the source
+    names the commit and the kernel duration of that pass, so a bench line
+    whose avg_launch_us has moved away from it shows that the byte count may
+    be stale."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
     if not os.path.exists(path):
-        return None
+        return None, None
     for line in open(path):
         kv = dict(x.split("=", 1) for x in line.split() if "=" in x)
         if kv.get("config") == config:
-            return int(kv["fetch_bytes"]) + int(kv["write_bytes"])
-    return None
+            src = {"file": "profiles/hbm_traffic.txt",
+                   "method": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; copy-calibrated",
+                   "commit": kv.get("commit"),
+                   "profiled_launch_us": float(kv["launch_us"]) if "launch_us" in kv else None}
+            return int(kv["fetch_bytes"]) + int(kv["write_bytes"]), src
+    return None, None
 
 
 def time_attend(w, iters):
@@ -404,6 +413,58 @@ def copy_calibration(args):
                       "gbs_read_plus_write": round(2 * n / t / 1e9, 1)}), flush=True)
 
 
+def run_write(pa, args):
+    """The KV-cache write of BASELINE config 3's chunk: pa_reshape_and_cache
+    of 4 x 2048 new tokens (pasts 0 / 512 / 1024 / 2048, 8 kv heads x 128,
+    bf16) through seeded random block tables; the slot runs are
+    block-aligned, so every block goes whole.  HBM-bound: algorithmic bytes
+    = K and V read + written + the slots."""
+    g = torch.Generator().manual_seed(2)
+    hkv, d = 8, 128
+    pasts, chunk = [0, 512, 1024, 2048], 2048
+    nblks = [(p + chunk + 15) // 16 for p in pasts]
+    pool = sum(nblks) + 16
+    perm = torch.randperm(pool, generator=g)
+    slots, o = [], 0
+    for p, n in zip(pasts, nblks):
+        pos = torch.arange(p, p + chunk)
+        slots.append(perm[o:o + n][pos // 16] * 16 + pos % 16)
+        o += n
+    slots = torch.cat(slots).to(torch.int64).to(DEV)
+    t = slots.numel()
+    dg = torch.Generator(device=DEV).manual_seed(1234)
+    k = torch.randn(t, hkv, d, generator=dg, device=DEV).to(torch.bfloat16)
+    v = torch.randn(t, hkv, d, generator=dg, device=DEV).to(torch.bfloat16)
+    kc, vc = pa.ops.new_cache(pool, hkv, d, torch.bfloat16, DEV)
+
+    class W:
+        def attend(self):
+            pa.reshape_and_cache(k, v, kc, vc, slots)
+    w = W()
+    for _ in range(args.warmup):
+        w.attend()
+    tm = time_attend(w, max(args.steps, 20))
+    tf = None if args.no_flush else time_attend_flushed(w, max(args.steps, 20))
+    alg = 2 * 2 * t * hkv * d * 2 + t * 8
+    achieved = alg / tm / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "pa_reshape_and_cache (cache_write_kernel, whole blocks)",
+            "alg_bytes_per_launch": alg, "avg_launch_us": round(tm * 1e6, 2)}
+    if tf:
+        roof["flushed_launch_us"] = round(tf * 1e6, 2)
+        roof["flushed_frac"] = round(alg / tf / 1e9 / HBM_PEAK_GBS, 4)
+    print(json.dumps({
+        "metric": "paged KV-cache write tokens/s (config 3 chunk)",
+        "value": round(t / tm, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(tm * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) K/V, random block tables)",
+        "config": {"workload": "config 3 write: 4 x 2048 tokens, 8 kv heads x 128, bf16",
+                   "global_batch": 4, "seq_len": chunk, "parallelism": "none (1 GPU)"},
+        "roofline": roof, "cpu_baseline": None}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -411,7 +472,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="decode",
                     choices=["decode", "decode-fp8", "prefill", "prefill-fp8", "splitk", "qwen",
-                             "e2e", "copy"])
+                             "e2e", "copy", "write"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-flush", action="store_true",
                     help="skip the cache-flushed timing leg (keeps a kernel trace to warm launches)")
@@ -427,6 +488,8 @@ def main():
         return copy_calibration(args)
     if args.config == "e2e":
         return run_e2e(pa, args)
+    if args.config == "write":
+        return run_write(pa, args)
     w = Workload(pa, args.config)
     for _ in range(args.warmup):
         w.step()
@@ -444,9 +507,10 @@ def main():
         value = w.B * args.steps / el
         unit = "tokens/s"
         achieved = w.alg_bytes / t_attn / 1e9
+        traffic, traffic_src = measured_traffic(args.config)
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.config),
+                "traffic": traffic, "traffic_source": traffic_src,
                 "alg_bytes_per_launch": w.alg_bytes,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
         if t_flush:
@@ -466,9 +530,10 @@ def main():
     else:
         value = w.flops / t_attn / 1e12
         unit = "TFLOP/s"
+        traffic, traffic_src = measured_traffic(args.config)
         roof = {"bound": "mfma", "achieved": round(value, 2), "peak": BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(value / BF16_PEAK_TFLOPS, 4),
-                "traffic": measured_traffic(args.config),
+                "traffic": traffic, "traffic_source": traffic_src,
                 "kernel": ("pa_prefill (prefill_tiled_kernel, FP8 tiles)" if w.fp8 else
                            "pa_prefill (prefill_tiled_kernel)"), "flops_per_launch": w.flops,
                 "avg_launch_us": round(t_attn * 1e6, 2)}

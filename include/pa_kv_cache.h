@@ -159,7 +159,9 @@ int32_t pa_batch_qkv_rope_cache(pa_batch* batch, pa_kv_cache* cache, int32_t lay
  *   device f32 or NULL, scale = attn_factor / sqrt(D).
  * key == value == NULL (and inv_freq NULL): the step's K / V are already in
  * the cache and q is final (pa_batch_qkv_rope_cache ran); attention only.
- * Allocates (once, grown on demand) the decode workspace. */
+ * Allocates (once, grown on demand) the decode workspace; a call that would
+ * grow it while `stream` is capturing returns PA_ERR_WORKSPACE instead (run
+ * one eager step of the captured shape first). */
 int32_t pa_batch_attention(pa_batch* batch, pa_kv_cache* cache, int32_t layer, int32_t num_heads,
                            void* q, int64_t q_stride, const void* key, int64_t key_stride,
                            const void* value, int64_t value_stride, const float* inv_freq,

@@ -138,3 +138,35 @@ def test_prepare_rejects_bad_tables(pa):
     # the attention-only call itself runs (zero caches: zero output)
     out = batch.attention(cache, 0, q, None, None)
     assert out.shape == q.shape and not torch.isnan(out.float()).any()
+
+
+def test_decode_workspace_growth_refused_under_capture(pa):
+    # A decode step whose workspace would have to grow inside a stream
+    # capture returns an error (hipMalloc cannot be captured) instead of
+    # allocating; after one eager step of the shape the capture succeeds.
+    hq, hkv, d, nb = 8, 2, 128, 512
+    cache = pa.PagedKvCache(1, hkv, d, nb, torch.bfloat16, DEV)
+    batch = pa.StepBatch()
+    blocks = [list(range(i * 128, (i + 1) * 128)) for i in range(4)]
+    batch.set_capacity(2048)
+    batch.prepare(cache, [1] * 4, [1500] * 4, blocks)
+    q = torch.randn(4, hq, d, device=DEV).to(torch.bfloat16)
+    k = torch.randn(4, hkv, d, device=DEV).to(torch.bfloat16)
+    v = torch.randn(4, hkv, d, device=DEV).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="capturing"):
+        with torch.cuda.graph(g, stream=stream):
+            batch.attention(cache, 0, q, k, v)
+    torch.cuda.synchronize()
+    eager = batch.attention(cache, 0, q, k, v)
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=stream):
+        captured = batch.attention(cache, 0, q, k, v)
+    for _ in range(2):
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+    batch.close()
+    cache.close()

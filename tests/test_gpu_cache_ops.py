@@ -152,3 +152,101 @@ def test_block_hash(pa, oracle):
     blk = np.asarray(case["bits"], np.uint32).view(np.float32).reshape(1, 1, 16, 2)
     got = to_np(pa.block_hash(to_dev(blk), to_dev(np.array([0], np.int32)))).view(np.uint64)
     assert int(got[0]) == int(case["expect"])
+
+
+def prefill_slots(rng, nb, pasts, chunks):
+    """slot_mapping of chunked-prefill rows: sequence s writes positions
+    past_s .. past_s + chunk_s - 1 through its own random block table."""
+    nblk = [(p + c + 15) // 16 for p, c in zip(pasts, chunks)]
+    perm = rng.permutation(nb)
+    assert sum(nblk) <= nb
+    slots, o = [], 0
+    for p, c, n in zip(pasts, chunks, nblk):
+        table = perm[o:o + n]
+        o += n
+        pos = np.arange(p, p + c)
+        slots.append(table[pos // 16] * 16 + pos % 16)
+    return np.concatenate(slots).astype(np.int64)
+
+
+# runs of consecutive slots: block-aligned and unaligned starts, chunks
+# shorter than a block, a chunk ending mid-block, one slot skipped inside a
+# run (its block then goes token by token)
+PREFILL_CASES = [([0, 16, 37, 5, 130, 3], [64, 40, 130, 7, 77, 16]),
+                 ([0, 0, 8], [15, 17, 300])]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", range(len(PREFILL_CASES)))
+@pytest.mark.parametrize("h,d", [(8, 128), (2, 64), (1, 512), (3, 40)])
+def test_reshape_and_cache_prefill_runs(pa, oracle, dtype, case, h, d):
+    # the block-coalesced write path (whole blocks from runs of consecutive
+    # slots) and the token-by-token path around it, bit-exact against the
+    # oracle's per-token writes; untouched slots keep their contents
+    rng = np.random.default_rng(case * 100 + h + d)
+    pasts, chunks = PREFILL_CASES[case]
+    nb = sum((p + c + 15) // 16 for p, c in zip(pasts, chunks)) + 6
+    slots = prefill_slots(rng, nb, pasts, chunks)
+    slots[50] = -1
+    t = slots.size
+    k = rng.standard_normal((t, h, d), dtype=np.float32)
+    v = rng.standard_normal((t, h, d), dtype=np.float32)
+    kc = rng.standard_normal((nb, h, 16, d), dtype=np.float32)
+    vc = rng.standard_normal((nb, h, 16, d), dtype=np.float32)
+    if dtype == "bf16":
+        k, v, kc, vc = (oracle.f32_to_bf16(x) for x in (k, v, kc, vc))
+    gk, gv = to_dev(kc), to_dev(oracle.v_from_ref(vc))
+    pa.reshape_and_cache(to_dev(k), to_dev(v), gk, gv, to_dev(slots))
+    oracle.reshape_and_cache(k, v, kc, vc, slots)
+    assert np.array_equal(to_np(gk), kc)
+    assert np.array_equal(oracle.v_to_ref(to_np(gv)), vc)
+
+
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+def test_reshape_and_cache_fp8_prefill_runs(pa, oracle, src):
+    rng = np.random.default_rng(31)
+    h, d = 8, 128
+    pasts, chunks = PREFILL_CASES[0]
+    nb = sum((p + c + 15) // 16 for p, c in zip(pasts, chunks)) + 6
+    slots = prefill_slots(rng, nb, pasts, chunks)
+    t = slots.size
+    k = rng.standard_normal((t, h, d), dtype=np.float32) * 3
+    v = rng.standard_normal((t, h, d), dtype=np.float32)
+    k[3, 0, :3] = [np.nan, np.inf, -np.inf]
+    if src == "bf16":
+        kb, vb = oracle.f32_to_bf16(k), oracle.f32_to_bf16(v)
+        k, v = oracle.bf16_to_f32(kb), oracle.bf16_to_f32(vb)
+        dk, dv = to_dev(kb), to_dev(vb)
+    else:
+        dk, dv = to_dev(k), to_dev(v)
+    kc, vc = pa.ops.new_cache(nb, h, d, torch.uint8, DEV)
+    pa.reshape_and_cache_fp8(dk, dv, kc, vc, to_dev(slots))
+    want_k = np.zeros((nb, h, 16, d), np.uint8)
+    want_v = np.zeros_like(want_k)
+    kq, vq = oracle.fp8_encode(k), oracle.fp8_encode(v)
+    for i, s in enumerate(slots):
+        want_k[s // 16, :, s % 16, :] = kq[i]
+        want_v[s // 16, :, s % 16, :] = vq[i]
+    assert np.array_equal(to_np(kc), want_k)
+    assert np.array_equal(oracle.v_to_ref(to_np(vc)), want_v)
+
+
+def test_reshape_and_cache_config3_chunk_strided(pa, oracle):
+    # BASELINE config 3's write: 4 x 2048 tokens on pasts 0 / 512 / 1024 /
+    # 2048 (every run block-aligned), 8 kv heads x 128, K / V as strided
+    # views of a fused projection output
+    rng = np.random.default_rng(3)
+    h, d = 8, 128
+    pasts, chunks = [0, 512, 1024, 2048], [2048] * 4
+    nb = sum((p + c + 15) // 16 for p, c in zip(pasts, chunks)) + 16
+    slots = prefill_slots(rng, nb, pasts, chunks)
+    t = slots.size
+    kv = oracle.f32_to_bf16(rng.standard_normal((t, 3, h, d), dtype=np.float32))
+    g = to_dev(kv)
+    gk, gv = pa.ops.new_cache(nb, h, d, torch.bfloat16, DEV)
+    pa.reshape_and_cache(g[:, 1], g[:, 2], gk, gv, to_dev(slots))
+    kc = np.zeros((nb, h, 16, d), np.uint16)
+    vc = np.zeros_like(kc)
+    oracle.reshape_and_cache(kv[:, 1], kv[:, 2], kc, vc, slots)
+    assert np.array_equal(to_np(gk), kc)
+    assert np.array_equal(oracle.v_to_ref(to_np(gv)), vc)

@@ -271,8 +271,19 @@ extern "C" int32_t pa_batch_attention(pa_batch* b, pa_kv_cache* cache, int32_t l
                "pa_batch_attention: context %d exceeds the capacity %d", b->max_ctx,
                b->capacity);
     const int max_ctx = b->capacity > 0 ? b->capacity : b->max_ctx;
-    const size_t need = pa_decode_workspace_size(b->num_seqs, num_heads, d, max_ctx);
-    if ((rc = b->workspace.ensure(std::max<size_t>(need, 256)))) return rc;
+    const size_t need = std::max<size_t>(
+        pa_decode_workspace_size(b->num_seqs, num_heads, d, max_ctx), 256);
+    if (need > b->workspace.bytes) {
+      // growing frees and allocates, which a stream capture cannot record
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      PA_REQUIRE(hipStreamIsCapturing((hipStream_t)stream, &cap) == hipSuccess &&
+                     cap == hipStreamCaptureStatusNone,
+                 PA_ERR_WORKSPACE,
+                 "pa_batch_attention: the decode workspace must grow to %zu bytes while the "
+                 "stream is capturing; run one eager step of this shape before the capture",
+                 need);
+      if ((rc = b->workspace.ensure(need))) return rc;
+    }
     return pa::decode_strided(out, q, q_stride, kc, vc, (const int32_t*)b->tables.ptr,
                               b->max_blocks, (const int32_t*)b->ctx_lens.ptr, max_ctx,
                               b->num_seqs, num_heads, hkv, d, b->num_blocks, scale,

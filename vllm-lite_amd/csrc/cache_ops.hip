@@ -98,6 +98,134 @@ __global__ __launch_bounds__(256) void reshape_and_cache_fp8_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Block-coalesced scatter (the write path for D % 8 == 0 and 16-byte aligned
+// operands).  Workgroup g owns input tokens [16 g, 16 g + 16).  When the
+// token 16 g goes to offset o of its block and the 16 tokens from 16 g - o
+// go to offsets 0 .. 15 of that one block in order (a prefill chunk's run of
+// consecutive slots), the workgroup writes that whole block: each head's K
+// block [16, D] and its token-minor V block [D, 16] are contiguous, so every
+// store is a full 16-byte piece (the V block is transposed through LDS).
+// Tokens of the workgroup's range that no such full-block range covers
+// (its own, or the one workgroup g + 1 writes) go one by one as in
+// reshape_and_cache_kernel: a decode step's scattered tokens, the partial
+// blocks at the ends of a chunk.  Each token is written once; with
+// duplicate slots in slot_mapping the surviving value is unspecified.
+// TC = TS copies bits; TC = uint8_t encodes with the reference's FP8
+// encoder (fp8_encode).
+
+template <typename TS, typename TC>
+struct Unit8 {
+  TC v[8];
+};
+template <typename TS, typename TC>
+__device__ inline Unit8<TS, TC> load_unit(const TS* __restrict__ p) {
+  Unit8<TS, TC> u;
+  if constexpr (sizeof(TC) == 1) {
+    TS raw[8];
+    if constexpr (sizeof(TS) == 2) {
+      *reinterpret_cast<uint4*>(raw) = *reinterpret_cast<const uint4*>(p);
+    } else {
+      reinterpret_cast<uint4*>(raw)[0] = reinterpret_cast<const uint4*>(p)[0];
+      reinterpret_cast<uint4*>(raw)[1] = reinterpret_cast<const uint4*>(p)[1];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) u.v[e] = fp8_encode(Elem<TS>::load(raw + e));
+  } else {
+    static_assert(sizeof(TS) == sizeof(TC), "copy");
+#pragma unroll
+    for (int q = 0; q < (int)sizeof(TC) / 2; ++q)
+      reinterpret_cast<uint4*>(u.v)[q] = reinterpret_cast<const uint4*>(p)[q];
+  }
+  return u;
+}
+template <typename TS, typename TC>
+__device__ inline void store_unit(TC* __restrict__ p, const Unit8<TS, TC>& u) {
+  if constexpr (sizeof(TC) == 1) {
+    *reinterpret_cast<uint2*>(p) = *reinterpret_cast<const uint2*>(u.v);
+  } else {
+#pragma unroll
+    for (int q = 0; q < (int)sizeof(TC) / 2; ++q)
+      reinterpret_cast<uint4*>(p)[q] = reinterpret_cast<const uint4*>(u.v)[q];
+  }
+}
+
+template <typename TS, typename TC>
+__global__ __launch_bounds__(256) void cache_write_kernel(
+    const TS* __restrict__ key, const TS* __restrict__ value, TC* __restrict__ k_cache,
+    TC* __restrict__ v_cache, const int64_t* __restrict__ slots, int T, int H, int D,
+    int64_t num_slots, int64_t key_stride, int64_t value_stride) {
+  __shared__ int range_start[2];  // full-block range of this workgroup / of g + 1, or -1
+  __shared__ __align__(16) TC vt[kBlock * 512];
+  const int tid = threadIdx.x;
+  const int t0 = blockIdx.x * kBlock;
+  const int h = blockIdx.y;  // one kv head per workgroup
+  if (tid < 64) {
+    // lanes 0-15 test this workgroup's range, 16-31 the next one's
+    const int half = (tid >> 4) & 1, j = tid & 15;
+    const int tb = t0 + kBlock * half;
+    int start = -1;
+    bool ok = false;
+    if (tid < 32 && tb < T) {
+      const int64_t s0 = slots[tb];
+      if (s0 >= 0 && s0 < num_slots) {
+        start = tb - (int)(s0 % kBlock);
+        if (start >= 0 && start + kBlock <= T)
+          ok = slots[start + j] == s0 - s0 % kBlock + j;
+      }
+    }
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(ok);
+    if (tid == 0) range_start[0] = (bal & 0xFFFFull) == 0xFFFFull ? start : -1;
+    if (tid == 16) range_start[1] = ((bal >> 16) & 0xFFFFull) == 0xFFFFull ? start : -1;
+  }
+  __syncthreads();
+  const int r0 = range_start[0], r1 = range_start[1];
+  const int units = D / 8;  // 8-element units per head row
+  if (r0 >= 0) {
+    const int64_t blk = slots[r0] / kBlock;
+    // K: the head's block [16, D] in order; V: staged as [16 tokens][D] in
+    // LDS, then each thread writes one dim row of 16 tokens
+    TC* kd = k_cache + (blk * H + h) * kBlock * (int64_t)D;
+    for (int i = tid; i < kBlock * units; i += blockDim.x) {
+      const int u = i % units, j = i / units;
+      const int64_t src = (int64_t)(r0 + j) * key_stride + (int64_t)h * D + 8 * u;
+      store_unit<TS, TC>(kd + j * D + 8 * u, load_unit<TS, TC>(key + src));
+      const int64_t vsrc = (int64_t)(r0 + j) * value_stride + (int64_t)h * D + 8 * u;
+      store_unit<TS, TC>(vt + j * D + 8 * u, load_unit<TS, TC>(value + vsrc));
+    }
+    __syncthreads();
+    TC* vd = v_cache + (blk * H + h) * (int64_t)D * kBlock;
+    for (int d = tid; d < D; d += blockDim.x) {
+      TC row[kBlock];
+#pragma unroll
+      for (int j = 0; j < kBlock; ++j) row[j] = vt[j * D + d];
+#pragma unroll
+      for (int q = 0; q < (int)(kBlock * sizeof(TC)) / 16; ++q)
+        reinterpret_cast<uint4*>(vd + d * kBlock)[q] = reinterpret_cast<const uint4*>(row)[q];
+    }
+  }
+  // tokens of [t0, t0 + 16) outside both full-block ranges, one unit per
+  // thread: K unit stores, V element by element into the block rows
+  for (int i = tid; i < kBlock * units; i += blockDim.x) {
+    const int j = i / units, u = i % units;
+    const int t = t0 + j;
+    if (t >= T) break;
+    if ((r0 >= 0 && t >= r0 && t < r0 + kBlock) || (r1 >= 0 && t >= r1 && t < r1 + kBlock))
+      continue;
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= num_slots) continue;
+    const int64_t blk = slot / kBlock;
+    const int off = (int)(slot % kBlock);
+    store_unit<TS, TC>(k_cache + ((blk * H + h) * kBlock + off) * (int64_t)D + 8 * u,
+                       load_unit<TS, TC>(key + (int64_t)t * key_stride + (int64_t)h * D + 8 * u));
+    const Unit8<TS, TC> vv =
+        load_unit<TS, TC>(value + (int64_t)t * value_stride + (int64_t)h * D + 8 * u);
+    TC* vd = v_cache + ((blk * H + h) * (int64_t)D + 8 * u) * kBlock + off;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vd[e * kBlock] = vv.v[e];
+  }
+}
+
 // Dequantising gather from FP8 caches (f32 out).
 __global__ __launch_bounds__(256) void read_kv_fp8_kernel(const uint8_t* __restrict__ k_cache,
                                                           const uint8_t* __restrict__ v_cache,
@@ -246,6 +374,18 @@ extern "C" int32_t pa_reshape_and_cache(const void* key, const void* value, void
                    ((uintptr_t)value % 16) == 0 && ((uintptr_t)k_cache % 16) == 0;
   const dim3 grid(num_tokens), block(256);
   hipStream_t s = (hipStream_t)stream;
+  const dim3 wgrid((num_tokens + kBlock - 1) / kBlock, num_kv_heads);
+  if (vec && head_dim <= 512 && ((uintptr_t)v_cache % 16) == 0) {
+    if (dtype == PA_DTYPE_BF16)
+      cache_write_kernel<uint16_t, uint16_t><<<wgrid, block, 0, s>>>(
+          (const uint16_t*)key, (const uint16_t*)value, (uint16_t*)k_cache, (uint16_t*)v_cache,
+          slot_mapping, num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride);
+    else
+      cache_write_kernel<float, float><<<wgrid, block, 0, s>>>(
+          (const float*)key, (const float*)value, (float*)k_cache, (float*)v_cache, slot_mapping,
+          num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride);
+    return check_launch("pa_reshape_and_cache");
+  }
   if (dtype == PA_DTYPE_BF16) {
     auto* kc = (uint16_t*)k_cache;
     auto* vc = (uint16_t*)v_cache;
@@ -296,6 +436,21 @@ extern "C" int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, 
   const bool vec = head_dim % 8 == 0 && ((uintptr_t)k_cache % 8) == 0;
   const dim3 grid(num_tokens), block(256);
   hipStream_t s = (hipStream_t)stream;
+  const size_t es = dtype_size(src_dtype);
+  if (vec && head_dim <= 512 && ((uintptr_t)v_cache % 16) == 0 && ((uintptr_t)key % 16) == 0 &&
+      ((uintptr_t)value % 16) == 0 && (key_stride * es) % 16 == 0 &&
+      (value_stride * es) % 16 == 0) {
+    const dim3 wgrid((num_tokens + kBlock - 1) / kBlock, num_kv_heads);
+    if (src_dtype == PA_DTYPE_BF16)
+      cache_write_kernel<uint16_t, uint8_t><<<wgrid, block, 0, s>>>(
+          (const uint16_t*)key, (const uint16_t*)value, k_cache, v_cache, slot_mapping,
+          num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride);
+    else
+      cache_write_kernel<float, uint8_t><<<wgrid, block, 0, s>>>(
+          (const float*)key, (const float*)value, k_cache, v_cache, slot_mapping, num_tokens,
+          num_kv_heads, head_dim, num_slots, key_stride, value_stride);
+    return check_launch("pa_reshape_and_cache_fp8");
+  }
 #define PA_LAUNCH_Q(T, V)                                                                    \
   reshape_and_cache_fp8_kernel<T, V><<<grid, block, 0, s>>>(                                 \
       (const T*)key, (const T*)value, k_cache, v_cache, slot_mapping, num_kv_heads, head_dim, \
