@@ -231,3 +231,29 @@ def test_ids_outside_pool_are_absent_keys(pa, oracle, dtype, hq, hkv, d):
     assert np.isfinite(got).all()
     tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
     assert_close(got, ref, *tol, f"decode with out-of-pool ids {dtype} {hq}/{hkv}x{d}")
+
+
+@pytest.mark.parametrize("hq,hkv,d,seed", [(32, 8, 128, 0), (8, 8, 64, 1), (16, 2, 256, 2),
+                                           (28, 4, 128, 3)])
+def test_balanced_split_ragged(pa, oracle, hq, hkv, d, seed):
+    # Long, ragged contexts (the balanced split-K launch: the work cut
+    # evenly over the wavefronts, a wavefront's range crossing sequence and
+    # kv-head boundaries): empty contexts, a single token, block edges and
+    # long sequences side by side, more than 64 sequences.
+    rng = np.random.default_rng(40 + seed)
+    b = 70 if d <= 128 else 9
+    ctx = rng.integers(1, 12000, b)
+    ctx[::7] = rng.integers(9000, 16000, len(ctx[::7]))
+    ctx[3], ctx[5], ctx[8] = 0, 1, 32
+    case = make_decode_case(rng, b, hq, hkv, d, np.maximum(ctx, 1), dtype="bf16")
+    case["ctx"] = ctx.astype(np.int32)
+    out = pa.decode(to_dev(case["q"]), to_dev(case["k_cache"]),
+                    to_dev(oracle.v_from_ref(case["v_cache_ref"])), to_dev(case["block_tables"]),
+                    to_dev(case["ctx"]), int(ctx.max()))
+    got = oracle.bf16_to_f32(to_np(out))
+    live = ctx > 0
+    ref = np.zeros_like(got)
+    sub = {k: (v[live] if k in ("q", "block_tables", "ctx") else v) for k, v in case.items()}
+    ref[live] = ref_f32(oracle, sub)
+    assert np.all(got[~live] == 0)
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, f"balanced {hq}/{hkv}x{d}")

@@ -818,6 +818,262 @@ __global__ __launch_bounds__(1024) void decode_f32_group_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Balanced split-K ("stream-K") decode for long, ragged contexts.
+//
+// A partitioned launch gives every (sequence, kv head) the same number of
+// fixed-length partitions; with ragged contexts the workgroups of the last
+// dispatch round run with the GPU mostly idle (measured on BASELINE config
+// 4: about 2000 wavefronts in flight for 110 us, then a 55 us tail in which
+// they drain).  Here the work is cut evenly instead: a unit is one 32-token
+// step of one (sequence, kv head) segment, the segments are laid end to end
+// (sequence-major, kv head minor), and wavefront w of N takes units
+// [floor(w U / N), floor((w + 1) U / N)) of the U in all, crossing segment
+// boundaries as it goes.  For every segment piece it writes one partial
+// result (m, l, o per query head) into slot w - first(segment) of the
+// segment's rows; decode_reduce_kernel merges a row's slots.  Both kernels
+// derive U, N and a segment's first and last wavefront from context_lens
+// the same way, so no offsets travel between them.
+// Measured on config 4 (B 16, contexts 8k-32k, flushed caches): 162 us
+// against 177 us for 512-token partitions; with every block private, 6.2
+// TB/s.  One wavefront per SIMD: the two-deep step pipeline takes most of
+// the register file (2048 or more wavefronts of the unpipelined loop
+// measured 2-20% slower).
+constexpr int kBalanceMinUnits = 8;   // units per wavefront at least (256 tokens)
+constexpr int kBalanceWaves = 1024;   // one wavefront per SIMD of the 256 CUs
+
+// A wavefront-uniform 64-bit value held in vector registers, moved to
+// scalar ones (every lane holds the same value).
+__device__ inline int64_t uniform64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ inline int seq_units(const int32_t* __restrict__ context_lens, int s, int mbs) {
+  const int ctx = min(context_lens[s], mbs * kBlock);
+  return ctx > 0 ? (ctx + 2 * kBlock - 1) / (2 * kBlock) : 0;
+}
+// Units of the sequences before `upto` (times the kv heads), summed over a
+// wavefront; every lane returns the same value.
+__device__ inline int64_t units_before(const int32_t* __restrict__ context_lens, int upto,
+                                       int mbs, int Hkv) {
+  const int lane = threadIdx.x & 63;
+  int64_t acc = 0;
+  for (int s = lane; s < upto; s += 64) acc += seq_units(context_lens, s, mbs);
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  return uniform64(acc * Hkv);
+}
+__device__ inline int balance_waves(int64_t total, int max_waves) {
+  return (int)max((int64_t)1, min((int64_t)max_waves, total / kBalanceMinUnits));
+}
+// The wavefront whose range holds unit g: the largest w with
+// floor(w U / N) <= g.
+__device__ inline int wave_of(int64_t g, int64_t total, int nw) {
+  return (int)(((g + 1) * nw - 1) / total);
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void decode_balanced_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ context_lens, int B, int Hq, int Hkv, int G, int num_blocks,
+    float scale_log2, int slots, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    int64_t q_row) {
+  constexpr int KS = D / 32;  // QK reduction steps
+  constexpr int DT = D / 16;  // PV output tiles
+  const int lane = threadIdx.x;
+  const int c = lane & 15, j = lane >> 4;
+  const int64_t total = units_before(context_lens, B, mbs, Hkv);
+  const int nw = balance_waves(total, gridDim.x);
+  const int w = blockIdx.x;
+  if (total == 0 || w >= nw) return;
+  const int64_t lo = (int64_t)w * total / nw, hi = (int64_t)(w + 1) * total / nw;
+  if (lo >= hi) return;
+
+  // The sequence holding unit lo: scan the per-sequence unit counts 64 at a
+  // time (inclusive prefix sums across the wavefront).
+  int s = 0;
+  int64_t cs = 0;  // first unit of sequence s
+  for (int base = 0;; base += 64) {
+    const int n = base + lane < B ? seq_units(context_lens, base + lane, mbs) : 0;
+    int64_t incl = (int64_t)n * Hkv;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t t = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += t;
+    }
+    const uint64_t past = __builtin_amdgcn_ballot_w64(cs + incl > lo);
+    if (past) {
+      const int first = __builtin_ctzll(past);
+      s = base + first;
+      cs = uniform64(cs + __shfl(incl, first, 64) - (int64_t)__shfl(n, first, 64) * Hkv);
+      break;
+    }
+    cs = uniform64(cs + __shfl(incl, 63, 64));
+  }
+
+  const int64_t head_stride = (int64_t)kBlock * D;
+  constexpr int SLICE = kBlock * D * 2;
+  const int koff = (c * D + 8 * j) * 2, voff = (c * kBlock + 4 * j) * 2;
+  struct Step {
+    bf16x8 ka[KS], kb[KS];
+    uint64_t va[DT], vb[DT];
+    int lim0, lim1;
+  };
+  for (int64_t g = lo; g < hi;) {
+    const int n = seq_units(context_lens, s, mbs);
+    if (n == 0 || g >= cs + (int64_t)n * Hkv) {  // next sequence
+      cs += (int64_t)n * Hkv;
+      ++s;
+      continue;
+    }
+    const int kvh = (int)((g - cs) / n);
+    const int u0 = (int)((g - cs) % n);
+    const int64_t seg = cs + (int64_t)kvh * n;  // the segment's first unit
+    const int u1 = (int)min((int64_t)n, u0 + (hi - g));
+    const int ctx = min(context_lens[s], mbs * kBlock);
+    const int tok0 = u0 * 2 * kBlock, tok_end = min(ctx, u1 * 2 * kBlock);
+    const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;
+    const int head = kvh * G + c;
+    bf16x8 qv[KS];
+#pragma unroll
+    for (int st = 0; st < KS; ++st)
+      qv[st] = c < G ? *reinterpret_cast<const bf16x8*>(q + (int64_t)s * q_row + (int64_t)head * D +
+                                                        32 * st + 8 * j)
+                     : bf16x8{};
+    f32x4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = kNegBig, lsum = 0.f;
+    const int32_t* btab = block_tables + (int64_t)s * mbs + tok0 / kBlock;
+    // Steps software-pipelined two deep for D <= 128, as decode_fp8_kernel:
+    // the loads are unconditional non-temporal loads and the block ids come
+    // through explicit scalar loads, so the compiler's wait counts stay
+    // exact.
+    auto table_id = [&](int idx) -> int32_t {
+      int32_t v;
+      asm volatile("s_load_dword %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+                   : "=s"(v)
+                   : "s"(btab), "s"(idx * 4));
+      return v;
+    };
+    auto load_step = [&](int ib, Step& st) {
+      int32_t b0 = table_id(ib);
+      const bool has1 = ib + 1 < nblk;
+      int32_t b1 = table_id(has1 ? ib + 1 : ib);
+      const int rem = tok_end - (tok0 + ib * kBlock);
+      st.lim0 = rem < kBlock ? rem : kBlock;
+      st.lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
+      if (b0 < 0 || b0 >= num_blocks) { b0 = 0; st.lim0 = 0; }
+      if (b1 < 0 || b1 >= num_blocks) { b1 = 0; st.lim1 = 0; }
+      const auto rk0 = slice_rsrc(kc + ((int64_t)b0 * Hkv + kvh) * head_stride, SLICE);
+      const auto rk1 = slice_rsrc(kc + ((int64_t)b1 * Hkv + kvh) * head_stride, SLICE);
+      const auto rv0 = slice_rsrc(vc + ((int64_t)b0 * Hkv + kvh) * head_stride, SLICE);
+      const auto rv1 = slice_rsrc(vc + ((int64_t)b1 * Hkv + kvh) * head_stride, SLICE);
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        st.ka[t] = __builtin_bit_cast(bf16x8, bload16<kPolicyNT>(rk0, koff + 64 * t));
+        st.kb[t] = __builtin_bit_cast(bf16x8, bload16<kPolicyNT>(rk1, koff + 64 * t));
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        st.va[dt] = bload8<kPolicyNT>(rv0, voff + dt * 16 * kBlock * 2);
+        st.vb[dt] = bload8<kPolicyNT>(rv1, voff + dt * 16 * kBlock * 2);
+      }
+    };
+    auto compute = [&](Step& st) {
+      f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.ka[t], qv[t], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.kb[t], qv[t], s1, 0, 0, 0);
+      }
+      float x[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = s0[r] * scale_log2;
+        x[4 + r] = s1[r] * scale_log2;
+      }
+      if (st.lim0 < kBlock || st.lim1 < kBlock) {  // wave-uniform
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (4 * j + r >= st.lim0) x[r] = -INFINITY;
+          if (4 * j + r >= st.lim1) x[4 + r] = -INFINITY;
+        }
+        // stale cache contents beyond the context may hold any bits
+        const int n0 = min(max(st.lim0 - 4 * j, 0), 4), n1 = min(max(st.lim1 - 4 * j, 0), 4);
+        const uint64_t mk0 = n0 >= 4 ? ~0ull : ((1ull << (16 * n0)) - 1);
+        const uint64_t mk1 = n1 >= 4 ? ~0ull : ((1ull << (16 * n1)) - 1);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          st.va[dt] &= mk0;
+          st.vb[dt] &= mk1;
+        }
+      }
+      float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                       fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+      if (__builtin_amdgcn_ballot_w64(bm > m + 8.0f)) {  // lazy rescale
+        bm = fmaxf(bm, shfl_xor_f(bm, 16));
+        bm = fmaxf(bm, shfl_xor_f(bm, 32));
+        const float mn = fmaxf(m, bm);
+        const float a = fast_exp2(m - mn);
+        m = mn;
+        lsum *= a;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= a;
+      }
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = fast_exp2(x[i] - m);
+        lsum += p[i];
+      }
+      bf16x8 pb;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pb[i] = (__bf16)p[i];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint64_t pair[2] = {st.va[dt], st.vb[dt]};
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(pair);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
+      }
+    };
+#pragma unroll
+    for (int st = 0; st < KS; ++st) asm volatile("" ::"v"(qv[st]));
+    if constexpr (D <= 128) {
+      Step sa, sb;
+      if (nblk > 0) load_step(0, sa);
+      for (int ib = 0; ib < nblk; ib += 4) {
+        if (ib + 2 < nblk) load_step(ib + 2, sb);
+        compute(sa);
+        if (ib + 2 >= nblk) break;
+        if (ib + 4 < nblk) load_step(ib + 4, sa);
+        compute(sb);
+      }
+    } else {
+      // D = 256: two steps do not fit the register file; one at a time
+      for (int ib = 0; ib < nblk; ib += 2) {
+        Step st;
+        load_step(ib, st);
+        compute(st);
+      }
+    }
+    lsum += shfl_xor_f(lsum, 16);
+    lsum += shfl_xor_f(lsum, 32);
+    if (c < G) {
+      const int k = w - wave_of(seg, total, nw);
+      const int64_t row = ((int64_t)s * Hq + head) * slots + k;
+      float* orow = ws_o + row * D + 4 * j;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(orow + 16 * dt) = o[dt];
+      if (j == 0) {
+        ws_ml[2 * row] = m;
+        ws_ml[2 * row + 1] = lsum;
+      }
+    }
+    g += u1 - u0;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Partition merge: one workgroup of 256 threads per (sequence, query head).
 // The partitions' (m, l) are reduced over the workgroup to M and L; thread
 // t then accumulates output dims of lane t % 64 over the partitions
@@ -827,7 +1083,10 @@ template <typename T>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(
     T* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ context_lens, int Hq, int D, int num_parts, int mbs,
-    int part_len) {
+    int part_len, int balance_nw, int B, int Hkv) {
+  // balance_nw > 0: partial results of decode_balanced_kernel launched with
+  // balance_nw wavefronts (num_parts = slots per row); else partitions of
+  // part_len tokens.
   __shared__ float wsh[1024];
   __shared__ float red[4][512];
   __shared__ float ml[2][4];
@@ -835,7 +1094,20 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
   const int row = blockIdx.x;  // seq * Hq + head
   const int seq = row / Hq;
   const int ctx = min(context_lens[seq], mbs * kBlock);
-  const int np = min(min(num_parts, (ctx + part_len - 1) / part_len), 1024);
+  int np;
+  if (balance_nw > 0) {
+    // the slots of this row's segment: its first to its last wavefront
+    const int64_t total = units_before(context_lens, B, mbs, Hkv);
+    const int n = seq_units(context_lens, seq, mbs);
+    np = 0;
+    if (total > 0 && n > 0) {
+      const int nw = balance_waves(total, balance_nw);
+      const int64_t seg = units_before(context_lens, seq, mbs, Hkv) + (int64_t)((row % Hq) / (Hq / Hkv)) * n;
+      np = min(wave_of(seg + n - 1, total, nw) - wave_of(seg, total, nw) + 1, num_parts);
+    }
+  } else {
+    np = min(min(num_parts, (ctx + part_len - 1) / part_len), 1024);
+  }
   const int64_t row0 = (int64_t)row * num_parts;
   // Wavefront w sums the partitions w, w + 4, ... of dims lane and lane + 64
   // (head_dim <= 128: the common case, in chunks of kRU partitions whose
@@ -932,10 +1204,12 @@ using namespace pa;
 
 extern "C" size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
                                            int32_t max_context_len) {
-  // Sized for the shortest partition any launch uses.
+  // Sized for the shortest partition any launch uses, plus one: a balanced
+  // launch writes up to ceil(max_context_len / 256) + 1 partial results per
+  // row.
   const int np = num_partitions(max_context_len, kPart);
   if (np <= 1 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  return (size_t)num_seqs * num_heads * np * (head_dim + 2) * sizeof(float);
+  return (size_t)num_seqs * num_heads * (np + 1) * (head_dim + 2) * sizeof(float);
 }
 
 namespace {
@@ -943,7 +1217,8 @@ namespace {
 // partition length and count, and how many partitions one workgroup merges.
 struct DecodePlan {
   bool mfma, f32_group;
-  int part_len, np, merge_waves;
+  bool balanced;  // bf16 launches that would need the reduce: decode_balanced_kernel
+  int part_len, np, merge_waves;  // np: partitions, or partial-result slots per row
   size_t ws_bytes;  // workspace the launch needs (0: none)
 };
 DecodePlan decode_plan(int32_t dtype, bool quantized, int32_t num_seqs, int32_t num_heads,
@@ -969,6 +1244,14 @@ DecodePlan decode_plan(int32_t dtype, bool quantized, int32_t num_seqs, int32_t 
                   : p.np <= 4           ? 4
                   : (p.np <= 8 && head_dim <= 128) ? 8
                                                    : 1;
+  // Partitioned launches that need the reduce (long, ragged contexts) cut
+  // the work evenly over the GPU instead (bf16 caches): a segment of n units
+  // meets at most ceil(n / kBalanceMinUnits) + 1 wavefronts.
+  p.balanced = p.mfma && !fp8 && p.np > 1 && p.merge_waves == 1;
+  if (p.balanced) {
+    const int max_units = (max_context_len + 2 * kBlock - 1) / (2 * kBlock);
+    p.np = (max_units + kBalanceMinUnits - 1) / kBalanceMinUnits + 1;
+  }
   p.ws_bytes = p.np > 1 && p.merge_waves == 1
                    ? (size_t)num_seqs * num_heads * p.np * (head_dim + 2) * sizeof(float)
                    : 0;
@@ -1018,7 +1301,23 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
              "pa_decode: q row stride %lld below num_heads * head_dim", (long long)q_row);
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  if (mfma) {
+  if (plan.balanced) {
+    if (head_dim == 64)
+      decode_balanced_kernel<64><<<kBalanceWaves, 64, 0, s>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,
+          max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,
+          scale_log2, np, ws_o, ws_ml, q_row);
+    else if (head_dim == 128)
+      decode_balanced_kernel<128><<<kBalanceWaves, 64, 0, s>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,
+          max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,
+          scale_log2, np, ws_o, ws_ml, q_row);
+    else
+      decode_balanced_kernel<256><<<kBalanceWaves, 64, 0, s>>>(
+          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,
+          max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,
+          scale_log2, np, ws_o, ws_ml, q_row);
+  } else if (mfma) {
     const dim3 grid(merge_waves > 1 ? 1 : np, num_kv_heads, num_seqs);
     auto* o = (uint16_t*)out;
     auto* qq = (const uint16_t*)q;
@@ -1087,14 +1386,17 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   int32_t rc = check_launch("pa_decode");
   if (rc != PA_OK || np == 1 || merge_waves > 1) return rc;
   const dim3 rgrid(num_seqs * num_heads);
+  const int bal = plan.balanced ? kBalanceWaves : 0;
   if (dtype == PA_DTYPE_BF16 || fp8)
     decode_reduce_kernel<uint16_t><<<rgrid, 256, 0, s>>>((uint16_t*)out, ws_o, ws_ml,
                                                          context_lens, num_heads, head_dim, np,
-                                                         max_blocks_per_seq, part_len);
+                                                         max_blocks_per_seq, part_len, bal,
+                                                         num_seqs, num_kv_heads);
   else
     decode_reduce_kernel<float><<<rgrid, 256, 0, s>>>((float*)out, ws_o, ws_ml, context_lens,
                                                       num_heads, head_dim, np,
-                                                      max_blocks_per_seq, part_len);
+                                                      max_blocks_per_seq, part_len, bal,
+                                                      num_seqs, num_kv_heads);
   return check_launch("pa_decode reduce");
 }
 }  // namespace
