@@ -46,12 +46,12 @@ def test_version_and_empty_error(lib):
 
 
 def test_workspace_size(lib):
-    # one partition (<= 256 tokens) needs none; otherwise B*Hq*(P+1)*(D+2) f32
-    # with P = ceil(ctx / 256) (a balanced launch writes up to P + 1 partial
-    # results per row)
+    # one partition (<= 256 tokens) needs none; otherwise B*Hq*(P+2)*(D+2) f32
+    # with P = ceil(ctx / 256) (a balanced launch writes up to P + 2 partial
+    # results per row) and one int per sequence
     assert lib.pa_decode_workspace_size(64, 32, 128, 256) == 0
-    assert lib.pa_decode_workspace_size(64, 32, 128, 4096) == 64 * 32 * 17 * 130 * 4
-    assert lib.pa_decode_workspace_size(2, 4, 64, 257) == 2 * 4 * 3 * 66 * 4
+    assert lib.pa_decode_workspace_size(64, 32, 128, 4096) == 64 * 32 * 18 * 130 * 4 + 64 * 4
+    assert lib.pa_decode_workspace_size(2, 4, 64, 257) == 2 * 4 * 4 * 66 * 4 + 2 * 4
 
 
 def test_argument_errors_without_gpu(lib):

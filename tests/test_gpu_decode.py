@@ -257,3 +257,34 @@ def test_balanced_split_ragged(pa, oracle, hq, hkv, d, seed):
     ref[live] = ref_f32(oracle, sub)
     assert np.all(got[~live] == 0)
     assert_close(got, ref, BF16_ATOL, BF16_RTOL, f"balanced {hq}/{hkv}x{d}")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (8, 8, 64), (16, 8, 256),
+                                      (16, 4, 128)])
+def test_balanced_shared_prefix_groups(pa, oracle, hq, hkv, d):
+    # Long contexts whose tables share prefixes in some sequence groups (the
+    # balanced launch attends a group's common prefix once for all its
+    # members): a 50-block prefix (odd: it ends inside a 2-block unit) shared
+    # by most sequences, a member that diverges after 7 blocks, a member
+    # shorter than the prefix, a group with nothing shared, and a
+    # sequence count that leaves a partial last group.
+    rng = np.random.default_rng(hq + hkv + d)
+    b = 13
+    ctx = rng.integers(3000, 9000, b).astype(np.int32)
+    ctx[4] = 500          # shorter than the shared prefix
+    case = make_decode_case(rng, b, hq, hkv, d, ctx, dtype="bf16", shared_prefix_blocks=50)
+    bt = case["block_tables"]
+    nb = case["num_blocks"]
+    extra = rng.permutation(np.arange(nb, nb + 200)).astype(np.int32)
+    bt[2, 7:50] = extra[:43]              # diverges after 7 blocks
+    bt[9:12, :50] = extra[43:193].reshape(3, 50)  # a group without a common prefix
+    grow = 200
+    for key in ("k_cache", "v_cache_ref"):
+        pad = rng.standard_normal((grow,) + case[key].shape[1:], dtype=np.float32)
+        case[key] = np.concatenate([case[key], oracle.f32_to_bf16(pad)])
+    out = pa.decode(to_dev(case["q"]), to_dev(case["k_cache"]),
+                    to_dev(oracle.v_from_ref(case["v_cache_ref"])), to_dev(bt),
+                    to_dev(ctx), int(ctx.max()))
+    got = oracle.bf16_to_f32(to_np(out))
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL,
+                 f"balanced shared prefix {hq}/{hkv}x{d}")

@@ -852,16 +852,38 @@ __device__ inline int seq_units(const int32_t* __restrict__ context_lens, int s,
   const int ctx = min(context_lens[s], mbs * kBlock);
   return ctx > 0 ? (ctx + 2 * kBlock - 1) / (2 * kBlock) : 0;
 }
-// Units of the sequences before `upto` (times the kv heads), summed over a
-// wavefront; every lane returns the same value.
-__device__ inline int64_t units_before(const int32_t* __restrict__ context_lens, int upto,
-                                       int mbs, int Hkv) {
-  const int lane = threadIdx.x & 63;
-  int64_t acc = 0;
-  for (int s = lane; s < upto; s += 64) acc += seq_units(context_lens, s, mbs);
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-  return uniform64(acc * Hkv);
-}
+
+// Work layout of a balanced launch.  Sequences are taken in groups of SP
+// consecutive ones (SP = 16 / G, the sequences whose query heads fill the
+// 16 MFMA columns together; SP = 1 without sharing).  lcp[g] (or 0) is the
+// number of leading units every member of group g holds in full and whose
+// blocks all members' tables share (a common prefix).  Group g's units:
+//   the shared segments (kv head 0 .. Hkv-1, lcp[g] units each, every
+//   member attended at once), then for each member the private segments
+//   (kv head 0 .. Hkv-1, its units past the prefix).
+struct BalanceLayout {
+  const int32_t* __restrict__ ctx;
+  const int32_t* __restrict__ lcp;  // null: no shared prefixes
+  int B, mbs, Hkv, SP;
+  __device__ int units(int s) const { return seq_units(ctx, s, mbs); }
+  __device__ int shared(int g) const { return lcp ? lcp[g] : 0; }
+  __device__ int groups() const { return (B + SP - 1) / SP; }
+  __device__ int64_t group_units(int g) const {
+    const int L = shared(g);
+    int64_t n = L;
+    for (int m = g * SP; m < min(B, g * SP + SP); ++m) n += units(m) - L;
+    return n * Hkv;
+  }
+  // units of the groups before `upto`, summed over a wavefront (every lane
+  // returns the same value)
+  __device__ int64_t before(int upto) const {
+    const int lane = threadIdx.x & 63;
+    int64_t acc = 0;
+    for (int g = lane; g < upto; g += 64) acc += group_units(g);
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    return uniform64(acc);
+  }
+};
 __device__ inline int balance_waves(int64_t total, int max_waves) {
   return (int)max((int64_t)1, min((int64_t)max_waves, total / kBalanceMinUnits));
 }
@@ -870,6 +892,51 @@ __device__ inline int balance_waves(int64_t total, int max_waves) {
 __device__ inline int wave_of(int64_t g, int64_t total, int nw) {
   return (int)(((g + 1) * nw - 1) / total);
 }
+// Slots of a segment [start, start + len): its first to its last wavefront.
+__device__ inline int seg_slots(int64_t start, int len, int64_t total, int nw) {
+  return len > 0 ? wave_of(start + len - 1, total, nw) - wave_of(start, total, nw) + 1 : 0;
+}
+
+// Common prefix of each group's tables, in full units (the shared part of
+// BalanceLayout): one wavefront per group.
+__global__ __launch_bounds__(64) void decode_lcp_kernel(
+    const int32_t* __restrict__ block_tables, int mbs, const int32_t* __restrict__ context_lens,
+    int B, int SP, int32_t* __restrict__ lcp) {
+  const int g = blockIdx.x, lane = threadIdx.x;
+  const int g0 = g * SP, gn = min(SP, B - g0);
+  int L = INT32_MAX;
+  for (int m = 0; m < gn; ++m) L = min(L, min(context_lens[g0 + m], mbs * kBlock) / (2 * kBlock));
+  if (gn < 2) L = 0;
+  // the first block, below 2 L, where a member's table differs from the first's
+  for (int b0 = 0; b0 < 2 * L; b0 += 64) {
+    const int b = b0 + lane;
+    bool diff = false;
+    if (b < 2 * L) {
+      const int32_t id = block_tables[(int64_t)g0 * mbs + b];
+      for (int m = 1; m < gn; ++m) diff |= block_tables[(int64_t)(g0 + m) * mbs + b] != id;
+    }
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(diff);
+    if (bal) {
+      L = min(L, (b0 + (int)__builtin_ctzll(bal)) / 2);
+      break;
+    }
+  }
+  if (lane == 0) lcp[g] = L;
+}
+
+// One segment piece: kv head kvh, units [u0, u1) of the segment.  Shared
+// pieces attend group members [g0, g0 + gn) at once (MFMA column c: member
+// c / G, head c % G; every member holds the units in full, the blocks from
+// the first member's table); private pieces one sequence (column c: head
+// c), its units past the shared prefix.
+struct Piece {
+  bool shared;
+  int seq;      // private: the sequence; shared: the group's first member
+  int gn;       // shared: members
+  int kvh, u0, u1, unit_base;  // unit_base: the segment's first unit within the sequence
+  int64_t start;  // the segment's first unit in the layout
+  int slot_base;  // private: the row's shared slots
+};
 
 template <int D>
 __global__ __launch_bounds__(64) void decode_balanced_kernel(
@@ -877,37 +944,39 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int B, int Hq, int Hkv, int G, int num_blocks,
     float scale_log2, int slots, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int64_t q_row) {
+    int64_t q_row, const int32_t* __restrict__ lcp, int SP) {
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
   const int lane = threadIdx.x;
   const int c = lane & 15, j = lane >> 4;
-  const int64_t total = units_before(context_lens, B, mbs, Hkv);
+  const BalanceLayout lay{context_lens, lcp, B, mbs, Hkv, SP};
+  const int64_t total = lay.before(lay.groups());
   const int nw = balance_waves(total, gridDim.x);
   const int w = blockIdx.x;
   if (total == 0 || w >= nw) return;
   const int64_t lo = (int64_t)w * total / nw, hi = (int64_t)(w + 1) * total / nw;
   if (lo >= hi) return;
 
-  // The sequence holding unit lo: scan the per-sequence unit counts 64 at a
-  // time (inclusive prefix sums across the wavefront).
-  int s = 0;
-  int64_t cs = 0;  // first unit of sequence s
-  for (int base = 0;; base += 64) {
-    const int n = base + lane < B ? seq_units(context_lens, base + lane, mbs) : 0;
-    int64_t incl = (int64_t)n * Hkv;
+  // The group holding unit lo: scan the per-group unit counts 64 at a time
+  // (inclusive prefix sums across the wavefront).
+  const int ng = lay.groups();
+  int g = 0;
+  int64_t cg = 0;  // first unit of group g
+  for (int base = 0; base < ng; base += 64) {
+    const int64_t n = base + lane < ng ? lay.group_units(base + lane) : 0;
+    int64_t incl = n;
     for (int o = 1; o < 64; o <<= 1) {
       const int64_t t = __shfl_up(incl, o, 64);
       if (lane >= o) incl += t;
     }
-    const uint64_t past = __builtin_amdgcn_ballot_w64(cs + incl > lo);
+    const uint64_t past = __builtin_amdgcn_ballot_w64(cg + incl > lo);
     if (past) {
       const int first = __builtin_ctzll(past);
-      s = base + first;
-      cs = uniform64(cs + __shfl(incl, first, 64) - (int64_t)__shfl(n, first, 64) * Hkv);
+      g = base + first;
+      cg = uniform64(cg + __shfl(incl, first, 64) - __shfl(n, first, 64));
       break;
     }
-    cs = uniform64(cs + __shfl(incl, 63, 64));
+    cg = uniform64(cg + __shfl(incl, 63, 64));
   }
 
   const int64_t head_stride = (int64_t)kBlock * D;
@@ -918,32 +987,70 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
     uint64_t va[DT], vb[DT];
     int lim0, lim1;
   };
-  for (int64_t g = lo; g < hi;) {
-    const int n = seq_units(context_lens, s, mbs);
-    if (n == 0 || g >= cs + (int64_t)n * Hkv) {  // next sequence
-      cs += (int64_t)n * Hkv;
-      ++s;
+  for (int64_t gpos = lo; gpos < hi && g < ng;) {
+    const int64_t gu = lay.group_units(g);
+    if (gpos >= cg + gu) {  // next group
+      cg += gu;
+      ++g;
       continue;
     }
-    const int kvh = (int)((g - cs) / n);
-    const int u0 = (int)((g - cs) % n);
-    const int64_t seg = cs + (int64_t)kvh * n;  // the segment's first unit
-    const int u1 = (int)min((int64_t)n, u0 + (hi - g));
-    const int ctx = min(context_lens[s], mbs * kBlock);
-    const int tok0 = u0 * 2 * kBlock, tok_end = min(ctx, u1 * 2 * kBlock);
+    // the segment holding gpos
+    const int L = lay.shared(g), g0 = g * SP, gn = min(SP, B - g0);
+    int64_t r = gpos - cg;
+    Piece pc{};
+    if (r < (int64_t)Hkv * L) {
+      pc.shared = true;
+      pc.seq = g0;
+      pc.gn = gn;
+      pc.kvh = (int)(r / L);
+      pc.u0 = (int)(r % L);
+      pc.u1 = L;
+      pc.unit_base = 0;
+      pc.start = cg + (int64_t)pc.kvh * L;
+    } else {
+      r -= (int64_t)Hkv * L;
+      int64_t off = (int64_t)Hkv * L;
+      pc.seq = -1;
+      for (int m = g0; m < g0 + gn; ++m) {  // gpos lies in this group: a member holds it
+        const int len = lay.units(m) - L;
+        if (len > 0 && r < (int64_t)Hkv * len) {
+          pc.seq = m;
+          pc.kvh = (int)(r / len);
+          pc.u0 = (int)(r % len);
+          pc.u1 = len;
+          pc.unit_base = L;
+          pc.start = cg + off + (int64_t)pc.kvh * len;
+          // the row's shared slots come first
+          pc.slot_base = seg_slots(cg + (int64_t)pc.kvh * L, L, total, nw);
+          break;
+        }
+        r -= (int64_t)Hkv * max(len, 0);
+        off += (int64_t)Hkv * max(len, 0);
+      }
+      if (pc.seq < 0) break;  // (not reached: the layout sums to gu)
+    }
+    pc.u1 = (int)min((int64_t)pc.u1, pc.u0 + (hi - gpos));
+    const int kvh = pc.kvh;
+    const int ctx = min(context_lens[pc.seq], mbs * kBlock);
+    const int tok0 = (pc.unit_base + pc.u0) * 2 * kBlock;
+    const int tok_end = pc.shared ? (pc.unit_base + pc.u1) * 2 * kBlock
+                                  : min(ctx, (pc.unit_base + pc.u1) * 2 * kBlock);
     const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;
-    const int head = kvh * G + c;
+    // this lane's MFMA column: sequence and query head
+    const int col_seq = pc.shared ? pc.seq + c / G : pc.seq;
+    const int head = kvh * G + (pc.shared ? c % G : c);
+    const bool col_ok = pc.shared ? c < pc.gn * G : c < G;
     bf16x8 qv[KS];
 #pragma unroll
     for (int st = 0; st < KS; ++st)
-      qv[st] = c < G ? *reinterpret_cast<const bf16x8*>(q + (int64_t)s * q_row + (int64_t)head * D +
-                                                        32 * st + 8 * j)
-                     : bf16x8{};
+      qv[st] = col_ok ? *reinterpret_cast<const bf16x8*>(q + (int64_t)col_seq * q_row +
+                                                         (int64_t)head * D + 32 * st + 8 * j)
+                      : bf16x8{};
     f32x4 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = kNegBig, lsum = 0.f;
-    const int32_t* btab = block_tables + (int64_t)s * mbs + tok0 / kBlock;
+    const int32_t* btab = block_tables + (int64_t)pc.seq * mbs + tok0 / kBlock;
     // Steps software-pipelined two deep for D <= 128, as decode_fp8_kernel:
     // the loads are unconditional non-temporal loads and the block ids come
     // through explicit scalar loads, so the compiler's wait counts stay
@@ -988,15 +1095,15 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
       }
       float x[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = s0[r] * scale_log2;
-        x[4 + r] = s1[r] * scale_log2;
+      for (int r2 = 0; r2 < 4; ++r2) {
+        x[r2] = s0[r2] * scale_log2;
+        x[4 + r2] = s1[r2] * scale_log2;
       }
       if (st.lim0 < kBlock || st.lim1 < kBlock) {  // wave-uniform
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if (4 * j + r >= st.lim0) x[r] = -INFINITY;
-          if (4 * j + r >= st.lim1) x[4 + r] = -INFINITY;
+        for (int r2 = 0; r2 < 4; ++r2) {
+          if (4 * j + r2 >= st.lim0) x[r2] = -INFINITY;
+          if (4 * j + r2 >= st.lim1) x[4 + r2] = -INFINITY;
         }
         // stale cache contents beyond the context may hold any bits
         const int n0 = min(max(st.lim0 - 4 * j, 0), 4), n1 = min(max(st.lim1 - 4 * j, 0), 4);
@@ -1058,9 +1165,9 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
     }
     lsum += shfl_xor_f(lsum, 16);
     lsum += shfl_xor_f(lsum, 32);
-    if (c < G) {
-      const int k = w - wave_of(seg, total, nw);
-      const int64_t row = ((int64_t)s * Hq + head) * slots + k;
+    if (col_ok) {
+      const int k = (pc.shared ? 0 : pc.slot_base) + w - wave_of(pc.start, total, nw);
+      const int64_t row = ((int64_t)col_seq * Hq + head) * slots + k;
       float* orow = ws_o + row * D + 4 * j;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(orow + 16 * dt) = o[dt];
@@ -1069,7 +1176,7 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
         ws_ml[2 * row + 1] = lsum;
       }
     }
-    g += u1 - u0;
+    gpos += pc.u1 - pc.u0;
   }
 }
 
@@ -1083,10 +1190,10 @@ template <typename T>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(
     T* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ context_lens, int Hq, int D, int num_parts, int mbs,
-    int part_len, int balance_nw, int B, int Hkv) {
+    int part_len, int balance_nw, int B, int Hkv, const int32_t* __restrict__ lcp, int SP) {
   // balance_nw > 0: partial results of decode_balanced_kernel launched with
-  // balance_nw wavefronts (num_parts = slots per row); else partitions of
-  // part_len tokens.
+  // balance_nw wavefronts (num_parts = slots per row; lcp, SP its layout);
+  // else partitions of part_len tokens.
   __shared__ float wsh[1024];
   __shared__ float red[4][512];
   __shared__ float ml[2][4];
@@ -1096,14 +1203,22 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
   const int ctx = min(context_lens[seq], mbs * kBlock);
   int np;
   if (balance_nw > 0) {
-    // the slots of this row's segment: its first to its last wavefront
-    const int64_t total = units_before(context_lens, B, mbs, Hkv);
-    const int n = seq_units(context_lens, seq, mbs);
+    // this row's slots: those of its group's shared segment, then those of
+    // its private segment
+    const BalanceLayout lay{context_lens, lcp, B, mbs, Hkv, SP};
+    const int64_t total = lay.before(lay.groups());
     np = 0;
-    if (total > 0 && n > 0) {
+    if (total > 0) {
       const int nw = balance_waves(total, balance_nw);
-      const int64_t seg = units_before(context_lens, seq, mbs, Hkv) + (int64_t)((row % Hq) / (Hq / Hkv)) * n;
-      np = min(wave_of(seg + n - 1, total, nw) - wave_of(seg, total, nw) + 1, num_parts);
+      const int g = seq / SP, kvh = (row % Hq) / (Hq / Hkv);
+      const int64_t cg = lay.before(g);
+      const int L = lay.shared(g);
+      int64_t off = cg + (int64_t)Hkv * L;
+      for (int m = g * SP; m < seq; ++m) off += (int64_t)Hkv * (lay.units(m) - L);
+      const int len = lay.units(seq) - L;
+      np = min(seg_slots(cg + (int64_t)kvh * L, L, total, nw) +
+                   seg_slots(off + (int64_t)kvh * len, len, total, nw),
+               num_parts);
     }
   } else {
     np = min(min(num_parts, (ctx + part_len - 1) / part_len), 1024);
@@ -1204,12 +1319,13 @@ using namespace pa;
 
 extern "C" size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
                                            int32_t max_context_len) {
-  // Sized for the shortest partition any launch uses, plus one: a balanced
-  // launch writes up to ceil(max_context_len / 256) + 1 partial results per
-  // row.
+  // Sized for the shortest partition any launch uses, plus two: a balanced
+  // launch writes up to ceil(max_context_len / 256) + 2 partial results per
+  // row, and one int per sequence group.
   const int np = num_partitions(max_context_len, kPart);
   if (np <= 1 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  return (size_t)num_seqs * num_heads * (np + 1) * (head_dim + 2) * sizeof(float);
+  return (size_t)num_seqs * num_heads * (np + 2) * (head_dim + 2) * sizeof(float) +
+         (size_t)num_seqs * sizeof(int32_t);
 }
 
 namespace {
@@ -1218,6 +1334,7 @@ namespace {
 struct DecodePlan {
   bool mfma, f32_group;
   bool balanced;  // bf16 launches that would need the reduce: decode_balanced_kernel
+  int share_sp;   // balanced: sequences per shared-prefix group (1: no sharing)
   int part_len, np, merge_waves;  // np: partitions, or partial-result slots per row
   size_t ws_bytes;  // workspace the launch needs (0: none)
 };
@@ -1248,12 +1365,20 @@ DecodePlan decode_plan(int32_t dtype, bool quantized, int32_t num_seqs, int32_t 
   // the work evenly over the GPU instead (bf16 caches): a segment of n units
   // meets at most ceil(n / kBalanceMinUnits) + 1 wavefronts.
   p.balanced = p.mfma && !fp8 && p.np > 1 && p.merge_waves == 1;
+  // A row's slots: at most ceil(n / kBalanceMinUnits) + 1 for each of its
+  // two segments (shared prefix, private rest) of n units in all.  Groups of
+  // 16 / G sequences share a common prefix of their block tables (one
+  // launch of decode_lcp_kernel finds it; its results follow the partial
+  // results in the workspace).
+  p.share_sp = 1;
   if (p.balanced) {
     const int max_units = (max_context_len + 2 * kBlock - 1) / (2 * kBlock);
-    p.np = (max_units + kBalanceMinUnits - 1) / kBalanceMinUnits + 1;
+    p.np = (max_units + kBalanceMinUnits - 1) / kBalanceMinUnits + 2;
+    if (G <= 8 && num_seqs >= 2) p.share_sp = 16 / G;
   }
   p.ws_bytes = p.np > 1 && p.merge_waves == 1
-                   ? (size_t)num_seqs * num_heads * p.np * (head_dim + 2) * sizeof(float)
+                   ? (size_t)num_seqs * num_heads * p.np * (head_dim + 2) * sizeof(float) +
+                         (p.share_sp > 1 ? (size_t)num_seqs * sizeof(int32_t) : 0)
                    : 0;
   return p;
 }
@@ -1301,22 +1426,26 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
              "pa_decode: q row stride %lld below num_heads * head_dim", (long long)q_row);
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
+  const int sp = plan.share_sp;
+  int32_t* lcp = nullptr;
   if (plan.balanced) {
+    if (sp > 1) {
+      lcp = (int32_t*)(ws_ml + (size_t)num_seqs * num_heads * np * 2);
+      decode_lcp_kernel<<<(num_seqs + sp - 1) / sp, 64, 0, s>>>(
+          block_tables, max_blocks_per_seq, context_lens, num_seqs, sp, lcp);
+    }
+#define PA_LAUNCH_BALANCED(DD)                                                                \
+  decode_balanced_kernel<DD><<<kBalanceWaves, 64, 0, s>>>(                                    \
+      (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,   \
+      max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,     \
+      scale_log2, np, ws_o, ws_ml, q_row, lcp, sp)
     if (head_dim == 64)
-      decode_balanced_kernel<64><<<kBalanceWaves, 64, 0, s>>>(
-          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,
-          max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,
-          scale_log2, np, ws_o, ws_ml, q_row);
+      PA_LAUNCH_BALANCED(64);
     else if (head_dim == 128)
-      decode_balanced_kernel<128><<<kBalanceWaves, 64, 0, s>>>(
-          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,
-          max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,
-          scale_log2, np, ws_o, ws_ml, q_row);
+      PA_LAUNCH_BALANCED(128);
     else
-      decode_balanced_kernel<256><<<kBalanceWaves, 64, 0, s>>>(
-          (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,
-          max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,
-          scale_log2, np, ws_o, ws_ml, q_row);
+      PA_LAUNCH_BALANCED(256);
+#undef PA_LAUNCH_BALANCED
   } else if (mfma) {
     const dim3 grid(merge_waves > 1 ? 1 : np, num_kv_heads, num_seqs);
     auto* o = (uint16_t*)out;
@@ -1391,12 +1520,12 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
     decode_reduce_kernel<uint16_t><<<rgrid, 256, 0, s>>>((uint16_t*)out, ws_o, ws_ml,
                                                          context_lens, num_heads, head_dim, np,
                                                          max_blocks_per_seq, part_len, bal,
-                                                         num_seqs, num_kv_heads);
+                                                         num_seqs, num_kv_heads, lcp, sp);
   else
     decode_reduce_kernel<float><<<rgrid, 256, 0, s>>>((float*)out, ws_o, ws_ml, context_lens,
                                                       num_heads, head_dim, np,
                                                       max_blocks_per_seq, part_len, bal,
-                                                      num_seqs, num_kv_heads);
+                                                      num_seqs, num_kv_heads, lcp, sp);
   return check_launch("pa_decode reduce");
 }
 }  // namespace
