@@ -337,9 +337,6 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   const int head = kvh * G + head_in_group;
   const int r0 = tok0 + tsub * 16 * NT;  // first query row of this wavefront
   const bool rows_active = wave_active && r0 < qlen;
-  const int wave_key_last = min(past + min(qlen, r0 + 16 * NT), key_end) - 1;  // last key needed
-  const int n_steps = 2 * n_kt;                                     // workgroup steps
-  const int wave_steps = rows_active ? min(n_steps, wave_key_last / 32 + 1) : 0;
 
   bf16x8 qv[NT][KS];
   f32x4 o[NT][DT];
