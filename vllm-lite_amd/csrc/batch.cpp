@@ -51,14 +51,22 @@ struct DevBuf {
   }
 };
 
+// A region of the batch's index buffer.
+struct Region {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
 }  // namespace
 
 struct pa_batch {
   int num_seqs = 0, num_tokens = 0, max_blocks = 0, max_q = 0, max_ctx = 0, num_blocks = 0;
   int capacity = 0;  // fixed max context for decode launches (0 = per step)
   bool decode = false;
-  // device arrays
-  DevBuf positions, slots, tables, cu_q, past, ctx_lens, workspace;
+  // device arrays: the index arrays are regions of one buffer (one upload
+  // per prepare), at offsets that only change when a region must grow
+  DevBuf index_buf, workspace;
+  Region positions, slots, tables, cu_q, past, ctx_lens;
   // pinned staging, two slots used in turn: a prepare waits (on the event
   // recorded after its uploads) only for the uploads of the prepare two
   // calls back, so the host can prepare the next step while the device
@@ -150,7 +158,6 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
   }
   const size_t b_pos = pos.size() * 8, b_slot = slot.size() * 8, b_tab = table.size() * 4,
                b_cu = cu.size() * 4, b_past = past.size() * 4, b_ctx = ctxl.size() * 4;
-  const size_t total = b_pos + b_slot + b_tab + b_cu + b_past + b_ctx;
   const int sl = b->slot;
   if (b->pending[sl]) {  // this slot's previous uploads have been read
     if (hipEventSynchronize(b->uploaded[sl]) != hipSuccess) {
@@ -164,52 +171,55 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
     pa::set_error("pa_batch_prepare: event creation failed");
     return PA_ERR_HIP;
   }
-  if (total > b->stage_bytes[sl]) {
+  Region* regs[6] = {&b->positions, &b->slots, &b->tables, &b->cu_q, &b->past, &b->ctx_lens};
+  const size_t need[6] = {std::max<size_t>(b_pos, 8),  std::max<size_t>(b_slot, 8),
+                          std::max<size_t>(b_tab, 4),  std::max<size_t>(b_cu, 4),
+                          std::max<size_t>(b_past, 4), std::max<size_t>(b_ctx, 4)};
+  bool grow = false;
+  for (int i = 0; i < 6; ++i) grow = grow || need[i] > regs[i]->bytes;
+  hipStream_t s = (hipStream_t)stream;
+  if (grow) {
+    // New region capacities (twice the old, at least the need, 256-byte
+    // aligned).  The buffer is replaced: wait for the work queued on the
+    // stream (it may still read the old one) first.
+    if (hipStreamSynchronize(s) != hipSuccess) {
+      pa::set_error("pa_batch_prepare: stream synchronisation failed");
+      return PA_ERR_HIP;
+    }
+    size_t cap[6], total = 0;
+    for (int i = 0; i < 6; ++i) {
+      cap[i] = (std::max(need[i], 2 * regs[i]->bytes) + 255) / 256 * 256;
+      total += cap[i];
+    }
+    int32_t rc = b->index_buf.ensure(total);
+    if (rc != PA_OK) return rc;
+    size_t off = 0;
+    for (int i = 0; i < 6; ++i) {
+      regs[i]->ptr = (char*)b->index_buf.ptr + off;
+      regs[i]->bytes = cap[i];
+      off += cap[i];
+    }
+  }
+  // the upload spans the regions up to the end of the last one used
+  const size_t span = (size_t)((char*)b->ctx_lens.ptr - (char*)b->index_buf.ptr) + b_ctx;
+  if (span > b->stage_bytes[sl]) {
     if (b->stage[sl]) (void)hipHostFree(b->stage[sl]);
     b->stage[sl] = nullptr;
     b->stage_bytes[sl] = 0;
-    if (hipHostMalloc(&b->stage[sl], total, hipHostMallocDefault) != hipSuccess) {
-      pa::set_error("pa_batch_prepare: pinned staging of %zu bytes failed", total);
+    if (hipHostMalloc(&b->stage[sl], span, hipHostMallocDefault) != hipSuccess) {
+      pa::set_error("pa_batch_prepare: pinned staging of %zu bytes failed", span);
       return PA_ERR_HIP;
     }
-    b->stage_bytes[sl] = total;
+    b->stage_bytes[sl] = span;
   }
-  // A device array that must grow is replaced: wait for the work queued
-  // on the stream (it may still read the old one) first.
-  const bool grow = std::max<size_t>(b_pos, 8) > b->positions.bytes ||
-                    std::max<size_t>(b_slot, 8) > b->slots.bytes ||
-                    std::max<size_t>(b_tab, 4) > b->tables.bytes || b_cu > b->cu_q.bytes ||
-                    std::max<size_t>(b_past, 4) > b->past.bytes ||
-                    std::max<size_t>(b_ctx, 4) > b->ctx_lens.bytes;
-  hipStream_t s = (hipStream_t)stream;
-  if (grow && hipStreamSynchronize(s) != hipSuccess) {
-    pa::set_error("pa_batch_prepare: stream synchronisation failed");
-    return PA_ERR_HIP;
-  }
-  int32_t rc = PA_OK;
-  if ((rc = b->positions.ensure(std::max<size_t>(b_pos, 8))) ||
-      (rc = b->slots.ensure(std::max<size_t>(b_slot, 8))) ||
-      (rc = b->tables.ensure(std::max<size_t>(b_tab, 4))) || (rc = b->cu_q.ensure(b_cu)) ||
-      (rc = b->past.ensure(std::max<size_t>(b_past, 4))) ||
-      (rc = b->ctx_lens.ensure(std::max<size_t>(b_ctx, 4))))
-    return rc;
   char* st = (char*)b->stage[sl];
-  struct Part {
-    const void* src;
-    size_t bytes;
-    void* dst;
-  } parts[] = {{pos.data(), b_pos, b->positions.ptr},   {slot.data(), b_slot, b->slots.ptr},
-               {table.data(), b_tab, b->tables.ptr},   {cu.data(), b_cu, b->cu_q.ptr},
-               {past.data(), b_past, b->past.ptr},     {ctxl.data(), b_ctx, b->ctx_lens.ptr}};
-  size_t off = 0;
-  for (const Part& p : parts) {
-    if (p.bytes == 0) continue;
-    std::memcpy(st + off, p.src, p.bytes);
-    if (hipMemcpyAsync(p.dst, st + off, p.bytes, hipMemcpyHostToDevice, s) != hipSuccess) {
-      pa::set_error("pa_batch_prepare: upload failed");
-      return PA_ERR_HIP;
-    }
-    off += p.bytes;
+  const void* src[6] = {pos.data(), slot.data(), table.data(), cu.data(), past.data(), ctxl.data()};
+  const size_t bytes[6] = {b_pos, b_slot, b_tab, b_cu, b_past, b_ctx};
+  for (int i = 0; i < 6; ++i)
+    if (bytes[i]) std::memcpy(st + ((char*)regs[i]->ptr - (char*)b->index_buf.ptr), src[i], bytes[i]);
+  if (span > 0 && hipMemcpyAsync(b->index_buf.ptr, st, span, hipMemcpyHostToDevice, s) != hipSuccess) {
+    pa::set_error("pa_batch_prepare: upload failed");
+    return PA_ERR_HIP;
   }
   if (hipEventRecord(b->uploaded[sl], s) != hipSuccess) {
     pa::set_error("pa_batch_prepare: event record failed");
