@@ -5,6 +5,8 @@ Independent checks: the reference's own test values
 (kv_cache_fp8/tests.rs), torch's float8_e4m3fn conversions wherever that
 format and the reference's agree, exhaustive round trips over the byte
 codes, and a brute-force nearest-value search for the encoder."""
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -94,3 +96,22 @@ def test_encode_is_nearest_with_ties_up(oracle):
     want = np.where(x < 0, -want, want)
     want = np.where(want == 0, 0.0, want)
     assert np.array_equal(got, want)
+
+
+def test_fp8_swar_helpers_exhaustive(tmp_path):
+    # The integer decode and the exotic-code mask that the FP8 attention
+    # kernels use, compiled for the host from pa_common.hpp and checked on
+    # every pair of codes / every code in every byte position.
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc not available")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    exe = str(tmp_path / "fp8_swar_check")
+    subprocess.run([hipcc, "-O2", "-std=c++17", "-x", "hip", "--offload-arch=gfx950",
+                    "-I", os.path.join(root, "vllm-lite_amd", "csrc"),
+                    os.path.join(root, "tests", "native", "fp8_swar_check.cpp"), "-o", exe],
+                   check=True, capture_output=True)
+    r = subprocess.run([exe], capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stdout
