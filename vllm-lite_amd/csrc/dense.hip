@@ -124,8 +124,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(T* __restrict__ out,
 //          path, whose projection output is bf16).
 // Weight tiles of the last column block that lie past N (N a multiple of 16)
 // read row n0 and are not stored.
-// Epilogue 3 (the decode step's QKV projection with RoPE and the KV-cache
-// write fused in): per token row m its position and cache slot, the
+// Epilogue 3 (NT = 1; the decode step's QKV projection with RoPE and the
+// KV-cache write fused in): per token row m its position and cache slot, the
 // inverse-frequency table, the layer's caches ([NB, Hkv, 16, D] keys,
 // token-minor [NB, Hkv, D, 16] values) and the head layout of the output
 // columns (Hq query heads, then Hkv key heads, then Hkv value heads of D).
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
     const uint16_t* __restrict__ bias, int M, int N, int K, int kw, int flags, float eps,
     float* __restrict__ ws, int* __restrict__ counters, const RopeCacheArgs ra) {
   static_assert(EPI != 2 || NT == 2, "SwiGLU pairs one gate and one up tile");
-  static_assert(EPI != 3 || NT == 2, "RoPE pairs the two halves of a head in two tiles");
+  static_assert(EPI != 3 || NT == 1, "RoPE pairs sit in one tile, partners 32 lanes apart");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, j = lane >> 4;
@@ -217,22 +217,54 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
       }
     }
   };
+  // Epilogue 3: with rope pairs, tile u of a query or key head holds head
+  // rows 8 u .. 8 u + 7 (tile rows 0-7: first members) and D / 2 + 8 u ..
+  // D / 2 + 8 u + 7 (tile rows 8-15: second members), as linear_pack_kernel
+  // packs them.  Lane (c, j) holds tile rows 4 j .. 4 j + 3 (head rows
+  // f .. f + 3), so its row 4 j + r belongs to pair 8 u + 4 (j & 1) + r and
+  // the partner member is in lane ^ 32; value heads keep their row order.
+  // Wavefront 0 loads the epilogue's other operands (bias, cache slots,
+  // positions) ahead of the weight stream, so their round trips do not
+  // queue behind it.
+  uint16_t bias3[4] = {0, 0, 0, 0};
+  int64_t slot3[2] = {-1, -1};
+  int64_t pos3 = 0;
+  if constexpr (EPI == 3) {
+    if (wave == 0) {
+      const int D = ra.D;
+      const int head = n0 / D, u = (n0 % D) / 16;
+      const bool rot = head < ra.Hq + ra.Hkv;
+      const int f = rot ? (j >> 1) * (D / 2) + 8 * u + 4 * (j & 1) : 16 * u + 4 * j;
+      if (bias) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bias3[r] = bias[head * D + f + r];
+      }
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) slot3[bb] = ra.slots[min(m0 + 16 * bb + c, M - 1)];
+      if (rot) pos3 = ra.positions[min(m0 + (j >= 2 ? 16 : 0) + c, M - 1)];
+    }
+  }
   if (s0 < s1) load(s0, a[0], b[0]);
-  // Epilogue 3: the rotation angles of this lane's pairs (batch rows c and
-  // 16 + c, pairs i = f0 + 4 j + r), computed by wavefront 0 while its first
-  // loads are in flight.
+  // The rotation angles of batch rows c (bb 0) and 16 + c (bb 1), computed
+  // by wavefront 0 while its loads are in flight: lanes j < 2 take batch
+  // row c, lanes j >= 2 batch row 16 + c (the same pairs), and the partners
+  // swap results.
   float rsn[2][4], rcs[2][4];
   if constexpr (EPI == 3) {
     const int head = n0 / ra.D;
     if (wave == 0 && head < ra.Hq + ra.Hkv) {
-      const int f0 = 8 * ((n0 % ra.D) / 16);
+      const int pi0 = 8 * ((n0 % ra.D) / 16) + 4 * (j & 1);
+      const bool hi = j >= 2;
+      const float pos = (float)pos3;
 #pragma unroll
-      for (int bb = 0; bb < 2; ++bb) {
-        const int m = min(m0 + 16 * bb + c, M - 1);
-        const float pos = (float)ra.positions[m];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          sincosf(pos * ra.inv_freq[f0 + 4 * j + r], &rsn[bb][r], &rcs[bb][r]);
+      for (int r = 0; r < 4; ++r) {
+        float sn, cs;
+        sincosf(pos * ra.inv_freq[pi0 + r], &sn, &cs);
+        const float osn = __shfl_xor(sn, 32, 64), ocs = __shfl_xor(cs, 32, 64);
+        rsn[0][r] = hi ? osn : sn;
+        rcs[0][r] = hi ? ocs : cs;
+        rsn[1][r] = hi ? sn : osn;
+        rcs[1][r] = hi ? cs : ocs;
       }
     }
   }
@@ -357,61 +389,46 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
       *reinterpret_cast<uint64_t*>(out + (int64_t)m * N + n0 + 4 * j) =
           *reinterpret_cast<const uint64_t*>(o4);
     } else if constexpr (EPI == 3) {
-      // Packed by linear_pack_kernel with rope pairs: within a query or key
-      // head the two tiles hold head rows 16 p .. +15 and D / 2 + 16 p .. +15
-      // (p = the tile pair), so this lane holds both members (i, i + D / 2)
-      // of the rotation pairs i = 16 p + 4 j + r of batch row m.  Value
-      // heads keep their row order.  Rounded to bf16 as the unfused
-      // projection output, then rotated as rope_cache_kernel does.
+      // Rounded to bf16 as the unfused projection output, then rotated as
+      // rope_cache_kernel does (the partner member from lane ^ 32; lanes c
+      // and c ^ 32 share the batch row, so both take this branch or neither).
+      // Value heads keep their row order.
       const int D = ra.D;
       const int head = n0 / D, u = (n0 % D) / 16;
       const bool rot = head < ra.Hq + ra.Hkv;
-      const int f0 = rot ? 8 * u : 16 * u;                   // head row of tile 0
-      const int f1 = rot ? D / 2 + 8 * u : 16 * u + 16;      // head row of tile 1
-      float y[2][4];
+      const int f = rot ? (j >> 1) * (D / 2) + 8 * u + 4 * (j & 1) : 16 * u + 4 * j;  // head row
+      float y[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float a0 = acc[0][bb][r] * inv[bb], a1 = acc[1][bb][r] * inv[bb];
-        if (bias) {
-          a0 += bf16_bits_to_f32(bias[head * D + f0 + 4 * j + r]);
-          a1 += bf16_bits_to_f32(bias[head * D + f1 + 4 * j + r]);
-        }
-        y[0][r] = bf16_bits_to_f32(f32_to_bf16_bits(a0));
-        y[1][r] = bf16_bits_to_f32(f32_to_bf16_bits(a1));
+        float a0 = acc[0][bb][r] * inv[bb];
+        if (bias) a0 += bf16_bits_to_f32(bias3[r]);
+        y[r] = bf16_bits_to_f32(f32_to_bf16_bits(a0));
       }
       if (rot) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+          const float p = __shfl_xor(y[r], 32, 64);
           const float sn = rsn[bb][r], cs = rcs[bb][r];
-          const float x1 = y[0][r], x2 = y[1][r];
-          y[0][r] = x1 * cs - x2 * sn;
-          y[1][r] = x2 * cs + x1 * sn;
+          y[r] = j < 2 ? y[r] * cs - p * sn : y[r] * cs + p * sn;
         }
       }
-      uint16_t o4[2][4];
+      uint16_t o4[4];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o4[t][r] = f32_to_bf16_bits(y[t][r]);
-      uint16_t* orow = out + (int64_t)m * N + head * D + 4 * j;
-      *reinterpret_cast<uint64_t*>(orow + f0) = *reinterpret_cast<const uint64_t*>(o4[0]);
-      *reinterpret_cast<uint64_t*>(orow + f1) = *reinterpret_cast<const uint64_t*>(o4[1]);
-      const int64_t slot = ra.slots[m];
+      for (int r = 0; r < 4; ++r) o4[r] = f32_to_bf16_bits(y[r]);
+      *reinterpret_cast<uint64_t*>(out + (int64_t)m * N + head * D + f) =
+          *reinterpret_cast<const uint64_t*>(o4);
+      const int64_t slot = slot3[bb];
       if (head >= ra.Hq && slot >= 0 && slot < ra.num_slots) {
         const int64_t blk = slot / kBlock;
         const int off = (int)(slot % kBlock);
         if (rot) {
-          uint16_t* kd = ra.k_cache + ((blk * ra.Hkv + (head - ra.Hq)) * kBlock + off) * D + 4 * j;
-          *reinterpret_cast<uint64_t*>(kd + f0) = *reinterpret_cast<const uint64_t*>(o4[0]);
-          *reinterpret_cast<uint64_t*>(kd + f1) = *reinterpret_cast<const uint64_t*>(o4[1]);
+          uint16_t* kd = ra.k_cache + ((blk * ra.Hkv + (head - ra.Hq)) * kBlock + off) * D + f;
+          *reinterpret_cast<uint64_t*>(kd) = *reinterpret_cast<const uint64_t*>(o4);
         } else {
           uint16_t* vd =
-              ra.v_cache + ((blk * ra.Hkv + (head - ra.Hq - ra.Hkv)) * D + 4 * j) * kBlock + off;
+              ra.v_cache + ((blk * ra.Hkv + (head - ra.Hq - ra.Hkv)) * D + f) * kBlock + off;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            vd[(f0 + r) * kBlock] = o4[0][r];
-            vd[(f1 + r) * kBlock] = o4[1][r];
-          }
+          for (int r = 0; r < 4; ++r) vd[r * kBlock] = o4[r];
         }
       }
     } else {
@@ -459,14 +476,14 @@ __global__ __launch_bounds__(256) void linear_pack_kernel(uint16_t* __restrict__
     const int step = (int)(frag % nsteps);
     const int64_t row = tile * 16 + (lane & 15);
     // With rope pairs (rope_d = head_dim, the first rope_rows rows being
-    // query and key heads): packed tile 2 p + h of a head takes the head's
-    // rows h * D / 2 + 16 p .. +15, so tiles 2 p and 2 p + 1 hold the two
-    // halves of the rotation pairs 16 p .. 16 p + 15.
+    // query and key heads): row c of packed tile u of a head is the head's
+    // row 8 u + c for c < 8 and D / 2 + 8 u + c - 8 for c >= 8, so a tile
+    // holds both members of the rotation pairs 8 u .. 8 u + 7.
     int64_t src_row = row;
     if (row < rope_rows) {
       const int64_t hd = row / rope_d;
-      const int u = (int)(row % rope_d) / 16;
-      src_row = hd * rope_d + (u & 1) * (rope_d / 2) + (u >> 1) * 16 + (lane & 15);
+      const int u = (int)(row % rope_d) / 16, c = lane & 15;
+      src_row = hd * rope_d + (c >> 3) * (rope_d / 2) + 8 * u + (c & 7);
     }
     const int col = step * 32 + 8 * (lane >> 4);
     uint4 v = *reinterpret_cast<const uint4*>(src + src_row * K + col);
@@ -863,12 +880,19 @@ extern "C" int32_t pa_linear_rope_cache(void* out, const void* x, const void* we
   // K split over the wavefronts as pa_linear splits it for this shape (up
   // to the 8 wavefronts this instance launches with), so the f32 sums, and
   // so the bf16 outputs, are those of pa_linear
-  const int kw = std::min(8, linear_plan(rows, n, in_features, PA_ACT_NONE, false).kw);
+  const LinearPlan lp = linear_plan(rows, n, in_features, PA_ACT_NONE, false);
+  const int kw = std::min(8, lp.kw);
   const RopeCacheArgs ra{positions, slot_mapping, inv_freq, (uint16_t*)k_cache,
                          (uint16_t*)v_cache, (int64_t)num_blocks * kBlock, num_heads,
                          num_kv_heads, head_dim};
-  linear_skinny_kernel<3, 2, true, 4><<<dim3(n / 32, (rows + 31) / 32), 64 * kw, 0, (hipStream_t)stream>>>(
-      (uint16_t*)out, (const uint16_t*)x, (const uint16_t*)weight, (const uint16_t*)bias, rows,
-      n, in_features, kw, flags, eps, nullptr, nullptr, ra);
+  const dim3 grid(n / 16, (rows + 31) / 32);
+  if (lp.stage == 8)
+    linear_skinny_kernel<3, 1, true, 8><<<grid, 64 * kw, 0, (hipStream_t)stream>>>(
+        (uint16_t*)out, (const uint16_t*)x, (const uint16_t*)weight, (const uint16_t*)bias, rows,
+        n, in_features, kw, flags, eps, nullptr, nullptr, ra);
+  else
+    linear_skinny_kernel<3, 1, true, 4><<<grid, 64 * kw, 0, (hipStream_t)stream>>>(
+        (uint16_t*)out, (const uint16_t*)x, (const uint16_t*)weight, (const uint16_t*)bias, rows,
+        n, in_features, kw, flags, eps, nullptr, nullptr, ra);
   return check_launch("pa_linear_rope_cache");
 }
