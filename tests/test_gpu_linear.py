@@ -177,8 +177,10 @@ def test_linear_split_k(pa, m, n, k, act, rms, add):
             torch.testing.assert_close(outs[0].float(), nsplit.float(), atol=2e-2, rtol=1e-2)
 
 
+# k = 4096: more than 64 K steps per workgroup, the stage-4 instance
 @pytest.mark.parametrize("rows,hq,hkv,d,k", [(32, 14, 2, 64, 896), (5, 32, 8, 128, 256),
-                                             (40, 4, 4, 64, 64), (1, 8, 2, 32, 128)])
+                                             (40, 4, 4, 64, 64), (1, 8, 2, 32, 128),
+                                             (3, 8, 2, 128, 4096)])
 @pytest.mark.parametrize("rms,with_bias", [(True, True), (False, False)])
 def test_linear_rope_cache_matches_unfused(pa, rows, hq, hkv, d, k, rms, with_bias):
     # pa_linear_rope_cache == pa_linear on the row-major-packed weight, then

@@ -224,13 +224,14 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
   // f .. f + 3), so its row 4 j + r belongs to pair 8 u + 4 (j & 1) + r and
   // the partner member is in lane ^ 32; value heads keep their row order.
   // Wavefront 0 loads the epilogue's other operands (bias, cache slots,
-  // positions) ahead of the weight stream, so their round trips do not
-  // queue behind it.
+  // positions); the one-stage instance (U = 8) ahead of the weight stream,
+  // so their round trips do not queue behind it, the 1024-thread instance,
+  // whose registers are fewer, after its K loop.
   uint16_t bias3[4] = {0, 0, 0, 0};
   int64_t slot3[2] = {-1, -1};
   int64_t pos3 = 0;
-  if constexpr (EPI == 3) {
-    if (wave == 0) {
+  auto epi_operands = [&]() {
+    if (EPI == 3 && wave == 0) {
       const int D = ra.D;
       const int head = n0 / D, u = (n0 % D) / 16;
       const bool rot = head < ra.Hq + ra.Hkv;
@@ -243,31 +244,34 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
       for (int bb = 0; bb < 2; ++bb) slot3[bb] = ra.slots[min(m0 + 16 * bb + c, M - 1)];
       if (rot) pos3 = ra.positions[min(m0 + (j >= 2 ? 16 : 0) + c, M - 1)];
     }
-  }
+  };
+  if constexpr (U == 8) epi_operands();
   if (s0 < s1) load(s0, a[0], b[0]);
   // The rotation angles of batch rows c (bb 0) and 16 + c (bb 1), computed
-  // by wavefront 0 while its loads are in flight: lanes j < 2 take batch
-  // row c, lanes j >= 2 batch row 16 + c (the same pairs), and the partners
-  // swap results.
+  // by wavefront 0 (with the operands above: U = 8 while its loads are in
+  // flight): lanes j < 2 take batch row c, lanes j >= 2 batch row 16 + c
+  // (the same pairs), and the partners swap results.
   float rsn[2][4], rcs[2][4];
-  if constexpr (EPI == 3) {
-    const int head = n0 / ra.D;
-    if (wave == 0 && head < ra.Hq + ra.Hkv) {
-      const int pi0 = 8 * ((n0 % ra.D) / 16) + 4 * (j & 1);
-      const bool hi = j >= 2;
-      const float pos = (float)pos3;
+  auto angles = [&]() {
+    if constexpr (EPI == 3) {
+      const int head = n0 / ra.D;
+      if (wave == 0 && head < ra.Hq + ra.Hkv) {
+        const int pi0 = 8 * ((n0 % ra.D) / 16) + 4 * (j & 1);
+        const bool hi = j >= 2;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float sn, cs;
-        sincosf(pos * ra.inv_freq[pi0 + r], &sn, &cs);
-        const float osn = __shfl_xor(sn, 32, 64), ocs = __shfl_xor(cs, 32, 64);
-        rsn[0][r] = hi ? osn : sn;
-        rcs[0][r] = hi ? ocs : cs;
-        rsn[1][r] = hi ? sn : osn;
-        rcs[1][r] = hi ? cs : ocs;
+        for (int r = 0; r < 4; ++r) {
+          float sn, cs;
+          sincosf((float)pos3 * ra.inv_freq[pi0 + r], &sn, &cs);
+          const float osn = __shfl_xor(sn, 32, 64), ocs = __shfl_xor(cs, 32, 64);
+          rsn[0][r] = hi ? osn : sn;
+          rcs[0][r] = hi ? ocs : cs;
+          rsn[1][r] = hi ? sn : osn;
+          rcs[1][r] = hi ? cs : ocs;
+        }
       }
     }
-  }
+  };
+  if constexpr (U == 8) angles();
   for (int s = s0; s < s1; s += 2 * U) {
     if (s + U < s1) load(s + U, a[1], b[1]);
     mma(s, a[0], b[0]);
@@ -276,6 +280,10 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
     mma(s + U, a[1], b[1]);
   }
 
+  if constexpr (U != 8) {
+    epi_operands();
+    angles();
+  }
   constexpr int MAXW = NT == 1 && U == 4 ? 16 : 8;
   __shared__ f32x4 red[MAXW - 1][2 * NT][64];
   __shared__ float rss[MAXW][2][16];
@@ -877,11 +885,11 @@ extern "C" int32_t pa_linear_rope_cache(void* out, const void* x, const void* we
   // K split over the wavefronts as pa_linear splits it for this shape (up
   // to the 8 wavefronts this instance launches with), so the f32 sums, and
   // so the bf16 outputs, are those of pa_linear
-  // K split over the wavefronts as pa_linear splits it for this shape (up
-  // to the 8 wavefronts this instance launches with), so the f32 sums, and
-  // so the bf16 outputs, are those of pa_linear
+  // K split over the wavefronts as pa_linear splits it for this shape (the
+  // same instance size), so the f32 sums, and so the bf16 outputs, are
+  // those of pa_linear
   const LinearPlan lp = linear_plan(rows, n, in_features, PA_ACT_NONE, false);
-  const int kw = std::min(8, lp.kw);
+  const int kw = lp.kw;
   const RopeCacheArgs ra{positions, slot_mapping, inv_freq, (uint16_t*)k_cache,
                          (uint16_t*)v_cache, (int64_t)num_blocks * kBlock, num_heads,
                          num_kv_heads, head_dim};
