@@ -518,13 +518,18 @@ def main():
             roof["flushed_frac"] = round(w.alg_bytes / t_flush / 1e9 / HBM_PEAK_GBS, 4)
         if args.config == "splitk":
             roof["unique_block_gbs"] = round((w.unique_kv_bytes) / t_attn / 1e9, 1)
+            # the profiled HBM bytes (FETCH + WRITE) over this run's launch time
+            if traffic:
+                roof["physical_frac"] = round(traffic / t_attn / 1e9 / HBM_PEAK_GBS, 4)
         # configs 2 (bf16, FP8): two 2048-token partitions per (kv head,
-        # sequence), merged in the workgroup; config 4: 512-token partitions and
-        # the reduce kernel; config 1 (f32): the group kernel and the reduce kernel
+        # sequence), merged in the workgroup; config 4: the work cut evenly over
+        # the GPU, a sequence group's shared block-table prefix attended once
+        # (its length found by decode_lcp_kernel), partial results merged by the
+        # reduce kernel; config 1 (f32): the group kernel and the reduce kernel
         roof["kernel"] = {
             "decode": "pa_decode (decode_mfma_kernel, partitions merged in the workgroup)",
             "decode-fp8": "pa_decode (decode_fp8_kernel, partitions merged in the workgroup)",
-            "splitk": "pa_decode (decode_mfma_kernel + decode_reduce_kernel)",
+            "splitk": "pa_decode (decode_lcp_kernel + decode_balanced_kernel + decode_reduce_kernel)",
             "qwen": "pa_decode (decode_f32_group_kernel + decode_reduce_kernel)",
         }[args.config]
     else:
