@@ -288,3 +288,47 @@ def test_balanced_shared_prefix_groups(pa, oracle, hq, hkv, d):
     got = oracle.bf16_to_f32(to_np(out))
     assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL,
                  f"balanced shared prefix {hq}/{hkv}x{d}")
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_balanced_random_sweep(pa, oracle, seed):
+    # Seeded random shapes on the balanced launch: group sizes 1-8, head
+    # dims 64 / 128, up to 24 sequences of 1-6000 tokens, and block tables
+    # whose prefixes are shared by random runs of sequences up to random
+    # divergence points (some shorter than the shared part), against the
+    # oracle.
+    rng = np.random.default_rng(700 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 4, 7, 8]))
+    hq, d = hkv * g, int(rng.choice([64, 128]))
+    b = int(rng.integers(2, 25))
+    ctx = rng.integers(1, 6000, b).astype(np.int32)
+    ctx[rng.integers(0, b)] = int(rng.integers(4200, 6000))   # at least one long row
+    if b > 3:
+        ctx[rng.integers(0, b)] = int(rng.integers(1, 40))    # and a short one
+    prefix = int(rng.integers(0, 120))
+    case = make_decode_case(rng, b, hq, hkv, d, ctx, dtype="bf16", shared_prefix_blocks=prefix)
+    bt = case["block_tables"]
+    nb = case["num_blocks"]
+    # private copies of the prefix for some sequences, diverging at random
+    extra = rng.permutation(np.arange(nb, nb + prefix * b + 1)).astype(np.int32)
+    used = 0
+    for s_ in range(b):
+        if prefix and rng.random() < 0.3:
+            cut = int(rng.integers(0, prefix))
+            n = min(prefix, (int(ctx[s_]) + 15) // 16) - cut
+            if n > 0:
+                bt[s_, cut:cut + n] = extra[used:used + n]
+                used += n
+    grow = len(extra) if used else 0   # the pool grows by every id `extra` may hold
+    if grow:
+        for key in ("k_cache", "v_cache_ref"):
+            pad = rng.standard_normal((grow,) + case[key].shape[1:], dtype=np.float32)
+            case[key] = np.concatenate([case[key], oracle.f32_to_bf16(pad)])
+    print(f"sweep seed {seed}: B {b}, {hq}/{hkv} x {d}, prefix {prefix}, max ctx {ctx.max()}",
+          flush=True)
+    out = pa.decode(to_dev(case["q"]), to_dev(case["k_cache"]),
+                    to_dev(oracle.v_from_ref(case["v_cache_ref"])), to_dev(bt),
+                    to_dev(ctx), int(ctx.max()))
+    got = oracle.bf16_to_f32(to_np(out))
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, f"sweep seed {seed}")
