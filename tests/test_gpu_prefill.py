@@ -183,3 +183,25 @@ def test_config3_full_size(pa, oracle):
                     to_dev(bt[seq]), to_dev(ctx), int(ctx.max()))
     assert_close(got, oracle.bf16_to_f32(to_np(dec)), 2e-2, 1e-2,
                  "config 3 full, all rows vs pa_decode")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_prefill_random_sweep(pa, oracle, seed):
+    # Seeded random shapes on the tiled kernel (bf16, D 64 / 128) and its
+    # persistent schedule: group sizes 1-8 (head groups of at most four per
+    # workgroup), 1-7 sequences with 1-400 new tokens on 0-800 past tokens,
+    # every row against the oracle.
+    rng = np.random.default_rng(900 + seed)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    g = int(rng.choice([1, 2, 3, 4, 7, 8]))
+    hq, d = hkv * g, int(rng.choice([64, 128]))
+    b = int(rng.integers(1, 8))
+    chunks = [int(x) for x in rng.integers(1, 401, b)]
+    pasts = [int(x) for x in rng.integers(0, 801, b)]
+    if b > 2:
+        pasts[0] = 0
+    print(f"prefill sweep seed {seed}: {hq}/{hkv} x {d}, chunks {chunks}, pasts {pasts}",
+          flush=True)
+    case = make_prefill_case(oracle, rng, pasts, chunks, hq, hkv, d, "bf16")
+    got, ref = run_prefill(pa, oracle, *case, "bf16")
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, f"prefill sweep seed {seed}")
