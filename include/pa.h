@@ -71,7 +71,10 @@ const char* pa_version(void);
 
 /* Scatter T tokens' K and V into the cache: token t goes to block
  * slot_mapping[t] / 16, offset slot_mapping[t] % 16.  Slots < 0 or
- * >= num_blocks * 16 are skipped.
+ * >= num_blocks * 16 are skipped.  Slots are expected to be distinct (as a
+ * scheduler's slot mapping is): the reference writes tokens in order, so a
+ * repeated slot keeps the last token's K / V, while here which of them
+ * survives is unspecified.
  *   key, value    [T, Hkv, D] with token strides key_stride / value_stride
  *                 (elements; 0 means Hkv * D, i.e. contiguous)
  *   slot_mapping  [T] int64
