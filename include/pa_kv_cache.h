@@ -121,7 +121,10 @@ void pa_batch_destroy(pa_batch* batch);
  * arrays may be reused on return): the launches that read the batch
  * (pa_batch_attention, pa_batch_qkv_rope_cache) must be on the same stream.
  * A prepare waits only for the uploads of the prepare two calls back, so
- * the host can prepare step n + 1 while the device runs step n. */
+ * the host can prepare step n + 1 while the device runs step n.
+ * A call rejected by validation leaves the batch as it was; one that fails
+ * later (a HIP allocation, upload or event error) leaves it empty (no
+ * tokens: the batch's launches then do nothing). */
 int32_t pa_batch_prepare(pa_batch* batch, int32_t num_seqs, const int32_t* num_tokens,
                          const int32_t* num_computed, const int64_t* block_ids,
                          const int32_t* block_counts, int32_t num_blocks, pa_stream_t stream);

@@ -114,6 +114,10 @@ def test_prepare_rejects_bad_tables(pa):
     with pytest.raises(pa.PaError, match="table holds"):
         batch.prepare(cache, [20], [0], [[1]])
     batch.prepare(cache, [17], [0], [[1, 2]])
+    # a prepare rejected by validation leaves the prepared step as it was
+    with pytest.raises(pa.PaError, match="out of bounds"):
+        batch.prepare(cache, [1, 1], [3, 3], [[1], [9]])
+    assert batch.num_tokens() == 17
     q = torch.zeros(17, 4, 64, dtype=torch.bfloat16, device=DEV)
     kv = torch.zeros(17, 2, 64, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(pa.PaError, match="layer_idx"):

@@ -136,6 +136,13 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
     PA_REQUIRE(block_ids[i] >= 0 && block_ids[i] < num_blocks, PA_ERR_OUT_OF_BOUNDS,
                "block_id %lld out of bounds for %d blocks", (long long)block_ids[i], num_blocks);
 
+  // From here on the previous step's arrays are being replaced: until this
+  // call succeeds the batch is empty (attention on it does nothing), so a
+  // failure below never pairs old counts with new, partly written arrays.
+  b->num_seqs = 0;
+  b->num_tokens = 0;
+  b->decode = false;
+
   // Host images of the index arrays, packed into one staging buffer.
   const int T = (int)total_tokens;
   std::vector<int64_t> pos(T), slot(T);
@@ -192,7 +199,11 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
       total += cap[i];
     }
     int32_t rc = b->index_buf.ensure(total);
-    if (rc != PA_OK) return rc;
+    if (rc != PA_OK) {
+      // the old buffer is gone: no region may point into it
+      for (int i = 0; i < 6; ++i) *regs[i] = Region{};
+      return rc;
+    }
     size_t off = 0;
     for (int i = 0; i < 6; ++i) {
       regs[i]->ptr = (char*)b->index_buf.ptr + off;

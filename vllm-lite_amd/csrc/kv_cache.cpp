@@ -66,9 +66,13 @@ struct pa_kv_cache {
 
 namespace {
 
+// Waits for the call's upload and launch.  Also after a failed launch: the
+// upload from the pinned stage may still be in flight, and the next call
+// refills the stage.  The first error is the one reported.
 int32_t finish(hipStream_t stream, int32_t rc) {
+  const bool synced = hipStreamSynchronize(stream) == hipSuccess;
   if (rc != PA_OK) return rc;
-  if (hipStreamSynchronize(stream) != hipSuccess) {
+  if (!synced) {
     pa::set_error("pa_kv_cache: stream synchronisation failed");
     return PA_ERR_HIP;
   }
