@@ -198,7 +198,11 @@ size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t hea
  *   block_tables  [num_seqs, max_blocks_per_seq] int32
  *   context_lens  [num_seqs] int32: keys 0 .. context_lens[s]-1 are attended
  *                 (the new token must already be in the cache)
- *   max_context_len  host upper bound of context_lens (sizes the split)
+ *   max_context_len  host upper bound of context_lens (sizes the split and
+ *                 the workspace); a sequence whose context_lens entry is
+ *                 above it (a caller error) gets an unspecified result for
+ *                 its rows, and nothing outside out and the workspace is
+ *                 written
  *   scale         softmax scale, e.g. attn_factor / sqrt(D)
  *   workspace     pa_decode_workspace_size() bytes (may be NULL if 0)
  * out[s, h] = softmax(scale * q[s, h] · K[s, h/g]ᵀ) · V[s, h/g].

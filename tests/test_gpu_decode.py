@@ -332,3 +332,30 @@ def test_balanced_random_sweep(pa, oracle, seed):
                     to_dev(ctx), int(ctx.max()))
     got = oracle.bf16_to_f32(to_np(out))
     assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, f"sweep seed {seed}")
+
+
+def test_context_above_max_context_len_stays_in_bounds(pa, oracle):
+    """A context_lens entry above the max_context_len argument (a caller
+    error) must not write outside the workspace pa_decode_workspace_size
+    sized for max_context_len: the balanced split-K launch clamps lengths to
+    it.  The other sequences' results are unaffected; a canary after the
+    sized workspace stays intact."""
+    rng = np.random.default_rng(77)
+    ctx = np.array([9000, 12000, 300, 5000], np.int32)
+    case = make_decode_case(rng, len(ctx), 32, 8, 128, ctx, dtype="bf16", kv_scale=0.5)
+    max_ctx = 6000  # below the first two sequences' lengths
+    need = pa.ops.decode_workspace_size(len(ctx), 32, 128, max_ctx)
+    assert need > 0
+    ws = torch.full((need + 65536,), 0x5A, dtype=torch.uint8, device=DEV)
+    out = pa.decode(to_dev(case["q"]), to_dev(case["k_cache"]),
+                    to_dev(oracle.v_from_ref(case["v_cache_ref"])), to_dev(case["block_tables"]),
+                    to_dev(ctx), max_ctx, workspace=ws)
+    torch.cuda.synchronize()
+    assert bool((ws[need:] == 0x5A).all()), "write past the sized workspace"
+    got = oracle.bf16_to_f32(to_np(out))
+    ref = oracle.bf16_to_f32(oracle.paged_attention(
+        case["q"], case["k_cache"], case["v_cache_ref"],
+        np.where(case["block_tables"] < 0, 0, case["block_tables"]), np.arange(len(ctx) + 1),
+        ctx - 1, scale=1.0 / math.sqrt(128)))
+    assert_close(got[2:], ref[2:], BF16_ATOL, BF16_RTOL, "sequences within max_context_len")
+    assert np.isfinite(got[:2]).all()

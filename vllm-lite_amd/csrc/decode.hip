@@ -848,8 +848,12 @@ __device__ inline int64_t uniform64(int64_t x) {
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)x >> 32));
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
-__device__ inline int seq_units(const int32_t* __restrict__ context_lens, int s, int mbs) {
-  const int ctx = min(context_lens[s], mbs * kBlock);
+// Context lengths are clamped to the table and to the launch's
+// max_context_len (`cap`): the workspace slots are sized from it, so a
+// length above it (a caller error) never gets more slots than a row has.
+__device__ inline int seq_units(const int32_t* __restrict__ context_lens, int s, int mbs,
+                                int cap) {
+  const int ctx = min(min(context_lens[s], mbs * kBlock), cap);
   return ctx > 0 ? (ctx + 2 * kBlock - 1) / (2 * kBlock) : 0;
 }
 
@@ -864,8 +868,8 @@ __device__ inline int seq_units(const int32_t* __restrict__ context_lens, int s,
 struct BalanceLayout {
   const int32_t* __restrict__ ctx;
   const int32_t* __restrict__ lcp;  // null: no shared prefixes
-  int B, mbs, Hkv, SP;
-  __device__ int units(int s) const { return seq_units(ctx, s, mbs); }
+  int B, mbs, Hkv, SP, cap;
+  __device__ int units(int s) const { return seq_units(ctx, s, mbs, cap); }
   __device__ int shared(int g) const { return lcp ? lcp[g] : 0; }
   __device__ int groups() const { return (B + SP - 1) / SP; }
   __device__ int64_t group_units(int g) const {
@@ -901,11 +905,12 @@ __device__ inline int seg_slots(int64_t start, int len, int64_t total, int nw) {
 // BalanceLayout): one wavefront per group.
 __global__ __launch_bounds__(64) void decode_lcp_kernel(
     const int32_t* __restrict__ block_tables, int mbs, const int32_t* __restrict__ context_lens,
-    int B, int SP, int32_t* __restrict__ lcp) {
+    int B, int SP, int cap, int32_t* __restrict__ lcp) {
   const int g = blockIdx.x, lane = threadIdx.x;
   const int g0 = g * SP, gn = min(SP, B - g0);
   int L = INT32_MAX;
-  for (int m = 0; m < gn; ++m) L = min(L, min(context_lens[g0 + m], mbs * kBlock) / (2 * kBlock));
+  for (int m = 0; m < gn; ++m)
+    L = min(L, min(min(context_lens[g0 + m], mbs * kBlock), cap) / (2 * kBlock));
   if (gn < 2) L = 0;
   // the first block, below 2 L, where a member's table differs from the first's
   for (int b0 = 0; b0 < 2 * L; b0 += 64) {
@@ -944,12 +949,12 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int B, int Hq, int Hkv, int G, int num_blocks,
     float scale_log2, int slots, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int64_t q_row, const int32_t* __restrict__ lcp, int SP) {
+    int64_t q_row, const int32_t* __restrict__ lcp, int SP, int cap) {
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
   const int lane = threadIdx.x;
   const int c = lane & 15, j = lane >> 4;
-  const BalanceLayout lay{context_lens, lcp, B, mbs, Hkv, SP};
+  const BalanceLayout lay{context_lens, lcp, B, mbs, Hkv, SP, cap};
   const int64_t total = lay.before(lay.groups());
   const int nw = balance_waves(total, gridDim.x);
   const int w = blockIdx.x;
@@ -1031,7 +1036,7 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
     }
     pc.u1 = (int)min((int64_t)pc.u1, pc.u0 + (hi - gpos));
     const int kvh = pc.kvh;
-    const int ctx = min(context_lens[pc.seq], mbs * kBlock);
+    const int ctx = min(min(context_lens[pc.seq], mbs * kBlock), cap);
     const int tok0 = (pc.unit_base + pc.u0) * 2 * kBlock;
     const int tok_end = pc.shared ? (pc.unit_base + pc.u1) * 2 * kBlock
                                   : min(ctx, (pc.unit_base + pc.u1) * 2 * kBlock);
@@ -1190,7 +1195,8 @@ template <typename T>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(
     T* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ context_lens, int Hq, int D, int num_parts, int mbs,
-    int part_len, int balance_nw, int B, int Hkv, const int32_t* __restrict__ lcp, int SP) {
+    int part_len, int balance_nw, int B, int Hkv, const int32_t* __restrict__ lcp, int SP,
+    int cap) {
   // balance_nw > 0: partial results of decode_balanced_kernel launched with
   // balance_nw wavefronts (num_parts = slots per row; lcp, SP its layout);
   // else partitions of part_len tokens.
@@ -1205,7 +1211,7 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
   if (balance_nw > 0) {
     // this row's slots: those of its group's shared segment, then those of
     // its private segment
-    const BalanceLayout lay{context_lens, lcp, B, mbs, Hkv, SP};
+    const BalanceLayout lay{context_lens, lcp, B, mbs, Hkv, SP, cap};
     const int64_t total = lay.before(lay.groups());
     np = 0;
     if (total > 0) {
@@ -1432,13 +1438,13 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
     if (sp > 1) {
       lcp = (int32_t*)(ws_ml + (size_t)num_seqs * num_heads * np * 2);
       decode_lcp_kernel<<<(num_seqs + sp - 1) / sp, 64, 0, s>>>(
-          block_tables, max_blocks_per_seq, context_lens, num_seqs, sp, lcp);
+          block_tables, max_blocks_per_seq, context_lens, num_seqs, sp, max_context_len, lcp);
     }
 #define PA_LAUNCH_BALANCED(DD)                                                                \
   decode_balanced_kernel<DD><<<kBalanceWaves, 64, 0, s>>>(                                    \
       (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,   \
       max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,     \
-      scale_log2, np, ws_o, ws_ml, q_row, lcp, sp)
+      scale_log2, np, ws_o, ws_ml, q_row, lcp, sp, max_context_len)
     if (head_dim == 64)
       PA_LAUNCH_BALANCED(64);
     else if (head_dim == 128)
@@ -1520,12 +1526,14 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
     decode_reduce_kernel<uint16_t><<<rgrid, 256, 0, s>>>((uint16_t*)out, ws_o, ws_ml,
                                                          context_lens, num_heads, head_dim, np,
                                                          max_blocks_per_seq, part_len, bal,
-                                                         num_seqs, num_kv_heads, lcp, sp);
+                                                         num_seqs, num_kv_heads, lcp, sp,
+                                                         max_context_len);
   else
     decode_reduce_kernel<float><<<rgrid, 256, 0, s>>>((float*)out, ws_o, ws_ml, context_lens,
                                                       num_heads, head_dim, np,
                                                       max_blocks_per_seq, part_len, bal,
-                                                      num_seqs, num_kv_heads, lcp, sp);
+                                                      num_seqs, num_kv_heads, lcp, sp,
+                                                      max_context_len);
   return check_launch("pa_decode reduce");
 }
 }  // namespace
