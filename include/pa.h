@@ -262,7 +262,10 @@ int32_t pa_decode_quantized(void* out, const void* q, const float* k_cache, cons
  * Query row i of sequence s sits at absolute position past_lens[s] + i and
  * attends keys j <= past_lens[s] + i, all read from the cache (write the
  * chunk's K/V with pa_reshape_and_cache first).  Table entries outside
- * [0, num_blocks) contribute no keys, as in pa_decode.
+ * [0, num_blocks) contribute no keys, as in pa_decode.  cu_q_lens entries
+ * outside [0, total_q], sequences of more than max_q_len rows and negative
+ * past_lens are caller errors: the rows concerned are unspecified, and no
+ * read or write leaves q and out (offsets are clamped on the device).
  * Replaces forward_prefill / forward_prefill_continue's attention
  * (rope_gqa.rs:261-372): tiled_attention (util.rs:188-234) for past = 0 and
  * compute_gqa_attention + prefill_continue_causal_mask

@@ -205,3 +205,30 @@ def test_prefill_random_sweep(pa, oracle, seed):
     case = make_prefill_case(oracle, rng, pasts, chunks, hq, hkv, d, "bf16")
     got, ref = run_prefill(pa, oracle, *case, "bf16")
     assert_close(got, ref, BF16_ATOL, BF16_RTOL, f"prefill sweep seed {seed}")
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d", [("bf16", 32, 8, 128), ("bf16", 4, 4, 256),
+                                            ("f32", 8, 2, 64)])
+def test_inconsistent_offsets_stay_in_bounds(pa, oracle, dtype, hq, hkv, d):
+    """cu_q_lens past total_q and a sequence longer than max_q_len (caller
+    errors): the kernels (tiled, D 256, generic) clamp the offsets, so
+    nothing is written past `out`; a consistent sequence is unaffected."""
+    rng = np.random.default_rng(hq + d + 5)
+    q, kc, vc, bt, cu, past = make_prefill_case(oracle, rng, [37, 0], [50, 70], hq, hkv, d, dtype)
+    total = 100  # the call owns 100 rows; the offsets claim 120
+    canary = 3.0  # exact in bf16 and f32
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    big = torch.full((total + 40, hq, d), canary, dtype=tdt, device=DEV)
+    out = big[:total]
+    qd = to_dev(q)[:total]
+    pa.prefill(qd, to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(bt), to_dev(cu),
+               to_dev(past), 60, out=out)  # max_q_len 60 < the second sequence's 70
+    torch.cuda.synchronize()
+    assert bool((big[total:].float() == canary).all()), "write past out"
+    got = to_np(out)[:50]
+    if dtype == "bf16":
+        got = oracle.bf16_to_f32(got)
+    ref = oracle.paged_attention(oracle.as_f32(q[:50]), oracle.as_f32(kc), oracle.as_f32(vc),
+                                 bt[:1], cu[:2], past[:1])
+    tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
+    assert_close(got, ref, *tol, "consistent sequence")

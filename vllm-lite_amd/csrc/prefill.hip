@@ -30,6 +30,22 @@ constexpr float kNegBig = -1.0e30f;
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float shfl_xor_f(float x, int mask) { return __shfl_xor(x, mask, 64); }
 
+// A sequence's query rows and past length as the kernels use them.  The
+// offsets are device data: they are clamped to the rows the call owns
+// ([0, total_q)) and to max_q rows per sequence (the grid is sized for
+// that), and a past outside [0, 2^30] is clamped into it, so inconsistent
+// offsets (a caller error) never move a read or write outside q and out.
+struct QRange {
+  int begin, len, past;
+};
+__device__ inline QRange q_range(const int32_t* __restrict__ cu_q,
+                                 const int32_t* __restrict__ past_lens, int seq, int total_q,
+                                 int max_q) {
+  const int b = min(max(cu_q[seq], 0), total_q);
+  const int e = min(max(cu_q[seq + 1], b), total_q);
+  return {b, min(e - b, max_q), min(max(past_lens[seq], 0), 1 << 30)};
+}
+
 constexpr int kWaves = 4;
 template <int V>
 using IC = std::integral_constant<int, V>;
@@ -45,7 +61,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
-    int num_blocks, float scale_log2, int64_t q_row) {
+    int num_blocks, float scale_log2, int64_t q_row, int total_q, int max_q) {
   constexpr int KS = D / 32;
   constexpr int DT = D / 16;
   constexpr int ROWS = 16 * NT;  // query rows per wavefront
@@ -53,11 +69,12 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_mfma_kernel(
   const int c = lane & 15, j = lane >> 4;
   const int h = blockIdx.y, seq = blockIdx.z;
   const int G = Hq / Hkv, kvh = h / G;
-  const int q_begin = cu_q[seq];
-  const int qlen = cu_q[seq + 1] - q_begin;
+  const QRange qr = q_range(cu_q, past_lens, seq, total_q, max_q);
+  const int q_begin = qr.begin;
+  const int qlen = qr.len;
   const int row0 = (blockIdx.x * kWaves + wave) * ROWS;
   if (row0 >= qlen) return;
-  const int past = past_lens[seq];
+  const int past = qr.past;
   const int row_end = min(qlen, row0 + ROWS);
   const int kv_len = min(past + row_end, mbs * kBlock);  // keys this wavefront needs
   const int nblk = (kv_len + kBlock - 1) / kBlock;
@@ -243,7 +260,8 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const TC* __restrict__ kc,
     const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
-    int num_blocks, float scale_log2, int B, int tiles_per_seq, int head_groups, int64_t q_row) {
+    int num_blocks, float scale_log2, int B, int tiles_per_seq, int head_groups, int64_t q_row,
+    int total_q, int max_q) {
   constexpr int KS = D / 32;   // QK reduction steps
   constexpr int DT = D / 16;   // PV output tiles
   // Cache elements: bf16 (TC = uint16_t) or FP8-E4M3 (TC = uint8_t), the
@@ -297,8 +315,8 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   __shared__ int seq_of_rank[64];
   if (B <= 64 && (int)threadIdx.x < B) {
     auto work = [&](int b) -> long long {
-      const long long ql = cu_q[b + 1] - cu_q[b];
-      return ql * (2 * (long long)past_lens[b] + ql);
+      const QRange r = q_range(cu_q, past_lens, b, total_q, max_q);
+      return (long long)r.len * (2 * (long long)r.past + r.len);
     };
     const int b = threadIdx.x;
     const long long wb = work(b);
@@ -322,11 +340,12 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   const int seq = seq_of(rem / tiles_per_seq);
   const int kvh = kvhg / head_groups, hg = kvhg % head_groups;
 
-  const int q_begin = cu_q[seq];
-  const int qlen = cu_q[seq + 1] - q_begin;
+  const QRange qr = q_range(cu_q, past_lens, seq, total_q, max_q);
+  const int q_begin = qr.begin;
+  const int qlen = qr.len;
   const int tok0 = tile * TT;
   if (tok0 >= qlen) return;  // uniform over the workgroup
-  const int past = past_lens[seq];
+  const int past = qr.past;
   const int key_end = min(past + min(qlen, tok0 + TT), mbs * kBlock);
   const int n_kt = (key_end + KT - 1) / KT;
   const int nblk = (key_end + kBlock - 1) / kBlock;
@@ -790,16 +809,18 @@ __global__ __launch_bounds__(64) void prefill_generic_kernel(
     T* __restrict__ out, const T* __restrict__ q, const TC* __restrict__ kc,
     const TC* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ past_lens, int Hq, int Hkv,
-    int D, int num_blocks, float scale_log2, const float* __restrict__ kv_scales, int64_t q_row) {
+    int D, int num_blocks, float scale_log2, const float* __restrict__ kv_scales, int64_t q_row,
+    int total_q, int max_q) {
   // kv_scales: per-block scales of a quantised (int8-in-f32) cache, or null
   __shared__ float qs[512];
   __shared__ float ps[64];
   __shared__ int32_t bids[64];
   const int row = blockIdx.x, h = blockIdx.y, seq = blockIdx.z, lane = threadIdx.x;
-  const int q_begin = cu_q[seq];
-  if (row >= cu_q[seq + 1] - q_begin) return;
+  const QRange qr = q_range(cu_q, past_lens, seq, total_q, max_q);
+  const int q_begin = qr.begin;
+  if (row >= qr.len) return;
   const int G = Hq / Hkv, kvh = h / G;
-  const int pos = past_lens[seq] + row;
+  const int pos = qr.past + row;
   const int64_t qoff = (int64_t)(q_begin + row) * q_row + (int64_t)h * D;
   for (int d = lane; d < D; d += 64) qs[d] = Elem<T>::load(q + qoff + d);
   float acc[8];
@@ -924,7 +945,7 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
   prefill_tiled_kernel<DD, NT, TC><<<grid, 64 * (16 / NT), 0, s>>>(                           \
       o, qq, (const TC*)k_cache, (const TC*)v_cache, block_tables, max_blocks_per_seq,        \
       cu_q_lens, past_lens, num_heads, num_kv_heads, num_blocks, scale_log2, num_seqs,        \
-      tiles_per_seq, head_groups, q_row)
+      tiles_per_seq, head_groups, q_row, total_q, max_q_len)
     if (fp8) {
       if (head_dim == 128)
         PA_LAUNCH_TILED(128, uint8_t);
@@ -948,7 +969,7 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
 #define PA_LAUNCH_PREFILL(DD)                                                                 \
   prefill_mfma_kernel<DD, NT><<<grid, 64 * kWaves, 0, s>>>(                                   \
       o, qq, kc, vc, block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads,       \
-      num_kv_heads, num_blocks, scale_log2, q_row)
+      num_kv_heads, num_blocks, scale_log2, q_row, total_q, max_q_len)
     PA_LAUNCH_PREFILL(256);
 #undef PA_LAUNCH_PREFILL
   } else {
@@ -957,17 +978,17 @@ int32_t prefill_impl(void* out, const void* q, const void* k_cache, const void* 
       prefill_generic_kernel<uint16_t, Fp8><<<grid, 64, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const Fp8*)k_cache, (const Fp8*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2, nullptr, q_row);
+          head_dim, num_blocks, scale_log2, nullptr, q_row, total_q, max_q_len);
     else if (dtype == PA_DTYPE_BF16)
       prefill_generic_kernel<uint16_t><<<grid, 64, 0, s>>>(
           (uint16_t*)out, (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2, nullptr, q_row);
+          head_dim, num_blocks, scale_log2, nullptr, q_row, total_q, max_q_len);
     else
       prefill_generic_kernel<float><<<grid, 64, 0, s>>>(
           (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,
           block_tables, max_blocks_per_seq, cu_q_lens, past_lens, num_heads, num_kv_heads,
-          head_dim, num_blocks, scale_log2, kv_scales, q_row);
+          head_dim, num_blocks, scale_log2, kv_scales, q_row, total_q, max_q_len);
   }
   return check_launch("pa_prefill");
 }
