@@ -108,7 +108,9 @@ int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, uint8_t* k_
  *   cu_seq_tokens [num_seqs + 1] int32, slot_mapping [T] int64 (out).
  * Replaces the index arithmetic of paged_gqa.rs:39-52 and :86-97.  The
  * reference silently falls back to block 0 for a missing table entry
- * (paged_gqa.rs:51, :97); here such tokens are skipped instead. */
+ * (paged_gqa.rs:51, :97); here such tokens are skipped instead.  Offsets
+ * outside [0, num_tokens] are clamped on the device (a caller error: the
+ * tokens concerned get no slot written). */
 int32_t pa_slot_mapping(const int32_t* block_tables, int32_t max_blocks_per_seq,
                         const int64_t* positions, const int32_t* cu_seq_tokens,
                         int32_t num_seqs, int32_t num_tokens, int64_t* slot_mapping,

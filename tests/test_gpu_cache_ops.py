@@ -250,3 +250,24 @@ def test_reshape_and_cache_config3_chunk_strided(pa, oracle):
     oracle.reshape_and_cache(kv[:, 1], kv[:, 2], kc, vc, slots)
     assert np.array_equal(to_np(gk), kc)
     assert np.array_equal(oracle.v_to_ref(to_np(gv)), vc)
+
+
+def test_slot_mapping_offsets_past_num_tokens_stay_in_bounds(pa, oracle):
+    """cu_seq_tokens claiming more tokens than num_tokens (a caller error):
+    the kernel clamps the offsets, so nothing is written past slot_mapping
+    and the tokens inside the call are mapped as usual."""
+    rng = np.random.default_rng(10)
+    bt = rng.permutation(40).astype(np.int32)[:6].reshape(2, 3)
+    positions = np.arange(30, dtype=np.int64)
+    cu = np.array([0, 20, 45], np.int32)  # 45 > the 30 tokens of the call
+    big = torch.full((64,), 7777, dtype=torch.int64, device=DEV)
+    lib = pa._lib.load()
+    dbt, dpos, dcu = to_dev(bt), to_dev(positions), to_dev(cu)
+    rc = lib.pa_slot_mapping(dbt.data_ptr(), 3, dpos.data_ptr(), dcu.data_ptr(), 2, 30,
+                             big.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    got = to_np(big)
+    assert np.all(got[30:] == 7777)
+    want = np.concatenate([oracle.slot_mapping(bt[0], positions[:20], 20),
+                           oracle.slot_mapping(bt[1], positions[20:30], 10)])
+    assert np.array_equal(got[:30], want)

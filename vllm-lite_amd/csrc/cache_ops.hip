@@ -250,11 +250,15 @@ __global__ __launch_bounds__(256) void read_kv_fp8_kernel(const uint8_t* __restr
 }
 
 // slot_mapping[t] = block_tables[s][pos / 16] * 16 + pos % 16.
+// The offsets cu are device data: clamped to the call's T tokens, so
+// inconsistent offsets (a caller error) never index outside positions /
+// slots.
 __global__ void slot_mapping_kernel(const int32_t* __restrict__ block_tables, int mbs,
                                     const int64_t* __restrict__ positions,
-                                    const int32_t* __restrict__ cu, int64_t* __restrict__ slots) {
+                                    const int32_t* __restrict__ cu, int T,
+                                    int64_t* __restrict__ slots) {
   const int s = blockIdx.x;
-  const int begin = cu[s], end = cu[s + 1];
+  const int begin = min(max(cu[s], 0), T), end = min(max(cu[s + 1], begin), T);
   for (int t = begin + threadIdx.x; t < end; t += blockDim.x) {
     const int64_t pos = positions[t];
     const int64_t bi = pos / kBlock;
@@ -481,7 +485,7 @@ extern "C" int32_t pa_slot_mapping(const int32_t* block_tables, int32_t max_bloc
   PA_REQUIRE(block_tables && positions && cu_seq_tokens && slot_mapping, PA_ERR_INVALID_ARG,
              "pa_slot_mapping: null pointer");
   slot_mapping_kernel<<<num_seqs, 256, 0, (hipStream_t)stream>>>(
-      block_tables, max_blocks_per_seq, positions, cu_seq_tokens, slot_mapping);
+      block_tables, max_blocks_per_seq, positions, cu_seq_tokens, num_tokens, slot_mapping);
   return check_launch("pa_slot_mapping");
 }
 
