@@ -382,8 +382,12 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   }
 
   // Block ids.  Each wavefront's HBM -> LDS copies of a tile all read one
-  // cache block (block `wblk` of the tile's 4), so per tile a wavefront
-  // loads just that id, one tile ahead of its use.  The index is clamped to
+  // cache block (block `wblk` of the tile's 4), so a wavefront needs just
+  // that id per tile: lane t of `ids` holds it for tile ids_base + t, loaded
+  // for 64 tiles at a time with one vector load (at the item's start, then
+  // every 64 tiles), and each tile takes it with a lane read.  (A scalar load
+  // per tile, through the same counter as the LDS reads, made the step wait
+  // for all its LDS reads at the load.)  The index is clamped to
   // the sequence's last block (keys past key_end are masked and their V
   // zeroed) and an id outside the pool reads block 0.  Whether any id of the
   // item's table lies outside the pool is found once per item (`bad_ids`);
@@ -397,9 +401,20 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
     bad |= (id < 0 || id >= num_blocks) ? 1 : 0;
   }
   const bool bad_ids = __syncthreads_or(bad) != 0;
-  auto fetch_id = [&](int kt) -> int32_t {
-    const int32_t id = btab[min(kt * (KT / kBlock) + wblk, max(nblk - 1, 0))];
+  auto load_ids = [&](int base) -> int32_t {
+    const int t = base + lane;
+    if (t >= n_kt) return 0;
+    const int32_t id = btab[min(t * (KT / kBlock) + wblk, max(nblk - 1, 0))];
     return (id >= 0 && id < num_blocks) ? id : 0;
+  };
+  int ids_base = 0;
+  int32_t ids = load_ids(0);
+  auto fetch_id = [&](int kt) -> int32_t {
+    if (kt - ids_base >= 64) {  // wavefront-uniform
+      ids_base = kt & ~63;
+      ids = load_ids(ids_base);
+    }
+    return __builtin_amdgcn_readlane(ids, kt - ids_base);
   };
   auto tile_valid = [&](int kt) -> int {
     if (!bad_ids) return (1 << (KT / kBlock)) - 1;
