@@ -232,3 +232,26 @@ def test_inconsistent_offsets_stay_in_bounds(pa, oracle, dtype, hq, hkv, d):
                                  bt[:1], cu[:2], past[:1])
     tol = (BF16_ATOL, BF16_RTOL) if dtype == "bf16" else (F32_ATOL, F32_RTOL)
     assert_close(got, ref, *tol, "consistent sequence")
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d", [("bf16", 32, 8, 128), ("bf16", 14, 2, 64),
+                                            ("fp8", 32, 8, 128)])
+def test_prefill_keys_past_64_tiles(pa, oracle, dtype, hq, hkv, d):
+    """Items whose keys span more than 64 LDS tiles (4096 keys): the
+    wavefront's block ids are loaded 64 tiles at a time, so pasts of 6000
+    and 9000 keys cross one and two reloads."""
+    rng = np.random.default_rng(d + hq)
+    pasts, chunks = [6000, 9000, 100], [200, 65, 300]
+    q, kc, vc, bt, cu, past = make_prefill_case(oracle, rng, pasts, chunks, hq, hkv, d,
+                                                "f32" if dtype == "fp8" else dtype)
+    if dtype == "fp8":
+        kcode, vcode = oracle.fp8_encode(kc * 0.5), oracle.fp8_encode(vc * 0.5)
+        qb = oracle.f32_to_bf16(q)
+        out = pa.prefill(to_dev(qb), to_dev(kcode), to_dev(oracle.v_from_ref(vcode)), to_dev(bt),
+                         to_dev(cu), to_dev(past), max(chunks))
+        got = oracle.bf16_to_f32(to_np(out))
+        ref = oracle.paged_attention(oracle.bf16_to_f32(qb), oracle.fp8_decode(kcode),
+                                     oracle.fp8_decode(vcode), bt, cu, past)
+    else:
+        got, ref = run_prefill(pa, oracle, q, kc, vc, bt, cu, past, dtype)
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, f"prefill past 64 tiles {dtype} {hq}/{hkv}x{d}")
