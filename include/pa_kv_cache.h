@@ -77,7 +77,8 @@ int32_t pa_kv_cache_write_kv_batch(pa_kv_cache* cache, int32_t layer, int64_t bl
  * block_ids[pos / 16] at offset pos % 16 with pos = positions[t] (t when
  * positions has fewer than T entries).  block_ids / positions are host
  * arrays.  A position whose block index is past the table is an error here
- * (the reference falls back to block 0, paged_gqa.rs:51). */
+ * (the reference falls back to block 0, paged_gqa.rs:51).  As in the
+ * reference's per-token loop, a slot named twice keeps the later token. */
 int32_t pa_kv_cache_write_prefill_kv(pa_kv_cache* cache, int32_t layer, const int64_t* block_ids,
                                      int32_t n_ids, const int64_t* positions, int32_t n_pos,
                                      int32_t num_tokens, const void* k, const void* v,
@@ -93,6 +94,30 @@ int32_t pa_kv_cache_write_prefill_kv(pa_kv_cache* cache, int32_t layer, const in
 int32_t pa_kv_cache_read_kv(pa_kv_cache* cache, int32_t layer, const int64_t* block_ids,
                             int32_t n_ids, int32_t seq_len, void* out_k, void* out_v,
                             int32_t* n_read, pa_stream_t stream);
+
+/* The per-layer block-hash map of PagedKvCache (block_hashes,
+ * tensor_store/mod.rs:42): every token written by pa_kv_cache_write_kv /
+ * _write_kv_batch / _write_prefill_kv inserts hash -> block_id for the K
+ * block it landed in, hashed as the block stands after that token
+ * (buffer.rs:263-264, in the tokens' order; an equal hash takes the later
+ * block id), with compute_block_hash_from_slice (layout.rs:51-58) over the
+ * block's stored K values in [head][token][dim] order (bf16 caches: their
+ * bf16 values; quantised caches: the stored integer values).  Its readers
+ * in the reference are the multi-node BlockDataSource::has_block and
+ * verify_chain_hash (paged_kv_cache_wrapper.rs:100-140), which look at
+ * layer 0.  The map lives on the host; writes through pa.h's stateless
+ * entry points do not update it.
+ *
+ * pa_kv_cache_block_hash_count: number of entries of the layer's map.
+ * pa_kv_cache_block_hashes: up to `capacity` entries, ascending by hash, into
+ *   hashes / block_ids (host); *written receives the count.
+ * pa_kv_cache_lookup_block_hash: *block_id = the block recorded for `hash`,
+ *   or -1. */
+int32_t pa_kv_cache_block_hash_count(const pa_kv_cache* cache, int32_t layer, int64_t* count);
+int32_t pa_kv_cache_block_hashes(const pa_kv_cache* cache, int32_t layer, uint64_t* hashes,
+                                 int64_t* block_ids, int64_t capacity, int64_t* written);
+int32_t pa_kv_cache_lookup_block_hash(const pa_kv_cache* cache, int32_t layer, uint64_t hash,
+                                      int64_t* block_id);
 
 /* ---------------------------------------------------------------------- */
 /* Batched step (replaces the per-sequence forward loop)                   */

@@ -61,6 +61,9 @@ SIGNATURES = {
     "pa_kv_cache_write_kv_batch": (_i32, [_p, _i32, _i64, _i64, _p, _p, _i32, _p]),
     "pa_kv_cache_write_prefill_kv": (_i32, [_p, _i32, _p, _i32, _p, _i32, _i32, _p, _p, _p]),
     "pa_kv_cache_read_kv": (_i32, [_p, _i32, _p, _i32, _i32, _p, _p, C.POINTER(_i32), _p]),
+    "pa_kv_cache_block_hash_count": (_i32, [_p, _i32, C.POINTER(_i64)]),
+    "pa_kv_cache_block_hashes": (_i32, [_p, _i32, _p, _p, _i64, C.POINTER(_i64)]),
+    "pa_kv_cache_lookup_block_hash": (_i32, [_p, _i32, C.c_uint64, C.POINTER(_i64)]),
     "pa_batch_create": (_i32, [C.POINTER(_p)]),
     "pa_batch_destroy": (None, [_p]),
     "pa_batch_prepare": (_i32, [_p, _i32, _p, _p, _p, _p, _i32, _p]),

@@ -6,6 +6,7 @@
 // token-minor V block ([D, 16] per head), one element per 32 B (bf16) or
 // 64 B (f32) row of the block.
 #include "pa_common.hpp"
+#include "pa_internal.hpp"
 
 namespace pa {
 
@@ -294,21 +295,40 @@ __global__ __launch_bounds__(256) void read_kv_kernel(const T* __restrict__ k_ca
   }
 }
 
-__device__ inline uint64_t hash_term(float x) {
-  const float y = fabsf(x) * 1000.0f;
-  if (!(y > 0.0f)) return 0;  // NaN, +0
-  if (y >= 18446744073709551616.0f) return ~0ull;
-  return (uint64_t)y;
-}
-
-__host__ __device__ inline uint64_t pow_u64(uint64_t b, uint64_t e) {
-  uint64_t r = 1;
-  while (e) {
-    if (e & 1) r *= b;
-    b *= b;
-    e >>= 1;
+// The reference's block-hash bookkeeping of a write (buffer.rs:263-264):
+// after every token written, the hash of the K block it landed in.  Runs
+// before the scatter of the same tokens, on the cache as it was before the
+// call: one workgroup per block task walks the task's tokens in order; per
+// token, slot o's rows come from the token that last wrote slot o in this
+// call (last[o]), the other slots from the cache; hashes[tok[i]] is the
+// hash after token tok[i] (tokens in call order).
+template <typename T>
+__global__ __launch_bounds__(256) void block_hash_replay_kernel(
+    const T* __restrict__ k_cache, const T* __restrict__ key, int H, int D,
+    const int32_t* __restrict__ task_block, const int32_t* __restrict__ task_beg,
+    const int32_t* __restrict__ tok, const int32_t* __restrict__ off,
+    uint64_t* __restrict__ hashes) {
+  __shared__ uint64_t red[256];
+  __shared__ int last[kBlock];
+  const int w = blockIdx.x;
+  const int n = H * kBlock * D;
+  const T* base = k_cache + (int64_t)task_block[w] * n;
+  if (threadIdx.x < kBlock) last[threadIdx.x] = -1;
+  __syncthreads();
+  for (int i = task_beg[w]; i < task_beg[w + 1]; ++i) {
+    if (threadIdx.x == 0) last[off[i]] = tok[i];
+    __syncthreads();
+    const uint64_t h = workgroup_block_hash(
+        n,
+        [&](int e) -> float {
+          const int hd = e / (kBlock * D), r = e % (kBlock * D);
+          const int j = last[r / D];
+          return j >= 0 ? Elem<T>::load(key + ((int64_t)j * H + hd) * D + r % D)
+                        : Elem<T>::load(base + e);
+        },
+        red);
+    if (threadIdx.x == 0) hashes[tok[i]] = h;
   }
-  return r;
 }
 
 // Polynomial hash sum_i x_i * 31^(n-1-i) (mod 2^64), split into per-thread
@@ -345,6 +365,22 @@ __global__ __launch_bounds__(256) void block_hash_kernel(const float* __restrict
 }
 
 }  // namespace
+
+int32_t launch_block_hash_replay(const void* k_cache, const void* key, int32_t dtype, int H,
+                                 int D, int num_tasks, const int32_t* task_block,
+                                 const int32_t* task_beg, const int32_t* tok,
+                                 const int32_t* off, uint64_t* hashes, hipStream_t stream) {
+  if (num_tasks == 0) return PA_OK;
+  if (dtype == PA_DTYPE_BF16)
+    block_hash_replay_kernel<uint16_t><<<num_tasks, 256, 0, stream>>>(
+        (const uint16_t*)k_cache, (const uint16_t*)key, H, D, task_block, task_beg, tok, off,
+        hashes);
+  else
+    block_hash_replay_kernel<float><<<num_tasks, 256, 0, stream>>>(
+        (const float*)k_cache, (const float*)key, H, D, task_block, task_beg, tok, off, hashes);
+  return check_launch("write_kv block hashes");
+}
+
 }  // namespace pa
 
 using namespace pa;

@@ -9,8 +9,10 @@
 // writes re-quantise whole blocks (quant.hip).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <map>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/pa_kv_cache.h"
@@ -22,6 +24,9 @@ struct pa_kv_cache {
   bool quantized = false;
   std::vector<void*> key, value;
   std::vector<float*> scales;  // quantised caches: [num_blocks] per layer
+  // The reference's per-layer block-hash map (tensor_store/mod.rs:42):
+  // hash of a K block after a token was written -> the block's id.
+  std::vector<std::unordered_map<uint64_t, int64_t>> block_hashes;
   // Staging for host index arrays: pinned host copy -> device copy.
   void* host_stage = nullptr;
   void* dev_stage = nullptr;
@@ -79,17 +84,38 @@ int32_t finish(hipStream_t stream, int32_t rc) {
   return PA_OK;
 }
 
-// Quantised write of T tokens at host-computed slots: the tokens are grouped
-// by block (keeping their order) and each block is re-quantised once per
-// token, as write_kv does.
-int32_t quant_scatter(pa_kv_cache* c, int layer, const std::vector<int64_t>& slots, const void* k,
-                      const void* v, hipStream_t stream) {
+// Writes T tokens at host-computed slots as the reference's per-token
+// write_kv does, block-hash bookkeeping included (buffer.rs:263-264): the
+// tokens are grouped by block (keeping their order) into tasks; every
+// token's K block is hashed as it stands after that token, and the map of
+// the layer receives hash -> block in token order.  Non-quantised caches:
+// the hashes are replayed from the cache before the scatter (one kernel),
+// then the tokens are scattered; quantised caches: each block is
+// re-quantised once per token (quant_write_kernel), which also hashes it.
+int32_t scatter(pa_kv_cache* c, int layer, const std::vector<int64_t>& slots, const void* k,
+                const void* v, hipStream_t stream) {
   std::map<int64_t, std::vector<int32_t>> by_block;  // block -> token indices, in order
   for (size_t t = 0; t < slots.size(); ++t) by_block[slots[t] / pa::kBlock].push_back((int32_t)t);
   const int tasks = (int)by_block.size();
   const int T = (int)slots.size();
-  std::vector<int32_t> host(tasks + (tasks + 1) + 2 * T);
-  int32_t* blk = host.data();
+  // one upload: slots (int64 [T]), hashes (uint64 [T], written on the
+  // device), then the int32 task arrays
+  const size_t n32 = (size_t)tasks + (tasks + 1) + 2 * (size_t)T;
+  std::vector<int64_t> host(2 * (size_t)T + (n32 + 1) / 2);
+  // The scatter writes every slot once, from the last token that names it
+  // (the reference writes token by token, so the last one wins; a slot
+  // named twice in one scatter would be unspecified): earlier ones are -1.
+  {
+    std::vector<int64_t> seen;
+    seen.reserve(T);
+    for (int t = T - 1; t >= 0; --t) {
+      const bool dup = std::find(seen.begin(), seen.end(), slots[t]) != seen.end();
+      host[t] = dup ? -1 : slots[t];
+      if (!dup) seen.push_back(slots[t]);
+    }
+  }
+  auto* i32 = reinterpret_cast<int32_t*>(host.data() + 2 * T);
+  int32_t* blk = i32;
   int32_t* beg = blk + tasks;
   int32_t* tok = beg + tasks + 1;
   int32_t* off = tok + T;
@@ -106,25 +132,34 @@ int32_t quant_scatter(pa_kv_cache* c, int layer, const std::vector<int64_t>& slo
   }
   beg[tasks] = i;
   int32_t rc = PA_OK;
-  auto* d = (int32_t*)c->upload(host.data(), host.size() * sizeof(int32_t), stream, &rc);
+  auto* d = (char*)c->upload(host.data(), host.size() * sizeof(int64_t), stream, &rc);
   if (rc != PA_OK) return rc;
-  rc = pa::launch_quant_write((float*)c->key[layer], (float*)c->value[layer], c->scales[layer],
-                              (const float*)k, (const float*)v, c->num_heads, c->head_dim, tasks,
-                              d, d + tasks, d + 2 * tasks + 1, d + 2 * tasks + 1 + T, stream);
-  return finish(stream, rc);
-}
-
-// Scatters T tokens at host-computed slots.
-int32_t scatter(pa_kv_cache* c, int layer, const std::vector<int64_t>& slots, const void* k,
-                const void* v, hipStream_t stream) {
-  if (c->quantized) return quant_scatter(c, layer, slots, k, v, stream);
-  int32_t rc = PA_OK;
-  void* d_slots = c->upload(slots.data(), slots.size() * sizeof(int64_t), stream, &rc);
+  const auto* d_slots = (const int64_t*)d;
+  auto* d_hash = (uint64_t*)(d + (size_t)T * sizeof(int64_t));
+  const auto* d32 = (const int32_t*)(d + 2 * (size_t)T * sizeof(int64_t));
+  const int32_t *d_blk = d32, *d_beg = d32 + tasks, *d_tok = d_beg + tasks + 1, *d_off = d_tok + T;
+  if (c->quantized) {
+    rc = pa::launch_quant_write((float*)c->key[layer], (float*)c->value[layer], c->scales[layer],
+                                (const float*)k, (const float*)v, c->num_heads, c->head_dim,
+                                tasks, d_blk, d_beg, d_tok, d_off, d_hash, stream);
+  } else {
+    rc = pa::launch_block_hash_replay(c->key[layer], k, c->dtype, c->num_heads, c->head_dim,
+                                      tasks, d_blk, d_beg, d_tok, d_off, d_hash, stream);
+    if (rc == PA_OK)
+      rc = pa_reshape_and_cache(k, v, c->key[layer], c->value[layer], d_slots, T, c->num_heads,
+                                c->head_dim, c->num_blocks, 0, 0, c->dtype, (pa_stream_t)stream);
+  }
+  rc = finish(stream, rc);
   if (rc != PA_OK) return rc;
-  rc = pa_reshape_and_cache(k, v, c->key[layer], c->value[layer], (const int64_t*)d_slots,
-                            (int32_t)slots.size(), c->num_heads, c->head_dim, c->num_blocks, 0, 0,
-                            c->dtype, (pa_stream_t)stream);
-  return finish(stream, rc);
+  std::vector<uint64_t> hashes(T);
+  if (hipMemcpy(hashes.data(), d_hash, (size_t)T * sizeof(uint64_t), hipMemcpyDeviceToHost) !=
+      hipSuccess) {
+    pa::set_error("pa_kv_cache: reading the block hashes back failed");
+    return PA_ERR_HIP;
+  }
+  auto& map = c->block_hashes[layer];
+  for (int t = 0; t < T; ++t) map[hashes[t]] = slots[t] / pa::kBlock;
+  return PA_OK;
 }
 
 }  // namespace
@@ -144,6 +179,7 @@ extern "C" int32_t pa_kv_cache_create(int32_t num_layers, int32_t num_kv_heads, 
   c->head_dim = head_dim;
   c->num_blocks = num_blocks;
   c->dtype = dtype;
+  c->block_hashes.resize(num_layers);
   const size_t bytes = c->layer_bytes();
   for (int l = 0; l < num_layers; ++l) {
     void *k = nullptr, *v = nullptr;
@@ -326,4 +362,45 @@ extern "C" int32_t pa_kv_cache_read_kv(pa_kv_cache* c, int32_t layer, const int6
   rc = finish(s, rc);
   if (rc == PA_OK) *n_read = n;
   return rc;
+}
+
+extern "C" int32_t pa_kv_cache_block_hash_count(const pa_kv_cache* c, int32_t layer,
+                                                int64_t* count) {
+  pa::clear_error();
+  PA_REQUIRE(c && count, PA_ERR_INVALID_ARG, "block_hash_count: null argument");
+  PA_REQUIRE(layer >= 0 && layer < c->num_layers, PA_ERR_OUT_OF_BOUNDS,
+             "layer_idx %d out of bounds for %d layers", layer, c->num_layers);
+  *count = (int64_t)c->block_hashes[layer].size();
+  return PA_OK;
+}
+
+extern "C" int32_t pa_kv_cache_block_hashes(const pa_kv_cache* c, int32_t layer,
+                                            uint64_t* hashes, int64_t* block_ids,
+                                            int64_t capacity, int64_t* written) {
+  pa::clear_error();
+  PA_REQUIRE(c && written && capacity >= 0 && (capacity == 0 || (hashes && block_ids)),
+             PA_ERR_INVALID_ARG, "block_hashes: bad arguments");
+  PA_REQUIRE(layer >= 0 && layer < c->num_layers, PA_ERR_OUT_OF_BOUNDS,
+             "layer_idx %d out of bounds for %d layers", layer, c->num_layers);
+  std::vector<std::pair<uint64_t, int64_t>> e(c->block_hashes[layer].begin(),
+                                              c->block_hashes[layer].end());
+  std::sort(e.begin(), e.end());
+  const int64_t n = std::min<int64_t>(capacity, (int64_t)e.size());
+  for (int64_t i = 0; i < n; ++i) {
+    hashes[i] = e[i].first;
+    block_ids[i] = e[i].second;
+  }
+  *written = n;
+  return PA_OK;
+}
+
+extern "C" int32_t pa_kv_cache_lookup_block_hash(const pa_kv_cache* c, int32_t layer,
+                                                 uint64_t hash, int64_t* block_id) {
+  pa::clear_error();
+  PA_REQUIRE(c && block_id, PA_ERR_INVALID_ARG, "lookup_block_hash: null argument");
+  PA_REQUIRE(layer >= 0 && layer < c->num_layers, PA_ERR_OUT_OF_BOUNDS,
+             "layer_idx %d out of bounds for %d layers", layer, c->num_layers);
+  const auto it = c->block_hashes[layer].find(hash);
+  *block_id = it == c->block_hashes[layer].end() ? -1 : it->second;
+  return PA_OK;
 }

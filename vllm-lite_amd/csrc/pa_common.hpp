@@ -81,6 +81,54 @@ __device__ inline bf16x8 fp8x8_to_bf16_exact(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// Block content hash of the reference (layout.rs:51-58):
+//   fold(0, |acc, x| acc * 31 + (|x| * 1000) as u64)  (wrapping u64)
+// over the block's K values in [head][token][dim] order, i.e.
+//   sum_i term(x_i) * 31^(n-1-i) mod 2^64.  term: Rust's saturating float ->
+// u64 cast (NaN and +0 -> 0, >= 2^64 -> u64::MAX).
+__host__ __device__ inline uint64_t hash_term(float x) {
+  const float y = fabsf(x) * 1000.0f;
+  if (!(y > 0.0f)) return 0;  // NaN, +0
+  if (y >= 18446744073709551616.0f) return ~0ull;
+  return (uint64_t)y;
+}
+__host__ __device__ inline uint64_t pow_u64(uint64_t b, uint64_t e) {
+  uint64_t r = 1;
+  while (e) {
+    if (e & 1) r *= b;
+    b *= b;
+    e >>= 1;
+  }
+  return r;
+}
+// The hash of n values val(0) .. val(n-1) by a workgroup of 256 threads:
+// thread t sums term(val(e)) * 31^(n-1-e) over e = t, t + 256, ...; the
+// partial sums are added through `red` (256 entries).  Every thread returns
+// the hash; ends with a barrier (red may be reused).
+template <typename F>
+__device__ inline uint64_t workgroup_block_hash(int n, F val, uint64_t* red) {
+  const int t = threadIdx.x;
+  uint64_t acc = 0;
+  if (t < n) {
+    const int last = (n - 1 - t) / 256;  // this thread's last element t + 256 last
+    uint64_t p = pow_u64(31u, (uint64_t)(n - 1 - (t + 256 * last)));
+    const uint64_t step = pow_u64(31u, 256u);
+    for (int k = last; k >= 0; --k) {
+      acc += hash_term(val(t + 256 * k)) * p;
+      p *= step;
+    }
+  }
+  red[t] = acc;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (t < s) red[t] += red[t + s];
+    __syncthreads();
+  }
+  const uint64_t h = red[0];
+  __syncthreads();
+  return h;
+}
+
 // bf16 <-> f32 on raw 16-bit patterns (round to nearest even, NaN kept quiet).
 __host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
   return __builtin_bit_cast(float, (uint32_t)h << 16);

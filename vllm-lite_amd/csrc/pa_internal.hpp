@@ -12,7 +12,15 @@ namespace pa {
 PA_HIDDEN int32_t launch_quant_write(float* k_cache, float* v_cache, float* scales,
                                      const float* k, const float* v, int H, int D, int num_tasks,
                                      const int32_t* task_block, const int32_t* task_beg,
-                                     const int32_t* tok, const int32_t* off, hipStream_t stream);
+                                     const int32_t* tok, const int32_t* off, uint64_t* hashes,
+                                     hipStream_t stream);
+// Block hashes after every token of a (non-quantised) write, before its
+// scatter: see cache_ops.hip.
+PA_HIDDEN int32_t launch_block_hash_replay(const void* k_cache, const void* key, int32_t dtype,
+                                           int H, int D, int num_tasks,
+                                           const int32_t* task_block, const int32_t* task_beg,
+                                           const int32_t* tok, const int32_t* off,
+                                           uint64_t* hashes, hipStream_t stream);
 PA_HIDDEN int32_t launch_quant_read(const float* k_cache, const float* v_cache,
                                     const float* scales, const int32_t* block_ids, int seq_len,
                                     int H, int D, float* out_k, float* out_v, hipStream_t stream);

@@ -12,6 +12,7 @@ namespace {
 
 // One workgroup per block task: block task_block[w] receives tokens
 // tok[i] at offsets off[i] for i in [task_beg[w], task_beg[w + 1]), in order.
+// hashes (optional): hashes[tok[i]] = the block hash after token tok[i].
 // Per token, as write_kv: every element of the block is dequantised with the
 // block's current scale (x * s), the token's K / V rows are stored raw, the
 // new scale is max(max|K|, max|V|) / 127 (1 for an all-zero block) and every
@@ -20,8 +21,10 @@ __global__ __launch_bounds__(256) void quant_write_kernel(
     float* __restrict__ kc, float* __restrict__ vc, float* __restrict__ scales,
     const float* __restrict__ k, const float* __restrict__ v, int H, int D,
     const int32_t* __restrict__ task_block, const int32_t* __restrict__ task_beg,
-    const int32_t* __restrict__ tok, const int32_t* __restrict__ off) {
+    const int32_t* __restrict__ tok, const int32_t* __restrict__ off,
+    uint64_t* __restrict__ hashes) {
   __shared__ float red[256];
+  __shared__ uint64_t hred[256];
   const int w = blockIdx.x, tid = threadIdx.x;
   const int64_t blk = task_block[w];
   const int n = H * kBlock * D;
@@ -54,6 +57,12 @@ __global__ __launch_bounds__(256) void quant_write_kernel(
     }
     s = sc;
     __syncthreads();  // red[] is reused by the next token
+    // the block hash of the stored (quantised) K after this token
+    // (buffer.rs:263-264), when asked for
+    if (hashes) {
+      const uint64_t h = workgroup_block_hash(n, [&](int e) { return kb[e]; }, hred);
+      if (tid == 0) hashes[t] = h;
+    }
   }
   if (tid == 0) scales[blk] = s;
 }
@@ -83,10 +92,10 @@ __global__ __launch_bounds__(256) void quant_read_kernel(const float* __restrict
 int32_t launch_quant_write(float* k_cache, float* v_cache, float* scales, const float* k,
                            const float* v, int H, int D, int num_tasks, const int32_t* task_block,
                            const int32_t* task_beg, const int32_t* tok, const int32_t* off,
-                           hipStream_t stream) {
+                           uint64_t* hashes, hipStream_t stream) {
   if (num_tasks == 0) return PA_OK;
   quant_write_kernel<<<num_tasks, 256, 0, stream>>>(k_cache, v_cache, scales, k, v, H, D,
-                                                    task_block, task_beg, tok, off);
+                                                    task_block, task_beg, tok, off, hashes);
   return check_launch("quantised write_kv");
 }
 

@@ -172,6 +172,27 @@ class PagedKvCache:
             C.c_void_p(out_v.data_ptr()) if cover else None, C.byref(n), self._stream()))
         return out_k[: n.value], out_v[: n.value]
 
+    def block_hashes(self, layer_idx):
+        """The layer's block-hash map (PagedKvCache::block_hashes,
+        tensor_store/mod.rs:42): {hash: block_id}, filled by every write
+        (buffer.rs:263-264)."""
+        cnt = C.c_int64(0)
+        _check("block_hash_count", self._lib.pa_kv_cache_block_hash_count(
+            self._h, layer_idx, C.byref(cnt)))
+        n = max(cnt.value, 1)
+        hs, ids = (C.c_uint64 * n)(), (C.c_int64 * n)()
+        got = C.c_int64(0)
+        _check("block_hashes", self._lib.pa_kv_cache_block_hashes(
+            self._h, layer_idx, hs, ids, cnt.value, C.byref(got)))
+        return {int(hs[i]): int(ids[i]) for i in range(got.value)}
+
+    def lookup_block_hash(self, layer_idx, h):
+        """The block id recorded for hash h in the layer's map, or None."""
+        bid = C.c_int64(0)
+        _check("lookup_block_hash", self._lib.pa_kv_cache_lookup_block_hash(
+            self._h, layer_idx, C.c_uint64(h), C.byref(bid)))
+        return None if bid.value < 0 else bid.value
+
 
 class StepBatch:
     """One engine step's batch for every layer (pa_batch_*).
