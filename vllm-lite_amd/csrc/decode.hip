@@ -1308,10 +1308,12 @@ int num_partitions(int max_ctx, int part_len) {
 int choose_partition(int num_seqs, int num_kv_heads, int max_ctx, int head_dim, int elem_bytes) {
   const long long units = (long long)num_seqs * num_kv_heads;
   auto items = [&](int p) { return units * ((max_ctx + p - 1) / p); };
-  // one-byte (FP8) caches: half the length, so the same contexts give twice
-  // the wavefronts (measured on the config-2 shape: 91.2 us at 2048, 84.7 us
-  // at 1024; a streaming probe: 5.7 TB/s with 1024 wavefronts, 6.75 with 2048)
-  const int long_part = elem_bytes == 1 ? 1024 : 2048;
+  // 1024 tokens: the config-2 shape then has 2048 wavefronts (four partitions
+  // merged per workgroup); measured bf16 159.6-159.9 us against 160.4-160.8
+  // at 2048 tokens, FP8 84.7 against 91.2 us (a streaming probe: 5.7 TB/s
+  // with 1024 wavefronts, 6.75 with 2048)
+  const int long_part = 1024;
+  (void)elem_bytes;
   if (max_ctx <= 8192 && items(long_part) >= 1024) return long_part;
   if (items(512) >= 1024) return 512;
   if (items(kPart) < 512 && max_ctx <= 1024 && head_dim <= 128) return kPart / 2;
