@@ -133,7 +133,7 @@ __device__ inline void merge_in_workgroup(uint16_t* __restrict__ out_group, cons
 //      which is exactly what the lane already holds from QK.  Result: lane
 //      holds Oᵀ[dim 16dt + 4j + r][head c].
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void decode_mfma_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
@@ -181,29 +181,37 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
 
   const int32_t* btab = block_tables + (int64_t)seq * mbs + tok0 / kBlock;
   const int64_t head_stride = (int64_t)kBlock * D;  // elements per (block, head)
+  constexpr int SLICE = kBlock * D * 2;  // bytes of one (block, head) of K or V
+  const int koff = (c * D + 8 * j) * 2, voff = (c * kBlock + 4 * j) * 2;
+  using Plain = std::integral_constant<int, 0>;
+  using Stream = std::integral_constant<int, kPolicyNT>;
 
-  for (int ib = 0; ib < nblk; ib += 2) {
+  // One step = two blocks (32 tokens): the K rows and Vᵀ pairs this lane
+  // feeds to the MFMAs, and the blocks' valid lengths.  Steps are
+  // software-pipelined two deep: the loads of step n + 1 are issued before
+  // step n is computed.
+  struct Step {
+    bf16x8 ka[KS], kb[KS];
+    uint64_t va[DT], vb[DT];
+    int lim0, lim1;
+  };
+  auto load_step = [&](int ib, Step& st) {
     // Block ids for this step; ids outside the pool read block 0 and are masked.
     int32_t b0 = btab[ib];
     const bool has1 = ib + 1 < nblk;
     int32_t b1 = has1 ? btab[ib + 1] : b0;
     const int rem = tok_end - (tok0 + ib * kBlock);  // tokens left from this step
-    int lim0 = rem < kBlock ? rem : kBlock;
-    int lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
-    if (b0 < 0 || b0 >= num_blocks) { b0 = 0; lim0 = 0; }
-    if (b1 < 0 || b1 >= num_blocks) { b1 = 0; lim1 = 0; }
-
+    st.lim0 = rem < kBlock ? rem : kBlock;
+    st.lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
+    if (b0 < 0 || b0 >= num_blocks) { b0 = 0; st.lim0 = 0; }
+    if (b1 < 0 || b1 >= num_blocks) { b1 = 0; st.lim1 = 0; }
     const int bi0 = tok0 / kBlock + ib;
     const bool nt0 = private_block(block_tables, mbs, seq, gridDim.z, bi0, b0);
     const bool nt1 = private_block(block_tables, mbs, seq, gridDim.z, bi0 + 1, b1);
-    constexpr int SLICE = kBlock * D * 2;  // bytes of one (block, head) of K or V
     const auto rk0 = slice_rsrc(kc + ((int64_t)b0 * Hkv + kvh) * head_stride, SLICE);
     const auto rk1 = slice_rsrc(kc + ((int64_t)b1 * Hkv + kvh) * head_stride, SLICE);
     const auto rv0 = slice_rsrc(vc + ((int64_t)b0 * Hkv + kvh) * head_stride, SLICE);
     const auto rv1 = slice_rsrc(vc + ((int64_t)b1 * Hkv + kvh) * head_stride, SLICE);
-    const int koff = (c * D + 8 * j) * 2, voff = (c * kBlock + 4 * j) * 2;
-    bf16x8 ka[KS], kb[KS];
-    uint64_t va[DT], vb[DT];
     auto load_block = [&](auto policy, const __amdgpu_buffer_rsrc_t& rk,
                           const __amdgpu_buffer_rsrc_t& rv, bf16x8 (&kx)[KS],
                           uint64_t (&vx)[DT]) {
@@ -213,16 +221,15 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) vx[dt] = bload8<P>(rv, voff + dt * 16 * kBlock * 2);
     };
-    using Plain = std::integral_constant<int, 0>;
-    using Stream = std::integral_constant<int, kPolicyNT>;
-    if (nt0) load_block(Stream{}, rk0, rv0, ka, va); else load_block(Plain{}, rk0, rv0, ka, va);
-    if (nt1) load_block(Stream{}, rk1, rv1, kb, vb); else load_block(Plain{}, rk1, rv1, kb, vb);
-
+    if (nt0) load_block(Stream{}, rk0, rv0, st.ka, st.va); else load_block(Plain{}, rk0, rv0, st.ka, st.va);
+    if (nt1) load_block(Stream{}, rk1, rv1, st.kb, st.vb); else load_block(Plain{}, rk1, rv1, st.kb, st.vb);
+  };
+  auto compute_step = [&](Step& st) {
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qv[s], s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[s], qv[s], s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.ka[s], qv[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(st.kb[s], qv[s], s1, 0, 0, 0);
     }
 
     float x[8];
@@ -231,6 +238,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
       x[r] = s0[r] * scale_log2;
       x[4 + r] = s1[r] * scale_log2;
     }
+    const int lim0 = st.lim0, lim1 = st.lim1;
     const bool partial = lim0 < kBlock || lim1 < kBlock;  // wave-uniform
     if (partial) {
 #pragma unroll
@@ -245,8 +253,8 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
       const uint64_t mk1 = n1 >= 4 ? ~0ull : ((1ull << (16 * n1)) - 1);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        va[dt] &= mk0;
-        vb[dt] &= mk1;
+        st.va[dt] &= mk0;
+        st.vb[dt] &= mk1;
       }
     }
 
@@ -278,10 +286,20 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(
 
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const uint64_t pair[2] = {va[dt], vb[dt]};
+      const uint64_t pair[2] = {st.va[dt], st.vb[dt]};
       const bf16x8 a = *reinterpret_cast<const bf16x8*>(pair);
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
     }
+  };
+
+  Step sa, sb;
+  if (nblk > 0) load_step(0, sa);
+  for (int ib = 0; ib < nblk; ib += 4) {
+    if (ib + 2 < nblk) load_step(ib + 2, sb);
+    compute_step(sa);
+    if (ib + 2 >= nblk) break;
+    if (ib + 4 < nblk) load_step(ib + 4, sa);
+    compute_step(sb);
   }
 
   lsum += shfl_xor_f(lsum, 16);
