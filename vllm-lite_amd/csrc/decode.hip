@@ -920,31 +920,37 @@ __device__ inline int seg_slots(int64_t start, int len, int64_t total, int nw) {
 }
 
 // Common prefix of each group's tables, in full units (the shared part of
-// BalanceLayout): one wavefront per group.
-__global__ __launch_bounds__(64) void decode_lcp_kernel(
+// BalanceLayout): one workgroup of kLcpThreads per group.  Every table entry
+// a member may share (below the row length, before the group's limit is
+// known) is loaded and compared at once, so the launch costs one round trip
+// for the context lengths and tables together; the first differing block
+// is the workgroup's minimum.
+constexpr int kLcpThreads = 1024;
+__global__ __launch_bounds__(kLcpThreads) void decode_lcp_kernel(
     const int32_t* __restrict__ block_tables, int mbs, const int32_t* __restrict__ context_lens,
     int B, int SP, int cap, int32_t* __restrict__ lcp) {
-  const int g = blockIdx.x, lane = threadIdx.x;
+  __shared__ int first_diff;
+  const int g = blockIdx.x, tid = threadIdx.x;
   const int g0 = g * SP, gn = min(SP, B - g0);
+  if (tid == 0) first_diff = INT32_MAX;
   int L = INT32_MAX;
   for (int m = 0; m < gn; ++m)
     L = min(L, min(min(context_lens[g0 + m], mbs * kBlock), cap) / (2 * kBlock));
   if (gn < 2) L = 0;
-  // the first block, below 2 L, where a member's table differs from the first's
-  for (int b0 = 0; b0 < 2 * L; b0 += 64) {
-    const int b = b0 + lane;
-    bool diff = false;
-    if (b < 2 * L) {
-      const int32_t id = block_tables[(int64_t)g0 * mbs + b];
-      for (int m = 1; m < gn; ++m) diff |= block_tables[(int64_t)(g0 + m) * mbs + b] != id;
-    }
-    const uint64_t bal = __builtin_amdgcn_ballot_w64(diff);
-    if (bal) {
-      L = min(L, (b0 + (int)__builtin_ctzll(bal)) / 2);
-      break;
-    }
+  // blocks below 2 L where a member's table differs from the first's (the
+  // loads do not wait for L: every index below mbs is inside the tables)
+  int diff = INT32_MAX;
+  for (int b = tid; b < mbs; b += kLcpThreads) {
+    const int32_t id = block_tables[(int64_t)g0 * mbs + b];
+    bool d = false;
+    for (int m = 1; m < gn; ++m) d |= block_tables[(int64_t)(g0 + m) * mbs + b] != id;
+    if (d && b < 2 * L) diff = min(diff, b);
   }
-  if (lane == 0) lcp[g] = L;
+  __syncthreads();
+  for (int o = 32; o > 0; o >>= 1) diff = min(diff, __shfl_xor(diff, o, 64));
+  if ((tid & 63) == 0 && diff != INT32_MAX) atomicMin(&first_diff, diff);
+  __syncthreads();
+  if (tid == 0) lcp[g] = min(L, first_diff / 2);
 }
 
 // One segment piece: kv head kvh, units [u0, u1) of the segment.  Shared
@@ -1205,11 +1211,12 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
 
 // ---------------------------------------------------------------------------
 // Partition merge: one workgroup of 256 threads per (sequence, query head).
-// The partitions' (m, l) are reduced over the workgroup to M and L; thread
-// t then accumulates output dims of lane t % 64 over the partitions
-// p = t / 64, t / 64 + 4, ... (loads of four partitions in flight per
-// step), and the four partial sums are added through LDS.
-template <typename T>
+// Wavefront w merges the partitions w, w + 4, ... in chunks of kRU whose
+// (m, l) pairs and output dims are loaded together (one round trip per
+// chunk), keeping a running max; the four wavefronts' (M, L, o) are then
+// merged through LDS with the same log-sum-exp rule.  Lane t holds dims
+// t, t + 64, ... (head_dim <= 64 * kDL).
+template <typename T, int kDL>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(
     T* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ context_lens, int Hq, int D, int num_parts, int mbs,
@@ -1218,9 +1225,8 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
   // balance_nw > 0: partial results of decode_balanced_kernel launched with
   // balance_nw wavefronts (num_parts = slots per row; lcp, SP its layout);
   // else partitions of part_len tokens.
-  __shared__ float wsh[1024];
-  __shared__ float red[4][512];
-  __shared__ float ml[2][4];
+  __shared__ float red[4][64 * kDL];
+  __shared__ float wml[2][4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int row = blockIdx.x;  // seq * Hq + head
   const int seq = row / Hq;
@@ -1245,69 +1251,63 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
                num_parts);
     }
   } else {
-    np = min(min(num_parts, (ctx + part_len - 1) / part_len), 1024);
+    np = min(num_parts, (ctx + part_len - 1) / part_len);
   }
   const int64_t row0 = (int64_t)row * num_parts;
-  // Wavefront w sums the partitions w, w + 4, ... of dims lane and lane + 64
-  // (head_dim <= 128: the common case, in chunks of kRU partitions whose
-  // loads are all in flight together; the first chunk is loaded before the
-  // max / sum pass so the two round trips overlap).
   constexpr int kRU = 8;
-  const bool two = D <= 128;
-  float v0[kRU], v1[kRU];
-  auto load_chunk = [&](int p0) {
+  float M = -INFINITY, L = 0.f, acc[kDL];
+#pragma unroll
+  for (int k = 0; k < kDL; ++k) acc[k] = 0.f;
+  for (int p0 = wave; p0 < np; p0 += 4 * kRU) {
+    float2 ml[kRU];
+    float v[kRU][kDL];
 #pragma unroll
     for (int u = 0; u < kRU; ++u) {
-      const int p = p0 + 4 * u;
-      const float* src = ws_o + (row0 + min(p, np - 1)) * D;
-      v0[u] = lane < D ? src[lane] : 0.f;
-      v1[u] = lane + 64 < D ? src[lane + 64] : 0.f;
-    }
-  };
-  if (two && np > 0) load_chunk(wave);
-  float M = -INFINITY;
-  for (int p = tid; p < np; p += 256) M = fmaxf(M, ws_ml[2 * (row0 + p)]);
-  for (int w = 32; w > 0; w >>= 1) M = fmaxf(M, __shfl_xor(M, w, 64));
-  if (lane == 0) ml[0][wave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(ml[0][0], ml[0][1]), fmaxf(ml[0][2], ml[0][3]));
-  float L = 0.f;
-  for (int p = tid; p < np; p += 256) {
-    const float w = exp2f(ws_ml[2 * (row0 + p)] - M);
-    wsh[p] = w;
-    L += w * ws_ml[2 * (row0 + p) + 1];
-  }
-  for (int w = 32; w > 0; w >>= 1) L += __shfl_xor(L, w, 64);
-  if (lane == 0) ml[1][wave] = L;
-  __syncthreads();
-  L = ml[1][0] + ml[1][1] + ml[1][2] + ml[1][3];
-  const float inv = L != 0.f ? 1.f / L : 0.f;
-  if (two) {
-    float a0 = 0.f, a1 = 0.f;
-    for (int p0 = wave; p0 < np; p0 += 4 * kRU) {
-      if (p0 != wave) load_chunk(p0);
+      const int64_t p = row0 + min(p0 + 4 * u, np - 1);
+      ml[u] = float2{ws_ml[2 * p], ws_ml[2 * p + 1]};
 #pragma unroll
-      for (int u = 0; u < kRU; ++u) {
-        const int p = p0 + 4 * u;
-        if (p < np) {
-          a0 += wsh[p] * v0[u];
-          a1 += wsh[p] * v1[u];
-        }
+      for (int k = 0; k < kDL; ++k) v[u][k] = lane + 64 * k < D ? ws_o[p * D + lane + 64 * k] : 0.f;
+    }
+    float cm = M;
+#pragma unroll
+    for (int u = 0; u < kRU; ++u)
+      if (p0 + 4 * u < np) cm = fmaxf(cm, ml[u].x);
+    if (cm == -INFINITY) continue;  // no keys so far
+    const float r = exp2f(M - cm);  // 0 while M is -inf
+    L *= r;
+#pragma unroll
+    for (int k = 0; k < kDL; ++k) acc[k] *= r;
+#pragma unroll
+    for (int u = 0; u < kRU; ++u) {
+      if (p0 + 4 * u < np) {
+        const float w = exp2f(ml[u].x - cm);
+        L += w * ml[u].y;
+#pragma unroll
+        for (int k = 0; k < kDL; ++k) acc[k] += w * v[u][k];
       }
     }
-    if (lane < D) red[wave][lane] = a0;
-    if (lane + 64 < D) red[wave][lane + 64] = a1;
-  } else {
-    for (int d = lane; d < D; d += 64) {
-      float acc = 0.f;
-      for (int p = wave; p < np; p += 4) acc += wsh[p] * ws_o[(row0 + p) * D + d];
-      red[wave][d] = acc;
-    }
+    M = cm;
+  }
+#pragma unroll
+  for (int k = 0; k < kDL; ++k)
+    if (lane + 64 * k < D) red[wave][lane + 64 * k] = acc[k];
+  if (lane == 0) {
+    wml[0][wave] = M;
+    wml[1][wave] = L;
   }
   __syncthreads();
+  const float Mx = fmaxf(fmaxf(wml[0][0], wml[0][1]), fmaxf(wml[0][2], wml[0][3]));
+  float sc[4], Lt = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    sc[w] = wml[0][w] == -INFINITY ? 0.f : exp2f(wml[0][w] - Mx);
+    Lt += sc[w] * wml[1][w];
+  }
+  const float inv = Lt != 0.f ? 1.f / Lt : 0.f;
   for (int d = tid; d < D; d += 256)
     Elem<T>::store(out + (int64_t)row * D + d,
-                   (red[0][d] + red[1][d] + red[2][d] + red[3][d]) * inv);
+                   (sc[0] * red[0][d] + sc[1] * red[1][d] + sc[2] * red[2][d] +
+                    sc[3] * red[3][d]) * inv);
 }
 
 int num_partitions(int max_ctx, int part_len) {
@@ -1457,7 +1457,7 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   if (plan.balanced) {
     if (sp > 1) {
       lcp = (int32_t*)(ws_ml + (size_t)num_seqs * num_heads * np * 2);
-      decode_lcp_kernel<<<(num_seqs + sp - 1) / sp, 64, 0, s>>>(
+      decode_lcp_kernel<<<(num_seqs + sp - 1) / sp, kLcpThreads, 0, s>>>(
           block_tables, max_blocks_per_seq, context_lens, num_seqs, sp, max_context_len, lcp);
     }
 #define PA_LAUNCH_BALANCED(DD)                                                                \
@@ -1542,18 +1542,23 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   if (rc != PA_OK || np == 1 || merge_waves > 1) return rc;
   const dim3 rgrid(num_seqs * num_heads);
   const int bal = plan.balanced ? kBalanceWaves : 0;
-  if (dtype == PA_DTYPE_BF16 || fp8)
-    decode_reduce_kernel<uint16_t><<<rgrid, 256, 0, s>>>((uint16_t*)out, ws_o, ws_ml,
-                                                         context_lens, num_heads, head_dim, np,
-                                                         max_blocks_per_seq, part_len, bal,
-                                                         num_seqs, num_kv_heads, lcp, sp,
-                                                         max_context_len);
-  else
-    decode_reduce_kernel<float><<<rgrid, 256, 0, s>>>((float*)out, ws_o, ws_ml, context_lens,
-                                                      num_heads, head_dim, np,
-                                                      max_blocks_per_seq, part_len, bal,
-                                                      num_seqs, num_kv_heads, lcp, sp,
-                                                      max_context_len);
+#define PA_LAUNCH_REDUCE(TT, DL)                                                              \
+  decode_reduce_kernel<TT, DL><<<rgrid, 256, 0, s>>>(                                         \
+      (TT*)out, ws_o, ws_ml, context_lens, num_heads, head_dim, np, max_blocks_per_seq,       \
+      part_len, bal, num_seqs, num_kv_heads, lcp, sp, max_context_len)
+  const bool wide = head_dim > 128;
+  if (dtype == PA_DTYPE_BF16 || fp8) {
+    if (wide)
+      PA_LAUNCH_REDUCE(uint16_t, 8);
+    else
+      PA_LAUNCH_REDUCE(uint16_t, 2);
+  } else {
+    if (wide)
+      PA_LAUNCH_REDUCE(float, 8);
+    else
+      PA_LAUNCH_REDUCE(float, 2);
+  }
+#undef PA_LAUNCH_REDUCE
   return check_launch("pa_decode reduce");
 }
 }  // namespace
