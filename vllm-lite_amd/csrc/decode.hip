@@ -352,80 +352,61 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 //  * P·V: reduction slot 8 j + i is token 8 (j & 1) + i of block j >> 1, so
 //    the Vᵀ operand of dims 16 dt + c is one 8-byte load from the
 //    token-minor block.
-template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
-    const uint8_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
-    const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
-    float scale_log2, int num_parts, int part_len, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, int64_t q_row) {
-  constexpr int KS = D / 32;  // QK reduction steps
-  constexpr int DT = D / 16;  // PV output tiles
-  constexpr int DL = D / 4;   // dims (bytes) of a K row per lane group
-  // NW > 1: the workgroup's wavefronts take partitions blockIdx.x * NW + w
-  // (the launch uses it only when one workgroup holds all of them) and merge
-  // them in LDS; NW = 1: one partition, merged by decode_reduce_kernel.
-  const int lane = threadIdx.x & 63;
-  const int c = lane & 15, j = lane >> 4;
-  const int part = blockIdx.x * NW + (NW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0);
-  const int kvh = blockIdx.y, seq = blockIdx.z;
-  const int ctx = min(context_lens[seq], mbs * kBlock);
-  const int tok0 = part * part_len;
-  const bool empty = tok0 >= ctx;
-  if (NW == 1 && empty) {
-    if (num_parts == 1 && c < G) {
-      uint16_t* orow = out + ((int64_t)seq * Hq + kvh * G + c) * D;
-      for (int d = 4 * j; d < D; d += 16) *reinterpret_cast<uint64_t*>(orow + d) = 0;
-    }
-    return;
-  }
-  const int tok_end = empty ? tok0 : min(ctx, tok0 + part_len);
-  const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;  // 0 for an empty partition
+// One partition of decode_fp8_kernel: where its blocks are, how a step (two
+// blocks) is loaded and how it enters the online softmax.  Shared by the
+// kernel's streaming loop and by fp8_exact_pass.
+template <int D>
+struct Fp8Partition {
+  static constexpr int KS = D / 32;  // QK reduction steps
+  static constexpr int DT = D / 16;  // PV output tiles
+  static constexpr int DL = D / 4;   // dims (bytes) of a K row per lane group
+  const uint8_t* kc;
+  const uint8_t* vc;
+  const int32_t* btab;  // the partition's first block-table entry
+  int Hkv, kvh, num_blocks, tok0, tok_end, nblk, c, j;
+  float scale_log2;
 
-  const int head = kvh * G + c;
-  bf16x8 qv[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    if (c < G)
-      qv[s] = *reinterpret_cast<const bf16x8*>(q + (int64_t)seq * q_row + (int64_t)head * D + DL * j + 8 * s);
-    else
-      qv[s] = bf16x8{};
-  }
-
-  f32x4 o[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = kNegBig, lsum = 0.f;
-
-  const int32_t* btab = block_tables + (int64_t)seq * mbs + tok0 / kBlock;
-  const int64_t head_stride = (int64_t)kBlock * D;  // bytes per (block, head)
-  const bool k_second = (c >> 3) != 0;              // this lane's K rows are in block 1
-  const int tk0 = 8 * ((c >> 2) & 1) + (c & 3);
-  const bool v_second = (j >> 1) != 0;              // this lane's P·V tokens are in block 1
-  const int tv0 = 8 * (j & 1);
-
+  // The online-softmax state of a lane.
+  struct State {
+    f32x4 o[DT];
+    float m, lsum;
+  };
   // One step = two blocks; its raw K/V bytes and the blocks' valid lengths.
-  // Steps are software-pipelined two deep (the bytes of step n + 1 are
-  // requested before step n is computed): an FP8 step moves half the bytes of
-  // a bf16 step, so one step in flight per wavefront would leave HBM
-  // latency-bound.
   struct Step {
     u32x4 k0[KS / 2], k1[KS / 2];  // 16 bytes = two reduction steps, token tk0 / tk0 + 4
     uint64_t v[DT];
     int lim0, lim1;
   };
+
+  __device__ void init(State& s) const {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) s.o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s.m = kNegBig;
+    s.lsum = 0.f;
+  }
   // Block ids through the scalar cache with a wait on the scalar counter only.
-  // (Written out because the register-only asm below keeps the compiler from
-  // proving the table unmodified; it would then read it with vector loads,
-  // each followed by vmcnt(0), draining the K/V loads in flight.)
-  auto table_id = [&](int idx) -> int32_t {
+  // (Written out because the register-only asm elsewhere keeps the compiler
+  // from proving the table unmodified; it would then read it with vector
+  // loads, each followed by vmcnt(0), draining the K/V loads in flight.)
+  // (Both operands are wavefront-uniform; the lane reads make that visible
+  // where they arrive in vector registers, as in fp8_exact_pass.)
+  __device__ int32_t table_id(int idx) const {
+    const uint64_t bt = (uint64_t)(uintptr_t)btab;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)bt);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(bt >> 32));
+    const int32_t* tab = (const int32_t*)(((uint64_t)hi << 32) | lo);
     int32_t v;
     asm volatile("s_load_dword %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
                  : "=s"(v)
-                 : "s"(btab), "s"(idx * 4));
+                 : "s"(tab), "s"(__builtin_amdgcn_readfirstlane(idx * 4)));
     return v;
-  };
-  auto load_step = [&](int ib, Step& st) {
+  }
+  __device__ void load_step(int ib, Step& st) const {
+    const int64_t head_stride = (int64_t)kBlock * D;  // bytes per (block, head)
+    const bool k_second = (c >> 3) != 0;              // this lane's K rows are in block 1
+    const int tk0 = 8 * ((c >> 2) & 1) + (c & 3);
+    const bool v_second = (j >> 1) != 0;              // this lane's P·V tokens are in block 1
+    const int tv0 = 8 * (j & 1);
     int32_t b0 = table_id(ib);
     const bool has1 = ib + 1 < nblk;
     int32_t b1 = table_id(has1 ? ib + 1 : ib);
@@ -449,12 +430,14 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
       st.v[dt] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(vr + dt * 16 * kBlock));
-  };
-  auto compute_step = [&](Step& st, auto exact_c) {
-    constexpr bool EXACT = decltype(exact_c)::value;
+  }
+  template <bool EXACT>
+  __device__ void compute_step(Step& st, const bf16x8 (&qv)[KS], State& S) const {
     auto cvt = [](uint32_t lo, uint32_t hi) {
       return EXACT ? fp8x8_to_bf16_exact(lo, hi) : fp8x8_to_bf16(lo, hi);
     };
+    const bool v_second = (j >> 1) != 0;
+    const int tv0 = 8 * (j & 1);
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -486,38 +469,117 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
 
     float bm = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
                      fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-    if (__builtin_amdgcn_ballot_w64(bm > m + 8.0f)) {
+    if (__builtin_amdgcn_ballot_w64(bm > S.m + 8.0f)) {
       bm = fmaxf(bm, shfl_xor_f(bm, 16));
       bm = fmaxf(bm, shfl_xor_f(bm, 32));
-      const float mn = fmaxf(m, bm);
-      const float a = fast_exp2(m - mn);
-      m = mn;
-      lsum *= a;
+      const float mn = fmaxf(S.m, bm);
+      const float a = fast_exp2(S.m - mn);
+      S.m = mn;
+      S.lsum *= a;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt] *= a;
+      for (int dt = 0; dt < DT; ++dt) S.o[dt] *= a;
     }
     float p[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      p[i] = fast_exp2(x[i] - m);
-      lsum += p[i];
+      p[i] = fast_exp2(x[i] - S.m);
+      S.lsum += p[i];
     }
     bf16x8 pb;
 #pragma unroll
     for (int i = 0; i < 8; ++i) pb[i] = (__bf16)p[i];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          cvt((uint32_t)st.v[dt], (uint32_t)(st.v[dt] >> 32)), pb, o[dt], 0, 0, 0);
-  };
+      S.o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          cvt((uint32_t)st.v[dt], (uint32_t)(st.v[dt] >> 32)), pb, S.o[dt], 0, 0, 0);
+  }
+};
+
+// The partition once more with the reference's exact decode of every code,
+// for the rare wavefront whose streaming pass met a code the hardware
+// conversion reads differently.  A call, not inlined: its registers are its
+// own, so the streaming loop keeps the budget of four wavefronts per SIMD
+// (the values live across the call are saved to scratch, once).
+template <int D>
+__device__ __attribute__((noinline)) typename Fp8Partition<D>::State fp8_exact_pass(
+    const Fp8Partition<D> p, const uint16_t* qrow) {
+  constexpr int KS = Fp8Partition<D>::KS;
+  bf16x8 qv[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    qv[s] = qrow ? *reinterpret_cast<const bf16x8*>(qrow + Fp8Partition<D>::DL * p.j + 8 * s)
+                 : bf16x8{};
+  typename Fp8Partition<D>::State S;
+  p.init(S);
+  typename Fp8Partition<D>::Step st;
+  const int nblk = __builtin_amdgcn_readfirstlane(p.nblk);
+  for (int ib = 0; ib < nblk; ib += 2) {
+    p.load_step(ib, st);
+    p.template compute_step<true>(st, qv, S);
+  }
+  return S;
+}
+
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1))) void decode_fp8_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
+    const uint8_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
+    const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
+    float scale_log2, int num_parts, int part_len, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml, int64_t q_row) {
+  using Part = Fp8Partition<D>;
+  constexpr int KS = Part::KS;
+  constexpr int DT = Part::DT;
+  constexpr int DL = Part::DL;
+  // NW > 1: the workgroup's wavefronts take partitions blockIdx.x * NW + w
+  // (the launch uses it only when one workgroup holds all of them) and merge
+  // them in LDS; NW = 1: one partition, merged by decode_reduce_kernel.
+  const int lane = threadIdx.x & 63;
+  const int c = lane & 15, j = lane >> 4;
+  const int part = blockIdx.x * NW + (NW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0);
+  const int kvh = blockIdx.y, seq = blockIdx.z;
+  const int ctx = min(context_lens[seq], mbs * kBlock);
+  const int tok0 = part * part_len;
+  const bool empty = tok0 >= ctx;
+  if (NW == 1 && empty) {
+    if (num_parts == 1 && c < G) {
+      uint16_t* orow = out + ((int64_t)seq * Hq + kvh * G + c) * D;
+      for (int d = 4 * j; d < D; d += 16) *reinterpret_cast<uint64_t*>(orow + d) = 0;
+    }
+    return;
+  }
+  const int tok_end = empty ? tok0 : min(ctx, tok0 + part_len);
+  const Part P{kc, vc, block_tables + (int64_t)seq * mbs + tok0 / kBlock, Hkv, kvh, num_blocks,
+               tok0, tok_end, (tok_end - tok0 + kBlock - 1) / kBlock /* 0 when empty */, c, j,
+               scale_log2};
+
+  const int head = kvh * G + c;
+  const uint16_t* qrow = c < G ? q + (int64_t)seq * q_row + (int64_t)head * D : nullptr;
+  bf16x8 qv[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    qv[s] = qrow ? *reinterpret_cast<const bf16x8*>(qrow + DL * j + 8 * s) : bf16x8{};
+  typename Part::State S;
+  P.init(S);
+
   // Codes the hardware conversion reads differently from the reference
   // (NaN / inf / off-OCP codes; never produced from finite input) are
   // tracked per lane while the partition streams; a wavefront that met any
-  // recomputes its partition with the exact integer decode (rare, and kept
-  // out of the streaming loop so that loop's registers and code stay those
-  // of the plain conversion).
+  // streams its partition again with the exact integer decode
+  // (fp8_exact_pass: rare, and a call, so that this loop's registers stay
+  // those of the plain conversion).
   uint32_t exotic = 0;
-  auto compute = [&](Step& st) {
+  // The q loads complete here, once: a wait for them that the compiler placed
+  // inside the loop would be vmcnt(0) on every iteration and drain the
+  // loads in flight.
+#pragma unroll
+  for (int s = 0; s < KS; ++s) asm volatile("" ::"v"(qv[s]));
+  // One step in flight per wavefront and four wavefronts per SIMD (the
+  // launch's partitions fill them): two steps in flight at two wavefronts
+  // per SIMD measured slower, their extra VALU work less hidden.
+  typename Part::Step st;
+  for (int ib = 0; ib < P.nblk; ib += 2) {
+    P.load_step(ib, st);
 #pragma unroll
     for (int s = 0; s < KS / 2; ++s)
 #pragma unroll
@@ -526,39 +588,15 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
       exotic |= fp8_exotic_bits((uint32_t)st.v[dt]) | fp8_exotic_bits((uint32_t)(st.v[dt] >> 32));
-    compute_step(st, std::false_type{});
-  };
-
-  // The q loads complete here, once: a wait for them that the compiler placed
-  // inside the loop would be vmcnt(0) on every iteration and drain the
-  // pipeline.
-#pragma unroll
-  for (int s = 0; s < KS; ++s) asm volatile("" ::"v"(qv[s]));
-  Step sa, sb;
-  if (nblk > 0) load_step(0, sa);
-  for (int ib = 0; ib < nblk; ib += 4) {
-    if (ib + 2 < nblk) load_step(ib + 2, sb);
-    compute(sa);
-    if (ib + 2 >= nblk) break;
-    if (ib + 4 < nblk) load_step(ib + 4, sa);
-    compute(sb);
+    P.template compute_step<false>(st, qv, S);
   }
-  if (__builtin_amdgcn_ballot_w64((exotic & 0x80808080u) != 0)) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m = kNegBig;
-    lsum = 0.f;
-#pragma unroll 1
-    for (int ib = 0; ib < nblk; ib += 2) {
-      load_step(ib, sa);
-      compute_step(sa, std::true_type{});
-    }
-  }
+  if (__builtin_amdgcn_ballot_w64((exotic & 0x80808080u) != 0)) S = fp8_exact_pass<D>(P, qrow);
 
+  float lsum = S.lsum;
   lsum += shfl_xor_f(lsum, 16);
   lsum += shfl_xor_f(lsum, 32);
   if constexpr (NW > 1) {
-    merge_in_workgroup<D, NW>(out + ((int64_t)seq * Hq + kvh * G) * D, o, m, lsum, c, j, G);
+    merge_in_workgroup<D, NW>(out + ((int64_t)seq * Hq + kvh * G) * D, S.o, S.m, lsum, c, j, G);
     return;
   }
   if (c >= G) return;
@@ -569,16 +607,16 @@ __global__ __launch_bounds__(64 * NW) void decode_fp8_kernel(
     for (int dt = 0; dt < DT; ++dt) {
       uint16_t w[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) w[r] = f32_to_bf16_bits(o[dt][r] * inv);
+      for (int r = 0; r < 4; ++r) w[r] = f32_to_bf16_bits(S.o[dt][r] * inv);
       *reinterpret_cast<uint64_t*>(orow + 16 * dt) = *reinterpret_cast<const uint64_t*>(w);
     }
   } else {
     const int64_t row = ((int64_t)seq * Hq + head) * num_parts + part;
     float* orow = ws_o + row * D + 4 * j;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(orow + 16 * dt) = o[dt];
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(orow + 16 * dt) = S.o[dt];
     if (j == 0) {
-      ws_ml[2 * row] = m;
+      ws_ml[2 * row] = S.m;
       ws_ml[2 * row + 1] = lsum;
     }
   }
@@ -1080,7 +1118,7 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
     for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = kNegBig, lsum = 0.f;
     const int32_t* btab = block_tables + (int64_t)pc.seq * mbs + tok0 / kBlock;
-    // Steps software-pipelined two deep for D <= 128, as decode_fp8_kernel:
+    // Steps software-pipelined two deep for D <= 128, as decode_mfma_kernel:
     // the loads are unconditional non-temporal loads and the block ids come
     // through explicit scalar loads, so the compiler's wait counts stay
     // exact.
@@ -1326,12 +1364,11 @@ int num_partitions(int max_ctx, int part_len) {
 int choose_partition(int num_seqs, int num_kv_heads, int max_ctx, int head_dim, int elem_bytes) {
   const long long units = (long long)num_seqs * num_kv_heads;
   auto items = [&](int p) { return units * ((max_ctx + p - 1) / p); };
-  // 1024 tokens: the config-2 shape then has 2048 wavefronts (four partitions
-  // merged per workgroup); measured bf16 159.6-159.9 us against 160.4-160.8
-  // at 2048 tokens, FP8 84.7 against 91.2 us (a streaming probe: 5.7 TB/s
-  // with 1024 wavefronts, 6.75 with 2048)
-  const int long_part = 1024;
-  (void)elem_bytes;
+  // bf16, 1024 tokens: the config-2 shape then has 2048 wavefronts (four
+  // partitions merged per workgroup); measured 159.6-159.9 us against
+  // 160.4-160.8 at 2048 tokens.  FP8 (four wavefronts per SIMD, one step in
+  // flight each), 512 tokens: 4096 wavefronts, every one resident at once.
+  const int long_part = elem_bytes == 1 ? 512 : 1024;
   if (max_ctx <= 8192 && items(long_part) >= 1024) return long_part;
   if (items(512) >= 1024) return 512;
   if (items(kPart) < 512 && max_ctx <= 1024 && head_dim <= 128) return kPart / 2;
