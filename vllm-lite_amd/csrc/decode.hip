@@ -1367,8 +1367,10 @@ int choose_partition(int num_seqs, int num_kv_heads, int max_ctx, int head_dim, 
   // bf16, 1024 tokens: the config-2 shape then has 2048 wavefronts (four
   // partitions merged per workgroup); measured 159.6-159.9 us against
   // 160.4-160.8 at 2048 tokens.  FP8 (four wavefronts per SIMD, one step in
-  // flight each), 512 tokens: 4096 wavefronts, every one resident at once.
-  const int long_part = elem_bytes == 1 ? 512 : 1024;
+  // flight each), 512 tokens: 4096 wavefronts, every one resident at once;
+  // past 4096 tokens 1024, so that one workgroup still merges a sequence's
+  // partitions (eight at most) and no reduce launch is needed.
+  const int long_part = elem_bytes == 1 && max_ctx <= 4096 ? 512 : 1024;
   if (max_ctx <= 8192 && items(long_part) >= 1024) return long_part;
   if (items(512) >= 1024) return 512;
   if (items(kPart) < 512 && max_ctx <= 1024 && head_dim <= 128) return kPart / 2;
