@@ -46,12 +46,13 @@ def test_version_and_empty_error(lib):
 
 
 def test_workspace_size(lib):
-    # one partition (<= 256 tokens) needs none; otherwise B*Hq*(P+2)*(D+2) f32
-    # with P = ceil(ctx / 256) (a balanced launch writes up to P + 2 partial
+    # one partition (<= 128 tokens) needs none; otherwise B*Hq*(P+2)*(D+2)
+    # f32 with P = ceil(ctx / 128) (the f32 group kernel's shortest
+    # partitions; a balanced launch writes up to ceil(ctx / 256) + 2 partial
     # results per row) and one int per sequence
-    assert lib.pa_decode_workspace_size(64, 32, 128, 256) == 0
-    assert lib.pa_decode_workspace_size(64, 32, 128, 4096) == 64 * 32 * 18 * 130 * 4 + 64 * 4
-    assert lib.pa_decode_workspace_size(2, 4, 64, 257) == 2 * 4 * 4 * 66 * 4 + 2 * 4
+    assert lib.pa_decode_workspace_size(64, 32, 128, 128) == 0
+    assert lib.pa_decode_workspace_size(64, 32, 128, 4096) == 64 * 32 * 34 * 130 * 4 + 64 * 4
+    assert lib.pa_decode_workspace_size(2, 4, 64, 257) == 2 * 4 * 5 * 66 * 4 + 2 * 4
 
 
 def test_argument_errors_without_gpu(lib):

@@ -52,6 +52,19 @@ def test_config1_qwen_f32(pa, oracle):
     assert_close(got, ref, F32_ATOL, F32_RTOL, "config 1")
 
 
+@pytest.mark.parametrize("b,hq,hkv,d", [(16, 32, 8, 128), (2, 16, 1, 64), (3, 8, 4, 32)])
+def test_f32_group_partition_lengths(pa, oracle, b, hq, hkv, d):
+    # The f32 group kernel takes 128-token partitions when 256-token ones
+    # give fewer workgroups than CUs and the group has at most 8 heads:
+    # B 16 x 8 kv heads x 4 partitions = 512 workgroups (256 tokens); a group
+    # of 16 heads (256 tokens); 3 x 4 x up to 8 (128 tokens).
+    rng = np.random.default_rng(b * 100 + hq)
+    ctx = rng.integers(600, 1025, size=b)
+    case = make_decode_case(rng, b, hq, hkv, d, ctx, dtype="f32")
+    got, ref = run_decode(pa, oracle, case, "f32")
+    assert_close(got, ref, F32_ATOL, F32_RTOL, f"f32 group {b}x{hq}/{hkv}x{d}")
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (14, 2, 64), (8, 8, 128), (16, 2, 256),
                                       (8, 4, 64), (16, 1, 128)])
 def test_bf16_mfma_shapes(pa, oracle, hq, hkv, d):

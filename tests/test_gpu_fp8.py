@@ -229,7 +229,7 @@ def plant_codes(rng, kc, vc, bt, ctx, hkv, d):
         vc[blk, :, n % 16:, 1] = 0x7C
 
 
-@pytest.mark.parametrize("B,ctx_hi", [(7, 3000), (64, 2048)])
+@pytest.mark.parametrize("B,ctx_hi", [(7, 3000), (64, 2048), (24, 6000)])
 def test_decode_fp8_special_codes(pa, oracle, B, ctx_hi):
     # The reference decodes 0x80 as NaN and 0x7C / 0xFC as +-inf, and
     # 0x01-0x07 / 0x7F as finite values the OCP conversion reads otherwise
@@ -237,7 +237,9 @@ def test_decode_fp8_special_codes(pa, oracle, B, ctx_hi):
     # oracle's attention over the reference-decoded caches: NaN / inf where
     # it has them, the finite entries within the bf16 bar, codes past the
     # context ignored.  B 7: partitions merged by the reduce kernel; B 64:
-    # merged inside the workgroup.
+    # 512-token partitions merged inside the workgroup; B 24 past 4096
+    # tokens: 1024-token partitions merged inside the workgroup.  Any
+    # wavefront that meets such a code runs the out-of-line exact pass.
     rng = np.random.default_rng(B)
     hq, hkv, d = 32, 8, 128
     ctx = rng.integers(ctx_hi // 2, ctx_hi + 1, B).astype(np.int32)

@@ -717,7 +717,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
 
 // ---------------------------------------------------------------------------
 // f32 caches (plain, or int8-in-f32 with one scale per block): one workgroup
-// of 1024 threads per (partition of kPart tokens, kv head, sequence) serving
+// of 4 PL threads per (partition of PL tokens, kv head, sequence) serving
 // all G query heads of the group, so each K / V byte is read once for the
 // group.  Small decode batches are latency-bound, so the work of a thread
 // is kept short and every load is issued at the start:
@@ -725,25 +725,32 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(
 //        four read one contiguous row), partial dot products with the G
 //        query rows (LDS) combined by two lane shuffles.
 //   softmax: one wavefront per query head, over the partition.
-//   PV:  lane (d, r) owns dim d of the blocks r, r + R, ... (R = 1024 / D);
+//   PV:  lane (d, r) owns dim d of the blocks r, r + R, ... (R = 4 PL / D);
 //        the R lanes of one dim are adjacent, so their partial sums are
 //        combined by lane shuffles.
 // Partial results use the split-K workspace format of decode_reduce_kernel.
 constexpr int kF32MaxG = 16;
-template <int D>
-__global__ __launch_bounds__(1024) void decode_f32_group_kernel(
+// PL = 256, or 128 for launches of few (kv head, sequence) pairs: a CU
+// reads its workgroup's K / V at a bounded rate (what it keeps in flight
+// over the memory latency), so small launches finish sooner spread over
+// twice the workgroups (query groups of at most 8 heads: one wavefront
+// each in the softmax).
+template <int D, int PL>
+__global__ __launch_bounds__(4 * PL) void decode_f32_group_kernel(
     float* __restrict__ out, const float* __restrict__ q, const float* __restrict__ kc,
     const float* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int num_blocks,
     float scale_log2, int num_parts, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     const float* __restrict__ kv_scales, int64_t q_row) {
   static_assert(256 % D == 0 && D % 16 == 0, "head_dim must divide 256, in 16-float steps");
-  constexpr int NPB = kPart / kBlock;        // blocks per partition
-  constexpr int R = 1024 / D;                // lanes per dim in P·V (a power of two <= 64)
+  constexpr int NTH = 4 * PL;                // threads
+  constexpr int NPB = PL / kBlock;           // blocks per partition
+  constexpr int R = NTH / D;                 // lanes per dim in P·V (a power of two <= 64)
+  static_assert(R >= 1 && R <= 64, "lanes per dim");
   constexpr int NBT = NPB >= R ? NPB / R : 1;  // blocks per lane in P·V
   constexpr int KQ = D / 16;                 // float4 per lane of a K row quarter
   __shared__ __attribute__((aligned(16))) float qs[kF32MaxG * D];
-  __shared__ __attribute__((aligned(16))) float ps[kF32MaxG][kPart];
+  __shared__ __attribute__((aligned(16))) float ps[kF32MaxG][PL];
   __shared__ int32_t bs[NPB];
   __shared__ float bsc[NPB];
   __shared__ float mls[kF32MaxG][2];
@@ -752,18 +759,18 @@ __global__ __launch_bounds__(1024) void decode_f32_group_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // The block ids and the query rows are loaded in the same round trip as
   // the context length (they depend only on the partition's position).
-  const int tok0 = part * kPart;
+  const int tok0 = part * PL;
   const int bi0 = tok0 / kBlock;
   int32_t braw = -1;
   if (tid < NPB && bi0 + tid < mbs) braw = block_tables[(int64_t)seq * mbs + bi0 + tid];
-  for (int e = tid; e < G * D; e += 1024) qs[e] = q[(int64_t)seq * q_row + (int64_t)kvh * G * D + e];
+  for (int e = tid; e < G * D; e += NTH) qs[e] = q[(int64_t)seq * q_row + (int64_t)kvh * G * D + e];
   const int ctx = min(context_lens[seq], mbs * kBlock);
   if (tok0 >= ctx) {
     if (num_parts == 1)
-      for (int e = tid; e < G * D; e += 1024) out[((int64_t)seq * Hq + kvh * G) * D + e] = 0.f;
+      for (int e = tid; e < G * D; e += NTH) out[((int64_t)seq * Hq + kvh * G) * D + e] = 0.f;
     return;
   }
-  const int n = min(ctx - tok0, kPart);
+  const int n = min(ctx - tok0, PL);
   const int nb = (n + kBlock - 1) / kBlock;
   if (tid < NPB) {
     const bool ok = tid < nb && braw >= 0 && braw < num_blocks;
@@ -813,10 +820,10 @@ __global__ __launch_bounds__(1024) void decode_f32_group_kernel(
   // softmax over the partition, one wavefront per query head
   if (wave < G) {
     const int g = wave;
-    float v[kPart / 64];
+    float v[PL / 64];
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kPart / 64; ++i) {
+    for (int i = 0; i < PL / 64; ++i) {
       v[i] = ps[g][lane + 64 * i];
       mx = fmaxf(mx, v[i]);
     }
@@ -824,7 +831,7 @@ __global__ __launch_bounds__(1024) void decode_f32_group_kernel(
     const float m = mx == -INFINITY ? kNegBig : mx;
     float l = 0.f;
 #pragma unroll
-    for (int i = 0; i < kPart / 64; ++i) {
+    for (int i = 0; i < PL / 64; ++i) {
       const float p = exp2f(v[i] - m);
       ps[g][lane + 64 * i] = p;
       l += p;
@@ -1384,10 +1391,11 @@ using namespace pa;
 
 extern "C" size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t head_dim,
                                            int32_t max_context_len) {
-  // Sized for the shortest partition any launch uses, plus two: a balanced
-  // launch writes up to ceil(max_context_len / 256) + 2 partial results per
-  // row, and one int per sequence group.
-  const int np = num_partitions(max_context_len, kPart);
+  // Sized for the shortest partition any launch that needs a workspace uses
+  // (128 tokens, the f32 group kernel's for small launches), plus two: a
+  // balanced launch writes up to ceil(max_context_len / 256) + 2 partial
+  // results per row; and one int per sequence group.
+  const int np = num_partitions(max_context_len, kPart / 2);
   if (np <= 1 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
   return (size_t)num_seqs * num_heads * (np + 2) * (head_dim + 2) * sizeof(float) +
          (size_t)num_seqs * sizeof(int32_t);
@@ -1417,6 +1425,11 @@ DecodePlan decode_plan(int32_t dtype, bool quantized, int32_t num_seqs, int32_t 
   p.part_len = p.mfma ? choose_partition(num_seqs, num_kv_heads, max_context_len, head_dim,
                                          fp8 ? 1 : 2)
                       : kPart;
+  // f32 group kernel: 128-token partitions when 256-token ones give fewer
+  // workgroups than the GPU has CUs
+  if (p.f32_group && G <= 8 &&
+      (long long)num_seqs * num_kv_heads * num_partitions(max_context_len, kPart) < 256)
+    p.part_len = kPart / 2;
   p.np = num_partitions(max_context_len, p.part_len);
   // MFMA kernels: up to 4 partitions (8 for head_dim <= 128) are taken by one
   // workgroup (one wavefront each) and merged in LDS, with no workspace and no
@@ -1561,7 +1574,13 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
           block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, head_dim,
           num_blocks, scale_log2, np, ws_o, ws_ml, nullptr, q_row);
     else if (f32_group) {
-#define PA_LAUNCH_F32(DD)                                                                     decode_f32_group_kernel<DD><<<dim3(np, num_kv_heads, num_seqs), 1024, 0, s>>>(                   (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache,                  block_tables, max_blocks_per_seq, context_lens, num_heads, num_kv_heads, num_blocks,       scale_log2, np, ws_o, ws_ml, kv_scales, q_row)
+#define PA_LAUNCH_F32_PL(DD, PL)                                                              \
+  decode_f32_group_kernel<DD, PL><<<dim3(np, num_kv_heads, num_seqs), 4 * PL, 0, s>>>(        \
+      (float*)out, (const float*)q, (const float*)k_cache, (const float*)v_cache, block_tables, \
+      max_blocks_per_seq, context_lens, num_heads, num_kv_heads, num_blocks, scale_log2, np,  \
+      ws_o, ws_ml, kv_scales, q_row)
+#define PA_LAUNCH_F32(DD)                                                                     \
+  (part_len == kPart ? PA_LAUNCH_F32_PL(DD, kPart) : PA_LAUNCH_F32_PL(DD, kPart / 2))
       switch (head_dim) {
         case 16: PA_LAUNCH_F32(16); break;
         case 32: PA_LAUNCH_F32(32); break;
@@ -1570,6 +1589,7 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
         default: PA_LAUNCH_F32(256); break;
       }
 #undef PA_LAUNCH_F32
+#undef PA_LAUNCH_F32_PL
     }
     else
       decode_generic_kernel<float><<<grid, 256, 0, s>>>(
