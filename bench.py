@@ -256,21 +256,40 @@ def time_attend(w, iters):
     return start.elapsed_time(stop) / iters / 1e3  # seconds
 
 
-def time_attend_flushed(w, iters, flush_bytes=512 << 20):
+def time_attend_flushed(w, iters, flush_bytes=512 << 20, dirty=False):
     """Median duration of the dominant launch with the caches flushed before
-    each one: a 512 MiB scratch write (larger than L2 + MALL) runs between
-    launches, and HIP events bracket each launch on its own."""
-    scratch = torch.empty(flush_bytes // 4, dtype=torch.float32, device=DEV)
+    each one: 512 MiB (larger than L2 + MALL) of scratch is streamed between
+    launches, and HIP events bracket each launch on its own.  By default
+    the scratch is read (a sum), which leaves the caches full of clean lines
+    of other data: a cold start.  dirty=True writes it instead (a fill), so
+    the launch also runs while that much dirty data is being written back."""
+    scratch = torch.ones(flush_bytes // 4, dtype=torch.float32, device=DEV)
+    sink = torch.empty((), dtype=torch.float32, device=DEV)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(iters)]
     torch.cuda.synchronize()
     for a, b in ev:
-        scratch.fill_(1.0)
+        if dirty:
+            scratch.fill_(1.0)
+        else:
+            torch.sum(scratch, dim=0, out=sink)
         a.record()
         w.attend()
         b.record()
     torch.cuda.synchronize()
     return float(np.median([a.elapsed_time(b) for a, b in ev])) / 1e3
+
+
+def flushed_legs(roof, w, iters, frac_of, no_flush):
+    """Adds the cache-flushed timing legs to a roofline dict: read flush
+    (cold, clean caches) as flushed_launch_us / flushed_frac, write flush
+    (dirty lines draining meanwhile) as flushed_dirty_launch_us / _frac."""
+    if no_flush:
+        return
+    for key, dirty in (("flushed", False), ("flushed_dirty", True)):
+        t = time_attend_flushed(w, iters, dirty=dirty)
+        roof[key + "_launch_us"] = round(t * 1e6, 2)
+        roof[key + "_frac"] = round(frac_of(t), 4)
 
 
 def gemm_ceiling(n=8192, iters=10):
@@ -444,16 +463,14 @@ def run_write(pa, args):
     for _ in range(args.warmup):
         w.attend()
     tm = time_attend(w, max(args.steps, 20))
-    tf = None if args.no_flush else time_attend_flushed(w, max(args.steps, 20))
     alg = 2 * 2 * t * hkv * d * 2 + t * 8
     achieved = alg / tm / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
             "kernel": "pa_reshape_and_cache (cache_write_kernel, whole blocks)",
             "alg_bytes_per_launch": alg, "avg_launch_us": round(tm * 1e6, 2)}
-    if tf:
-        roof["flushed_launch_us"] = round(tf * 1e6, 2)
-        roof["flushed_frac"] = round(alg / tf / 1e9 / HBM_PEAK_GBS, 4)
+    flushed_legs(roof, w, max(args.steps, 20), lambda x: alg / x / 1e9 / HBM_PEAK_GBS,
+                 args.no_flush)
     print(json.dumps({
         "metric": "paged KV-cache write tokens/s (config 3 chunk)",
         "value": round(t / tm, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -502,7 +519,6 @@ def main():
     ms_per_step = el / args.steps * 1e3
 
     t_attn = time_attend(w, max(args.steps, 20))
-    t_flush = None if args.no_flush else time_attend_flushed(w, max(args.steps, 20))
     if w.kind == "decode":
         value = w.B * args.steps / el
         unit = "tokens/s"
@@ -513,9 +529,8 @@ def main():
                 "traffic": traffic, "traffic_source": traffic_src,
                 "alg_bytes_per_launch": w.alg_bytes,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
-        if t_flush:
-            roof["flushed_launch_us"] = round(t_flush * 1e6, 2)
-            roof["flushed_frac"] = round(w.alg_bytes / t_flush / 1e9 / HBM_PEAK_GBS, 4)
+        flushed_legs(roof, w, max(args.steps, 20),
+                     lambda x: w.alg_bytes / x / 1e9 / HBM_PEAK_GBS, args.no_flush)
         if args.config == "splitk":
             roof["unique_block_gbs"] = round((w.unique_kv_bytes) / t_attn / 1e9, 1)
             # the profiled HBM bytes (FETCH + WRITE) over this run's launch time
@@ -542,9 +557,8 @@ def main():
                 "kernel": ("pa_prefill (prefill_tiled_kernel, FP8 tiles)" if w.fp8 else
                            "pa_prefill (prefill_tiled_kernel)"), "flops_per_launch": w.flops,
                 "avg_launch_us": round(t_attn * 1e6, 2)}
-        if t_flush:
-            roof["flushed_launch_us"] = round(t_flush * 1e6, 2)
-            roof["flushed_frac"] = round(w.flops / t_flush / 1e12 / BF16_PEAK_TFLOPS, 4)
+        flushed_legs(roof, w, max(args.steps, 20),
+                     lambda x: w.flops / x / 1e12 / BF16_PEAK_TFLOPS, args.no_flush)
         if not args.no_flush:
             ceil = gemm_ceiling()
             roof["gemm_ceiling_tflops"] = round(ceil, 1)
