@@ -347,6 +347,29 @@ def test_balanced_random_sweep(pa, oracle, seed):
     assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, f"sweep seed {seed}")
 
 
+def test_negative_context_in_shared_prefix_group(pa, oracle):
+    """A negative context_lens entry (a caller error) inside a sequence
+    group whose tables share a prefix: the group shares nothing, the row
+    attends no keys (zeros, as a zero length does) and the other members
+    match the oracle.  Before the common-prefix kernel clamped its result,
+    -1000 gave a negative shared length, so every member of the group also
+    attended the unit before its first token (the entry before its table
+    row)."""
+    rng = np.random.default_rng(91)
+    ctx = np.array([5000, 7000, 6000, 4500, 8000, 3000], np.int32)
+    case = make_decode_case(rng, len(ctx), 32, 8, 128, ctx, dtype="bf16",
+                            shared_prefix_blocks=100)
+    bad = ctx.copy()
+    bad[0] = -1000  # first member of the first group (4 sequences at 4:1 GQA)
+    out = pa.decode(to_dev(case["q"]), to_dev(case["k_cache"]),
+                    to_dev(oracle.v_from_ref(case["v_cache_ref"])), to_dev(case["block_tables"]),
+                    to_dev(bad), int(ctx.max()))
+    got = oracle.bf16_to_f32(to_np(out))
+    ref = ref_f32(oracle, case)
+    assert np.all(got[0] == 0)
+    assert_close(got[1:], ref[1:], BF16_ATOL, BF16_RTOL, "members beside a negative length")
+
+
 def test_context_above_max_context_len_stays_in_bounds(pa, oracle):
     """A context_lens entry above the max_context_len argument (a caller
     error) must not write outside the workspace pa_decode_workspace_size

@@ -981,7 +981,8 @@ __global__ __launch_bounds__(kLcpThreads) void decode_lcp_kernel(
   int L = INT32_MAX;
   for (int m = 0; m < gn; ++m)
     L = min(L, min(min(context_lens[g0 + m], mbs * kBlock), cap) / (2 * kBlock));
-  if (gn < 2) L = 0;
+  // a member's negative length (a caller error) shares nothing: L >= 0
+  if (gn < 2 || L < 0) L = 0;
   // blocks below 2 L where a member's table differs from the first's (the
   // loads do not wait for L: every index below mbs is inside the tables)
   int diff = INT32_MAX;
