@@ -13,6 +13,7 @@
 #include <cstring>
 #include <map>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/pa_kv_cache.h"
@@ -106,13 +107,9 @@ int32_t scatter(pa_kv_cache* c, int layer, const std::vector<int64_t>& slots, co
   // (the reference writes token by token, so the last one wins; a slot
   // named twice in one scatter would be unspecified): earlier ones are -1.
   {
-    std::vector<int64_t> seen;
-    seen.reserve(T);
-    for (int t = T - 1; t >= 0; --t) {
-      const bool dup = std::find(seen.begin(), seen.end(), slots[t]) != seen.end();
-      host[t] = dup ? -1 : slots[t];
-      if (!dup) seen.push_back(slots[t]);
-    }
+    std::unordered_set<int64_t> seen;
+    seen.reserve(2 * (size_t)T);
+    for (int t = T - 1; t >= 0; --t) host[t] = seen.insert(slots[t]).second ? slots[t] : -1;
   }
   auto* i32 = reinterpret_cast<int32_t*>(host.data() + 2 * T);
   int32_t* blk = i32;
