@@ -3,6 +3,8 @@ crates/model/src/components/kv_cache_fp8.rs): the quantising cache write is
 bit-exact against the oracle encoder, read_kv against the oracle decoder, and
 decode / prefill over FP8 caches match the oracle's attention over the
 dequantised caches within the bf16 tolerance."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -281,3 +283,53 @@ def test_prefill_fp8_special_codes(pa, oracle):
                                  oracle.fp8_decode(vc), bt, cu, past)
     assert np.isnan(ref).any() and np.isinf(ref).any() and np.isfinite(ref).any()
     assert_same_specials(got, ref, "fp8 prefill specials")
+
+
+def test_prefill_fp8_config3_full_size(pa, oracle):
+    # The config-3 workload over an FP8-E4M3 cache at full size (the
+    # prefill-fp8 benchmark): 4 x 2048 new tokens on past 0 / 512 / 1024 /
+    # 2048, 32 / 8 x 128.  Sampled query rows against the oracle over the
+    # decoded cache (row i of sequence s as a one-row sequence with past
+    # P_s + i: tile diagonal edges, both wavefront halves, the first and last
+    # rows, random rows), then every row against pa_decode over the same
+    # FP8 cache (the FP8 decode kernel is itself checked against the oracle).
+    from test_gpu_prefill import make_prefill_case
+    rng = np.random.default_rng(3)
+    pasts, chunk = [0, 512, 1024, 2048], 2048
+    q, kc, vc, bt, cu, past = make_prefill_case(oracle, rng, pasts, [chunk] * 4, 32, 8, 128,
+                                                "f32")
+    q = oracle.f32_to_bf16(q)
+    kc8, vc8 = oracle.fp8_encode(kc), oracle.fp8_encode(vc)
+    dk, dv, dbt = to_dev(kc8), to_dev(oracle.v_from_ref(vc8)), to_dev(bt)
+    out = pa.prefill(to_dev(q), dk, dv, dbt, to_dev(cu), to_dev(past), chunk)
+    got = oracle.bf16_to_f32(to_np(out))
+
+    rows = []
+    for s in range(4):
+        pick = {0, 1, 31, 32, 33, 2047, 2046}
+        pick |= {i for i in range(chunk) if i % 64 in (0, 63) and i % 512 < 64}
+        pick |= set(rng.integers(0, chunk, 8).tolist())
+        rows += [(s, i) for i in sorted(pick)]
+    sel = np.array([cu[s] + i for s, i in rows])
+    past1 = np.array([pasts[s] + i for s, i in rows], np.int32)
+    ref = oracle.paged_attention(oracle.bf16_to_f32(q[sel]), oracle.fp8_decode(kc8),
+                                 oracle.fp8_decode(vc8), bt[[s for s, _ in rows]],
+                                 np.arange(len(rows) + 1), past1, scale=1 / math.sqrt(128))
+    assert_close(got[sel], ref, BF16_ATOL, BF16_RTOL, "fp8 config 3 full, sampled rows")
+
+    seq = np.repeat(np.arange(4), chunk)
+    ctx = (np.asarray(pasts)[seq] + np.tile(np.arange(chunk), 4) + 1).astype(np.int32)
+    dec = pa.decode(to_dev(q), dk, dv, to_dev(bt[seq]), to_dev(ctx), int(ctx.max()))
+    assert_close(got, oracle.bf16_to_f32(to_np(dec)), 2e-2, 1e-2,
+                 "fp8 config 3 full, all rows vs pa_decode")
+
+
+def test_decode_fp8_config2_full_size(pa, oracle):
+    # The config-2 shape over an FP8-E4M3 cache at full size (the
+    # decode-fp8 benchmark: B 64, ctx 4096, 32 / 8 x 128; 512-token
+    # partitions merged eight per workgroup) against the oracle over the
+    # decoded cache.
+    rng = np.random.default_rng(12)
+    case, kc, vc = fp8_decode_case(oracle, rng, 64, 32, 8, 128, [4096] * 64)
+    got, ref = run_fp8_decode(pa, oracle, case, kc, vc)
+    assert_close(got, ref, BF16_ATOL, BF16_RTOL, "fp8 config 2 full")
