@@ -230,8 +230,10 @@ int32_t pa_decode(void* out, const void* q, const void* k_cache, const void* v_c
  * (pa_decode_noalloc_scratch_bytes() bytes, 64 MiB, one per GPU, held until
  * the process ends; its address is looked up once per device on the first
  * call).  Sizes whose split needs more (pa_decode_workspace_size() bounds
- * it) return PA_ERR_WORKSPACE without launching.  Calls on one GPU share the
- * array: calls that may overlap (other streams, other threads) race. */
+ * it) return PA_ERR_WORKSPACE without launching.  The stream must belong to
+ * the calling thread's current device (PA_ERR_INVALID_ARG otherwise).  Calls
+ * on one GPU share the array: calls that may overlap (other streams, other
+ * threads) race. */
 int32_t pa_decode_noalloc(void* out, const void* q, const void* k_cache, const void* v_cache,
                           const int32_t* block_tables, int32_t max_blocks_per_seq,
                           const int32_t* context_lens, int32_t max_context_len,

@@ -1727,6 +1727,16 @@ extern "C" int32_t pa_decode_noalloc(void* out, const void* q, const void* k_cac
                "split-K scratch, above the fixed %zu (use pa_decode with a workspace)",
                num_seqs, num_heads, max_context_len, plan.ws_bytes, kDecodeScratchBytes);
   }
+  // the array used is the current device's: the stream must run there
+  if (stream) {
+    int cur = -1;
+    hipDevice_t sdev = -1;
+    PA_REQUIRE(hipGetDevice(&cur) == hipSuccess &&
+                   hipStreamGetDevice((hipStream_t)stream, &sdev) == hipSuccess && sdev == cur,
+               PA_ERR_INVALID_ARG,
+               "pa_decode_noalloc: the stream belongs to device %d, not the current device %d",
+               (int)sdev, cur);
+  }
   void* ws = nullptr;
   const int32_t rc = scratch_ptr(&ws);
   if (rc != PA_OK) return rc;
