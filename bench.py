@@ -99,6 +99,9 @@ class Workload:
                 bt[b, 256:n] = perm[o:o + n - 256]
                 o += n - 256
             kv_scale = 1.0
+            # a second 4096-token prefix (blocks past the pool) for the
+            # batch-order check: two prefixes, each shared by 8 sequences
+            self.extra_blocks = 256
             self.workload = ("config 4: long-context split-K decode bf16, B 16, 32/8 x 128, "
                              "ctx log-U[8k, 32k], 4096-token shared prefix")
         elif name == "qwen":
@@ -166,9 +169,10 @@ class Workload:
                 pa.reshape_and_cache_fp8(kk, vv, self.kc, self.vc, sl)
             del kk, vv, sl
         else:
-            self.kc = (torch.randn(pool, hkv, 16, d, generator=dg, device=DEV) * kv_scale).to(
+            nbk = pool + getattr(self, "extra_blocks", 0)
+            self.kc = (torch.randn(nbk, hkv, 16, d, generator=dg, device=DEV) * kv_scale).to(
                 self.dtype)
-            self.vc = (torch.randn(pool, hkv, d, 16, generator=dg, device=DEV) * kv_scale).to(
+            self.vc = (torch.randn(nbk, hkv, d, 16, generator=dg, device=DEV) * kv_scale).to(
                 self.dtype)
         self.ctx_dev = self.ctx.to(DEV) if self.kind == "decode" else None
         es = torch.empty(0, dtype=self.dtype).element_size()
@@ -198,6 +202,19 @@ class Workload:
             tokens_all = sum(p + 2048 for p in [0, 512, 1024, 2048])
             kv_es = 1 if self.fp8 else es
             self.alg_bytes = (2 * tokens_all * hkv * d * kv_es + 2 * self.q.numel() * es)
+
+    def two_prefix_tables(self, interleaved):
+        """Config 4's tables with two 4096-token prefixes, each shared by 8
+        sequences: A by sequences 0-7 and B by 8-15 (ordered), or A by the
+        even and B by the odd batch slots (interleaved).  Same contexts,
+        same bytes and the same sharing in both; only the batch order of
+        the sharers differs."""
+        bt = self.bt.clone()
+        other = torch.arange(self.pool, self.pool + 256, dtype=torch.int32, device=DEV)
+        for b in range(self.B):
+            if (b % 2 == 1) if interleaved else (b >= self.B // 2):
+                bt[b, :256] = other
+        return bt
 
     def write_step(self):
         if self.fp8:
@@ -321,7 +338,7 @@ def cpu_baseline(w, budget_s=12.0):
 
     threads = cpu_threads()
     if w.kind != "decode":
-        return None
+        return cpu_baseline_prefill(w, oracle, threads, budget_s)
     nseq = min(8, w.B)
     bt = w.bt[:nseq].cpu().numpy()
     ctx = w.ctx[:nseq].numpy()
@@ -363,6 +380,142 @@ def cpu_baseline(w, budget_s=12.0):
             "sample": f"{nseq} sequences of the same workload x {reps} passes "
                       f"({el:.1f} s): oracle {'FP8 dequantisation + ' if w.fp8 else ''}"
                       "gather + expand_kv + dense f32 softmax attention, OpenMP"}
+
+
+def cpu_baseline_prefill(w, oracle, threads, budget_s):
+    """Config 3 on the C oracle (the reference's chunked-prefill path
+    restated: per 16-row query tile, gather the tile's visible keys to dense
+    f32, expand KV to every query head, masked dense softmax attention,
+    OpenMP over heads), timed on a bounded sample of the same workload: 8
+    query tiles of 16 rows spread evenly over each sequence's 2048-row chunk
+    (32 tiles), each attending its past + causal keys.  The rate is the
+    sample's causal (query, key) pairs x 4 Hq D FLOP per second, the unit of
+    the GPU figure."""
+    pasts = w.past.cpu().tolist()
+    cu = w.cu.cpu().tolist()
+    bt_all = w.bt.cpu().numpy()
+    tiles = []
+    for b, past in enumerate(pasts):
+        for t0 in np.linspace(0, w.max_q - 16, 8).astype(int).tolist():
+            tiles.append((b, past + t0, cu[b] + t0))
+    # the blocks the sample reads, remapped into a compact host pool
+    used = sorted({int(x) for b, p, _ in tiles for x in bt_all[b, :(p + 16 + 15) // 16]})
+    remap = np.zeros(int(bt_all.max()) + 1, np.int32)
+    remap[used] = np.arange(len(used), dtype=np.int32)
+    idx = torch.tensor(used, device=DEV)
+
+    def host(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    if w.fp8:
+        kc = oracle.fp8_decode(host8(w.kc[idx]))
+        vc = oracle.fp8_decode(host8(w.vc[idx].transpose(-1, -2)))
+        q = oracle.bf16_to_f32(host(w.q))
+    else:
+        kc = host(w.kc[idx])
+        vc = host(w.vc[idx].transpose(-1, -2))
+        q = host(w.q)
+    bt = np.stack([remap[bt_all[b]] for b, _, _ in tiles]).astype(np.int32)
+    qs = np.concatenate([q[r0:r0 + 16] for _, _, r0 in tiles])
+    past = np.array([p for _, p, _ in tiles], np.int32)
+    qstart = np.arange(0, 16 * len(tiles) + 1, 16, dtype=np.int32)
+    pairs = sum(16 * p + 16 * 17 // 2 for p in past.tolist())
+    flops = 4.0 * pairs * w.hq * w.d
+    oracle.paged_attention(qs[:16], kc, vc, bt[:1], qstart[:2], past[:1], scale=w.scale,
+                           threads=threads)  # warm
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        oracle.paged_attention(qs, kc, vc, bt, qstart, past, scale=w.scale, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 50:
+            break
+    return {"value": round(flops * reps / el / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{len(tiles)} query tiles of 16 rows spread over the 4 chunks "
+                      f"({pairs} causal pairs) x {reps} passes ({el:.1f} s): oracle "
+                      f"{'FP8 dequantisation (outside the timing) + ' if w.fp8 else ''}"
+                      "gather + expand_kv + masked dense f32 softmax attention, OpenMP"}
+
+
+def host8(t):
+    return t.contiguous().cpu().numpy()
+
+
+def run_kv_rw(pa, args):
+    """The reference's own published microbenchmark on this path,
+    paged_kv_cache/read_write (crates/model/benches/paged_kv_cache.rs:69-103):
+    a 1-layer f32 cache of 2 heads x 64 dims and 64 / 256 / 1024 blocks; each
+    iteration is one write_kv of one token into (block 0, offset 0) and one
+    read_kv of 1 token over block 0, here pa_kv_cache_write_kv +
+    pa_kv_cache_read_kv through the cache mirror (both synchronise, as the
+    reference's host copies do), timed end to end in ns per iteration.  The
+    reference's figures (docs/perf/v27-after.md:61-63) were taken on an
+    unnamed CUDA GPU.  The oracle's write_kv + read_kv on the same sizes is
+    timed on the host beside it."""
+    import ctypes as C
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    ref_ns = {64: 393358, 256: 712714, 1024: 1847365}
+    lib = pa._lib.load()
+    h, d = 2, 64
+    g = torch.Generator(device=DEV).manual_seed(7)
+    for nb in (64, 256, 1024):
+        cache = pa.PagedKvCache(1, h, d, nb, dtype=torch.float32, device=DEV)
+        k = torch.randn(1, h, d, generator=g, device=DEV)
+        v = torch.randn(1, h, d, generator=g, device=DEV)
+        out_k = torch.empty(1, h, d, device=DEV)
+        out_v = torch.empty_like(out_k)
+        ids = (C.c_int64 * 1)(0)
+        n = C.c_int32(0)
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        hnd = cache._h
+        kp, vp = C.c_void_p(k.data_ptr()), C.c_void_p(v.data_ptr())
+        okp, ovp = C.c_void_p(out_k.data_ptr()), C.c_void_p(out_v.data_ptr())
+
+        def it():
+            rc = lib.pa_kv_cache_write_kv(hnd, 0, 0, 0, kp, vp, stream)
+            rc |= lib.pa_kv_cache_read_kv(hnd, 0, ids, 1, 1, okp, ovp, C.byref(n), stream)
+            return rc
+        for _ in range(max(args.warmup, 20)):
+            assert it() == 0
+        torch.cuda.synchronize()
+        iters = max(args.steps, 200)
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            it()
+        torch.cuda.synchronize()
+        ns = (time.perf_counter() - t0) / iters * 1e9
+        assert torch.equal(out_k, k) and torch.equal(out_v, v)
+        cache.close()
+        cpu = None
+        if not args.no_cpu:
+            kc = np.zeros((nb, h, 16, d), np.float32)
+            vc = np.zeros_like(kc)
+            kh, vh = k.cpu().numpy()[0], v.cpu().numpy()[0]
+            reps, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < 3.0:
+                oracle.write_kv(kc, vc, 0, 0, kh, vh)
+                oracle.read_kv(kc, vc, [0], 1)
+                reps += 1
+            cpu_ns = (time.perf_counter() - t0) / reps * 1e9
+            cpu = {"value": round(cpu_ns, 1), "unit": "ns/iter", "cores": 1, "kind": "port",
+                   "sample": f"{reps} iterations of the oracle's write_kv + read_kv (3 s)"}
+        print(json.dumps({
+            "metric": "paged_kv_cache/read_write ns/iter (reference microbenchmark)",
+            "value": round(ns, 1), "unit": "ns/iter", "n_gpus": 1, "steps": iters,
+            "warmup": max(args.warmup, 20), "ms_per_step": round(ns / 1e6, 6),
+            "higher_is_better": False,
+            "vs_baseline": round(ns / ref_ns[nb], 5), "baseline_ns": ref_ns[nb],
+            "baseline_source": "docs/perf/v27-after.md:61-63 (unnamed CUDA GPU, candle)",
+            "speedup_vs_reference": round(ref_ns[nb] / ns, 1),
+            "dtype": "f32", "data": "synthetic (N(0,1) token K/V)",
+            "config": {"workload": f"paged_kv_cache read_write blocks{nb}_h2_d64: 1 layer, "
+                                   "write_kv (block 0, offset 0) + read_kv (1 token)",
+                       "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)"},
+            "roofline": None, "cpu_baseline": cpu}), flush=True)
 
 
 def run_e2e(pa, args):
@@ -489,7 +642,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="decode",
                     choices=["decode", "decode-fp8", "prefill", "prefill-fp8", "splitk", "qwen",
-                             "e2e", "copy", "write"])
+                             "e2e", "copy", "write", "kv-rw"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-flush", action="store_true",
                     help="skip the cache-flushed timing leg (keeps a kernel trace to warm launches)")
@@ -507,6 +660,8 @@ def main():
         return run_e2e(pa, args)
     if args.config == "write":
         return run_write(pa, args)
+    if args.config == "kv-rw":
+        return run_kv_rw(pa, args)
     w = Workload(pa, args.config)
     for _ in range(args.warmup):
         w.step()
@@ -533,18 +688,28 @@ def main():
                      lambda x: w.alg_bytes / x / 1e9 / HBM_PEAK_GBS, args.no_flush)
         if args.config == "splitk":
             roof["unique_block_gbs"] = round((w.unique_kv_bytes) / t_attn / 1e9, 1)
+            # batch-order independence of the shared-prefix grouping
+            bt0 = w.bt
+            order = {}
+            for key, inter in (("two_prefixes_ordered_us", False),
+                               ("two_prefixes_interleaved_us", True)):
+                w.bt = w.two_prefix_tables(inter)
+                w.attend()
+                order[key] = round(time_attend(w, max(args.steps, 20)) * 1e6, 2)
+            w.bt = bt0
+            roof["batch_order"] = order
             # the profiled HBM bytes (FETCH + WRITE) over this run's launch time
             if traffic:
                 roof["physical_frac"] = round(traffic / t_attn / 1e9 / HBM_PEAK_GBS, 4)
         # configs 2 (bf16, FP8): two 2048-token partitions per (kv head,
         # sequence), merged in the workgroup; config 4: the work cut evenly over
         # the GPU, a sequence group's shared block-table prefix attended once
-        # (its length found by decode_lcp_kernel), partial results merged by the
+        # (groups and prefixes found by decode_group_kernel), partial results merged by the
         # reduce kernel; config 1 (f32): the group kernel and the reduce kernel
         roof["kernel"] = {
             "decode": "pa_decode (decode_mfma_kernel, partitions merged in the workgroup)",
             "decode-fp8": "pa_decode (decode_fp8_kernel, partitions merged in the workgroup)",
-            "splitk": "pa_decode (decode_lcp_kernel + decode_balanced_kernel + decode_reduce_kernel)",
+            "splitk": "pa_decode (decode_group_kernel + decode_balanced_kernel + decode_reduce_kernel)",
             "qwen": "pa_decode (decode_f32_group_kernel + decode_reduce_kernel)",
         }[args.config]
     else:

@@ -48,11 +48,11 @@ def test_version_and_empty_error(lib):
 def test_workspace_size(lib):
     # one partition (<= 128 tokens) needs none; otherwise B*Hq*(P+2)*(D+2)
     # f32 with P = ceil(ctx / 128) (the f32 group kernel's shortest
-    # partitions; a balanced launch writes up to ceil(ctx / 256) + 2 partial
-    # results per row) and one int per sequence
+    # partitions; a balanced launch writes up to ceil(ctx / 256) + 3 partial
+    # results per row) and the shared-prefix group record (6 B + 2 ints)
     assert lib.pa_decode_workspace_size(64, 32, 128, 128) == 0
-    assert lib.pa_decode_workspace_size(64, 32, 128, 4096) == 64 * 32 * 34 * 130 * 4 + 64 * 4
-    assert lib.pa_decode_workspace_size(2, 4, 64, 257) == 2 * 4 * 5 * 66 * 4 + 2 * 4
+    assert lib.pa_decode_workspace_size(64, 32, 128, 4096) == 64 * 32 * 34 * 130 * 4 + 386 * 4
+    assert lib.pa_decode_workspace_size(2, 4, 64, 257) == 2 * 4 * 5 * 66 * 4 + 14 * 4
 
 
 def test_argument_errors_without_gpu(lib):

@@ -395,3 +395,68 @@ def test_context_above_max_context_len_stays_in_bounds(pa, oracle):
         ctx - 1, scale=1.0 / math.sqrt(128)))
     assert_close(got[2:], ref[2:], BF16_ATOL, BF16_RTOL, "sequences within max_context_len")
     assert np.isfinite(got[:2]).all()
+
+
+def _balanced_groups(ws, b, hq, d, max_ctx):
+    """The shared-prefix group record a balanced launch leaves in its
+    workspace (after the b * hq * slots partial results): group count,
+    members of each group (batch indices) and their shared 32-token units."""
+    units = (max_ctx + 31) // 32
+    slots = (units + 7) // 8 + 3
+    off = b * hq * slots * (d + 2) * 4
+    rec = ws[off:off + (6 * b + 2) * 4].cpu().numpy().view(np.int32)
+    ng = int(rec[0])
+    order, gstart, lcp = rec[1:1 + b], rec[1 + b:2 + 2 * b], rec[2 + 4 * b:2 + 5 * b]
+    return [sorted(order[gstart[g]:gstart[g + 1]].tolist()) for g in range(ng)], lcp[:ng]
+
+
+def test_config4_sharers_shuffled_among_private_sequences(pa, oracle):
+    # Config 4's 16 sharers of a 4096-token prefix, randomly permuted and
+    # interleaved with 8 sequences that share nothing: the groups of four
+    # sharers (16 / G MFMA columns) must still form and attend the prefix
+    # once, wherever the sharers sit in the batch.
+    rng = np.random.default_rng(33)
+    n_sh, n_pr = 16, 8
+    ctx = np.exp(rng.uniform(np.log(8192), np.log(32768), size=n_sh + n_pr)).astype(np.int32)
+    case = make_decode_case(rng, n_sh + n_pr, 32, 8, 128, ctx, dtype="bf16",
+                            shared_prefix_blocks=256)
+    bt = case["block_tables"]
+    nb = case["num_blocks"]
+    extra = rng.permutation(np.arange(nb, nb + 256 * n_pr)).astype(np.int32)
+    bt[n_sh:, :256] = extra.reshape(n_pr, 256)          # private prefixes
+    for key in ("k_cache", "v_cache_ref"):
+        pad = rng.standard_normal((len(extra),) + case[key].shape[1:], dtype=np.float32)
+        case[key] = np.concatenate([case[key], oracle.f32_to_bf16(pad)])
+    perm = rng.permutation(n_sh + n_pr)
+    for key in ("q", "block_tables", "ctx"):
+        case[key] = np.ascontiguousarray(case[key][perm])
+    b, max_ctx = n_sh + n_pr, int(case["ctx"].max())
+    ws = torch.zeros(pa.decode_workspace_size(b, 32, 128, max_ctx), dtype=torch.uint8,
+                     device=DEV)
+    out = pa.decode(to_dev(case["q"]), to_dev(case["k_cache"]),
+                    to_dev(oracle.v_from_ref(case["v_cache_ref"])),
+                    to_dev(case["block_tables"]), to_dev(case["ctx"]), max_ctx, workspace=ws)
+    got = oracle.bf16_to_f32(to_np(out))
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "config 4 shuffled")
+    groups, lcp = _balanced_groups(ws, b, 32, 128, max_ctx)
+    sharers = set(np.nonzero(perm < n_sh)[0].tolist())
+    shared_groups = [g for g in groups if len(g) > 1]
+    assert sorted(sum(shared_groups, [])) == sorted(sharers)
+    assert all(len(g) == 4 for g in shared_groups)
+    assert all(l == 128 for g, l in zip(groups, lcp) if len(g) > 1)   # 4096 tokens
+
+
+def test_balanced_row_needing_plus_three_slots(pa, oracle):
+    # A layout whose row needs ceil(units / 8) + 3 partial-result slots (32 /
+    # 8 x 128, contexts 4007 / 4096 / 1087, sequences 0 and 1 sharing 182
+    # blocks): the slot sizing must hold it (the former + 2 sizing wrote one
+    # slot past the row).
+    rng = np.random.default_rng(19)
+    ctx = np.array([4007, 4096, 1087], np.int32)
+    case = make_decode_case(rng, 3, 32, 8, 128, ctx, dtype="bf16", shared_prefix_blocks=182)
+    case["block_tables"][2, :68] = np.arange(case["num_blocks"], case["num_blocks"] + 68)
+    for key in ("k_cache", "v_cache_ref"):
+        pad = rng.standard_normal((68,) + case[key].shape[1:], dtype=np.float32)
+        case[key] = np.concatenate([case[key], oracle.f32_to_bf16(pad)])
+    got, _ = run_decode(pa, oracle, case, "bf16")
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "plus-three slots")

@@ -920,26 +920,48 @@ __device__ inline int seq_units(const int32_t* __restrict__ context_lens, int s,
   return ctx > 0 ? (ctx + 2 * kBlock - 1) / (2 * kBlock) : 0;
 }
 
-// Work layout of a balanced launch.  Sequences are taken in groups of SP
-// consecutive ones (SP = 16 / G, the sequences whose query heads fill the
-// 16 MFMA columns together; SP = 1 without sharing).  lcp[g] (or 0) is the
-// number of leading units every member of group g holds in full and whose
-// blocks all members' tables share (a common prefix).  Group g's units:
+// Work layout of a balanced launch.  Sequences are taken in groups of at
+// most SP (= 16 / G, the sequences whose query heads fill the 16 MFMA
+// columns together) that begin with the same block (a prefix-cache hit:
+// decode_group_kernel sorts the sequences by their first block, wherever
+// they sit in the batch, and cuts each run of equal first blocks into
+// groups of SP).  lcp[g] is the number of leading units every member of
+// group g holds in full and whose blocks all members' tables share (a
+// common prefix).  Group g's units:
 //   the shared segments (kv head 0 .. Hkv-1, lcp[g] units each, every
 //   member attended at once), then for each member the private segments
 //   (kv head 0 .. Hkv-1, its units past the prefix).
+// Without sharing (grp null) every sequence is its own group, in order.
+//
+// The group record `grp` (int32, 6 B + 2 entries, written by
+// decode_group_kernel): [0] group count ng; order[B] (sequence at each
+// sorted position); gstart[B + 1] (first position of each group, gstart[ng]
+// = B); gof[B] (group of each sequence); pos[B] (sorted position of each
+// sequence); lcp[B] (shared units of each group); gsum[B] (the members'
+// units summed, so a group's size needs no walk over its members).
+constexpr int kGrpOrder = 1;
+__device__ inline int grp_gstart(int B) { return 1 + B; }
+__device__ inline int grp_gof(int B) { return 2 + 2 * B; }
+__device__ inline int grp_pos(int B) { return 2 + 3 * B; }
+__device__ inline int grp_lcp(int B) { return 2 + 4 * B; }
+__device__ inline int grp_gsum(int B) { return 2 + 5 * B; }
+
 struct BalanceLayout {
   const int32_t* __restrict__ ctx;
-  const int32_t* __restrict__ lcp;  // null: no shared prefixes
-  int B, mbs, Hkv, SP, cap;
+  const int32_t* __restrict__ grp;  // null: no shared prefixes
+  int B, mbs, Hkv, cap;
   __device__ int units(int s) const { return seq_units(ctx, s, mbs, cap); }
-  __device__ int shared(int g) const { return lcp ? lcp[g] : 0; }
-  __device__ int groups() const { return (B + SP - 1) / SP; }
+  __device__ int groups() const { return grp ? grp[0] : B; }
+  // first sorted position of group g (g <= groups())
+  __device__ int first(int g) const { return grp ? grp[grp_gstart(B) + g] : g; }
+  __device__ int member(int p) const { return grp ? grp[kGrpOrder + p] : p; }
+  __device__ int group_of(int s) const { return grp ? grp[grp_gof(B) + s] : s; }
+  __device__ int pos_of(int s) const { return grp ? grp[grp_pos(B) + s] : s; }
+  __device__ int shared(int g) const { return grp ? grp[grp_lcp(B) + g] : 0; }
   __device__ int64_t group_units(int g) const {
-    const int L = shared(g);
-    int64_t n = L;
-    for (int m = g * SP; m < min(B, g * SP + SP); ++m) n += units(m) - L;
-    return n * Hkv;
+    if (!grp) return (int64_t)units(g) * Hkv;
+    const int L = shared(g), gn = first(g + 1) - first(g);
+    return ((int64_t)L + grp[grp_gsum(B) + g] - (int64_t)gn * L) * Hkv;
   }
   // units of the groups before `upto`, summed over a wavefront (every lane
   // returns the same value)
@@ -960,43 +982,113 @@ __device__ inline int wave_of(int64_t g, int64_t total, int nw) {
   return (int)(((g + 1) * nw - 1) / total);
 }
 // Slots of a segment [start, start + len): its first to its last wavefront.
+// Every wavefront's range holds at least kBalanceMinUnits units (N <= U /
+// kBalanceMinUnits), so a segment of n units meets at most
+// floor((n - 2) / kBalanceMinUnits) + 2 <= ceil(n / kBalanceMinUnits) + 1
+// wavefronts, and a row's two segments (n units in all) at most
+// ceil(n / kBalanceMinUnits) + 3: the slots per row decode_plan sizes.
 __device__ inline int seg_slots(int64_t start, int len, int64_t total, int nw) {
   return len > 0 ? wave_of(start + len - 1, total, nw) - wave_of(start, total, nw) + 1 : 0;
 }
 
-// Common prefix of each group's tables, in full units (the shared part of
-// BalanceLayout): one workgroup of kLcpThreads per group.  Every table entry
-// a member may share (below the row length, before the group's limit is
-// known) is loaded and compared at once, so the launch costs one round trip
-// for the context lengths and tables together; the first differing block
-// is the workgroup's minimum.
-constexpr int kLcpThreads = 1024;
-__global__ __launch_bounds__(kLcpThreads) void decode_lcp_kernel(
+// Shared-prefix groups and their common prefixes, in full units.  Every
+// workgroup (one per possible group, B in all) sorts the sequences by
+// (first block id, index) in LDS, redundantly, so no second launch is
+// needed: each thread ranks one key against all B <= kGroupMaxSeqs
+// (broadcast LDS reads, four barriers in all; a bitonic sort's ~40
+// barriers of 16 wavefronts cost 3 us more at B 16), cuts the runs of
+// sequences that begin with the same block into groups of at most SP, and
+// workgroup g finds group g's common
+// prefix: every table entry a member may share is loaded and compared at
+// once, and the first differing block is the workgroup's minimum.
+// Workgroup 0 writes the group record.  A sequence holding no full unit
+// (32 tokens) shares nothing and is a group of its own.
+constexpr int kGroupThreads = 1024;
+constexpr int kGroupMaxSeqs = 1024;  // larger launches are not grouped
+__global__ __launch_bounds__(kGroupThreads) void decode_group_kernel(
     const int32_t* __restrict__ block_tables, int mbs, const int32_t* __restrict__ context_lens,
-    int B, int SP, int cap, int32_t* __restrict__ lcp) {
+    int B, int SP, int cap, int32_t* __restrict__ grp) {
+  __shared__ uint64_t raw[kGroupMaxSeqs];
+  __shared__ uint64_t key[kGroupMaxSeqs];   // sorted
+  __shared__ uint8_t newg[kGroupMaxSeqs];   // a group starts at this position
+  __shared__ int32_t gid[kGroupMaxSeqs];
+  __shared__ int32_t gst[kGroupMaxSeqs + 1];
   __shared__ int first_diff;
-  const int g = blockIdx.x, tid = threadIdx.x;
-  const int g0 = g * SP, gn = min(SP, B - g0);
+  const int tid = threadIdx.x, g = blockIdx.x;
+  constexpr uint32_t kNone = 0xFFFFFFFFu;  // first "block" of a sequence that shares nothing
+  if (tid < B) {
+    const int units = min(min(context_lens[tid], mbs * kBlock), cap) / (2 * kBlock);
+    const uint32_t id = units > 0 ? (uint32_t)block_tables[(int64_t)tid * mbs] : kNone;
+    raw[tid] = ((uint64_t)id << 32) | (uint32_t)tid;
+  }
   if (tid == 0) first_diff = INT32_MAX;
+  __syncthreads();
+  if (tid < B) {  // the keys are distinct (the index is in the low half)
+    const uint64_t k = raw[tid];
+    int rank = 0;
+    for (int t = 0; t < B; ++t) rank += raw[t] < k;
+    key[rank] = k;
+  }
+  __syncthreads();
+  // runs of equal first blocks (a sequence that shares nothing is a run of
+  // its own), cut into groups of SP
+  if (tid < B) {
+    const uint32_t hi = (uint32_t)(key[tid] >> 32);
+    int r0 = tid;
+    if (hi != kNone)
+      while (r0 > 0 && (uint32_t)(key[r0 - 1] >> 32) == hi) --r0;
+    newg[tid] = (tid - r0) % SP == 0;
+  }
+  __syncthreads();
+  if (tid < B) {
+    int n = 0;
+    for (int t = 0; t <= tid; ++t) n += newg[t];
+    gid[tid] = n - 1;
+    if (newg[tid]) gst[n - 1] = tid;
+  }
+  __syncthreads();
+  const int ng = gid[B - 1] + 1;
+  if (tid == 0) gst[ng] = B;
+  __syncthreads();
+  if (g == 0) {
+    if (tid == 0) grp[0] = ng;
+    for (int r = tid; r < B; r += kGroupThreads) {
+      const int s = (int)(uint32_t)key[r];
+      grp[kGrpOrder + r] = s;
+      grp[grp_gof(B) + s] = gid[r];
+      grp[grp_pos(B) + s] = r;
+    }
+    for (int r = tid; r <= ng; r += kGroupThreads) grp[grp_gstart(B) + r] = gst[r];
+  }
+  if (g >= ng) return;
+  const int p0 = gst[g], gn = gst[g + 1] - p0;
+  const int s0 = (int)(uint32_t)key[p0];
   int L = INT32_MAX;
-  for (int m = 0; m < gn; ++m)
-    L = min(L, min(min(context_lens[g0 + m], mbs * kBlock), cap) / (2 * kBlock));
+  for (int m = 0; m < gn; ++m) {
+    const int s = (int)(uint32_t)key[p0 + m];
+    L = min(L, min(min(context_lens[s], mbs * kBlock), cap) / (2 * kBlock));
+  }
   // a member's negative length (a caller error) shares nothing: L >= 0
   if (gn < 2 || L < 0) L = 0;
   // blocks below 2 L where a member's table differs from the first's (the
   // loads do not wait for L: every index below mbs is inside the tables)
   int diff = INT32_MAX;
-  for (int b = tid; b < mbs; b += kLcpThreads) {
-    const int32_t id = block_tables[(int64_t)g0 * mbs + b];
+  for (int b = tid; b < mbs; b += kGroupThreads) {
+    const int32_t id = block_tables[(int64_t)s0 * mbs + b];
     bool d = false;
-    for (int m = 1; m < gn; ++m) d |= block_tables[(int64_t)(g0 + m) * mbs + b] != id;
+    for (int m = 1; m < gn; ++m)
+      d |= block_tables[(int64_t)(uint32_t)key[p0 + m] * mbs + b] != id;
     if (d && b < 2 * L) diff = min(diff, b);
   }
-  __syncthreads();
   for (int o = 32; o > 0; o >>= 1) diff = min(diff, __shfl_xor(diff, o, 64));
   if ((tid & 63) == 0 && diff != INT32_MAX) atomicMin(&first_diff, diff);
   __syncthreads();
-  if (tid == 0) lcp[g] = min(L, first_diff / 2);
+  if (tid == 0) {
+    grp[grp_lcp(B) + g] = min(L, first_diff / 2);
+    int sum = 0;
+    for (int m = 0; m < gn; ++m) sum += seq_units(context_lens, (int)(uint32_t)key[p0 + m], mbs, cap);
+    grp[grp_gsum(B) + g] = sum;
+  }
 }
 
 // One segment piece: kv head kvh, units [u0, u1) of the segment.  Shared
@@ -1007,7 +1099,7 @@ __global__ __launch_bounds__(kLcpThreads) void decode_lcp_kernel(
 struct Piece {
   bool shared;
   int seq;      // private: the sequence; shared: the group's first member
-  int gn;       // shared: members
+  int p0, gn;   // shared: the group's first sorted position, members
   int kvh, u0, u1, unit_base;  // unit_base: the segment's first unit within the sequence
   int64_t start;  // the segment's first unit in the layout
   int slot_base;  // private: the row's shared slots
@@ -1019,12 +1111,12 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int B, int Hq, int Hkv, int G, int num_blocks,
     float scale_log2, int slots, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int64_t q_row, const int32_t* __restrict__ lcp, int SP, int cap) {
+    int64_t q_row, const int32_t* __restrict__ grp, int cap) {
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
   const int lane = threadIdx.x;
   const int c = lane & 15, j = lane >> 4;
-  const BalanceLayout lay{context_lens, lcp, B, mbs, Hkv, SP, cap};
+  const BalanceLayout lay{context_lens, grp, B, mbs, Hkv, cap};
   const int64_t total = lay.before(lay.groups());
   const int nw = balance_waves(total, gridDim.x);
   const int w = blockIdx.x;
@@ -1070,12 +1162,13 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
       continue;
     }
     // the segment holding gpos
-    const int L = lay.shared(g), g0 = g * SP, gn = min(SP, B - g0);
+    const int L = lay.shared(g), p0 = lay.first(g), gn = lay.first(g + 1) - p0;
     int64_t r = gpos - cg;
     Piece pc{};
     if (r < (int64_t)Hkv * L) {
       pc.shared = true;
-      pc.seq = g0;
+      pc.seq = lay.member(p0);
+      pc.p0 = p0;
       pc.gn = gn;
       pc.kvh = (int)(r / L);
       pc.u0 = (int)(r % L);
@@ -1086,7 +1179,8 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
       r -= (int64_t)Hkv * L;
       int64_t off = (int64_t)Hkv * L;
       pc.seq = -1;
-      for (int m = g0; m < g0 + gn; ++m) {  // gpos lies in this group: a member holds it
+      for (int mp = p0; mp < p0 + gn; ++mp) {  // gpos lies in this group: a member holds it
+        const int m = lay.member(mp);
         const int len = lay.units(m) - L;
         if (len > 0 && r < (int64_t)Hkv * len) {
           pc.seq = m;
@@ -1112,9 +1206,9 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
                                   : min(ctx, (pc.unit_base + pc.u1) * 2 * kBlock);
     const int nblk = (tok_end - tok0 + kBlock - 1) / kBlock;
     // this lane's MFMA column: sequence and query head
-    const int col_seq = pc.shared ? pc.seq + c / G : pc.seq;
-    const int head = kvh * G + (pc.shared ? c % G : c);
     const bool col_ok = pc.shared ? c < pc.gn * G : c < G;
+    const int col_seq = pc.shared ? (col_ok ? lay.member(pc.p0 + c / G) : pc.seq) : pc.seq;
+    const int head = kvh * G + (pc.shared ? c % G : c);
     bf16x8 qv[KS];
 #pragma unroll
     for (int st = 0; st < KS; ++st)
@@ -1240,8 +1334,8 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
     }
     lsum += shfl_xor_f(lsum, 16);
     lsum += shfl_xor_f(lsum, 32);
-    if (col_ok) {
-      const int k = (pc.shared ? 0 : pc.slot_base) + w - wave_of(pc.start, total, nw);
+    const int k = (pc.shared ? 0 : pc.slot_base) + w - wave_of(pc.start, total, nw);
+    if (col_ok && k < slots) {  // (k < slots always holds: seg_slots' bound; a guard)
       const int64_t row = ((int64_t)col_seq * Hq + head) * slots + k;
       float* orow = ws_o + row * D + 4 * j;
 #pragma unroll
@@ -1266,10 +1360,9 @@ template <typename T, int kDL>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(
     T* __restrict__ out, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ context_lens, int Hq, int D, int num_parts, int mbs,
-    int part_len, int balance_nw, int B, int Hkv, const int32_t* __restrict__ lcp, int SP,
-    int cap) {
+    int part_len, int balance_nw, int B, int Hkv, const int32_t* __restrict__ grp, int cap) {
   // balance_nw > 0: partial results of decode_balanced_kernel launched with
-  // balance_nw wavefronts (num_parts = slots per row; lcp, SP its layout);
+  // balance_nw wavefronts (num_parts = slots per row; grp its groups);
   // else partitions of part_len tokens.
   __shared__ float red[4][64 * kDL];
   __shared__ float wml[2][4];
@@ -1281,17 +1374,20 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(
   if (balance_nw > 0) {
     // this row's slots: those of its group's shared segment, then those of
     // its private segment
-    const BalanceLayout lay{context_lens, lcp, B, mbs, Hkv, SP, cap};
+    const BalanceLayout lay{context_lens, grp, B, mbs, Hkv, cap};
     const int64_t total = lay.before(lay.groups());
     np = 0;
     if (total > 0) {
       const int nw = balance_waves(total, balance_nw);
-      const int g = seq / SP, kvh = (row % Hq) / (Hq / Hkv);
+      const int g = lay.group_of(seq), kvh = (row % Hq) / (Hq / Hkv);
       const int64_t cg = lay.before(g);
       const int L = lay.shared(g);
       int64_t off = cg + (int64_t)Hkv * L;
-      for (int m = g * SP; m < seq; ++m) off += (int64_t)Hkv * (lay.units(m) - L);
+      for (int p = lay.first(g), pe = lay.pos_of(seq); p < pe; ++p)
+        off += (int64_t)Hkv * (lay.units(lay.member(p)) - L);
       const int len = lay.units(seq) - L;
+      // (the cap never binds: seg_slots' bound sizes num_parts; it keeps
+      // the reads inside the row whatever the inputs)
       np = min(seg_slots(cg + (int64_t)kvh * L, L, total, nw) +
                    seg_slots(off + (int64_t)kvh * len, len, total, nw),
                num_parts);
@@ -1394,12 +1490,13 @@ extern "C" size_t pa_decode_workspace_size(int32_t num_seqs, int32_t num_heads, 
                                            int32_t max_context_len) {
   // Sized for the shortest partition any launch that needs a workspace uses
   // (128 tokens, the f32 group kernel's for small launches), plus two: a
-  // balanced launch writes up to ceil(max_context_len / 256) + 2 partial
-  // results per row; and one int per sequence group.
+  // balanced launch (contexts above 512 tokens) writes up to
+  // ceil(max_context_len / 256) + 3 partial results per row, which that
+  // covers; and the shared-prefix group record (6 B + 2 ints).
   const int np = num_partitions(max_context_len, kPart / 2);
   if (np <= 1 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
   return (size_t)num_seqs * num_heads * (np + 2) * (head_dim + 2) * sizeof(float) +
-         (size_t)num_seqs * sizeof(int32_t);
+         (6 * (size_t)num_seqs + 2) * sizeof(int32_t);
 }
 
 namespace {
@@ -1441,23 +1538,26 @@ DecodePlan decode_plan(int32_t dtype, bool quantized, int32_t num_seqs, int32_t 
                   : (p.np <= 8 && head_dim <= 128) ? 8
                                                    : 1;
   // Partitioned launches that need the reduce (long, ragged contexts) cut
-  // the work evenly over the GPU instead (bf16 caches): a segment of n units
-  // meets at most ceil(n / kBalanceMinUnits) + 1 wavefronts.
+  // the work evenly over the GPU instead (bf16 caches).
   p.balanced = p.mfma && !fp8 && p.np > 1 && p.merge_waves == 1;
-  // A row's slots: at most ceil(n / kBalanceMinUnits) + 1 for each of its
-  // two segments (shared prefix, private rest) of n units in all.  Groups of
-  // 16 / G sequences share a common prefix of their block tables (one
-  // launch of decode_lcp_kernel finds it; its results follow the partial
-  // results in the workspace).
+  // A row's slots: a segment of n units meets at most
+  // ceil(n / kBalanceMinUnits) + 1 wavefronts (every wavefront holds at
+  // least kBalanceMinUnits units), and a row has two segments (shared
+  // prefix, private rest) of n <= max_units units in all, so at most
+  // ceil(max_units / kBalanceMinUnits) + 3 slots.  Groups of up to 16 / G
+  // sequences that begin with the same block share a common prefix of
+  // their block tables (one launch of decode_group_kernel finds the groups
+  // and prefixes; its record follows the partial results in the
+  // workspace).
   p.share_sp = 1;
   if (p.balanced) {
     const int max_units = (max_context_len + 2 * kBlock - 1) / (2 * kBlock);
-    p.np = (max_units + kBalanceMinUnits - 1) / kBalanceMinUnits + 2;
-    if (G <= 8 && num_seqs >= 2) p.share_sp = 16 / G;
+    p.np = (max_units + kBalanceMinUnits - 1) / kBalanceMinUnits + 3;
+    if (G <= 8 && num_seqs >= 2 && num_seqs <= kGroupMaxSeqs) p.share_sp = 16 / G;
   }
   p.ws_bytes = p.np > 1 && p.merge_waves == 1
                    ? (size_t)num_seqs * num_heads * p.np * (head_dim + 2) * sizeof(float) +
-                         (p.share_sp > 1 ? (size_t)num_seqs * sizeof(int32_t) : 0)
+                         (p.share_sp > 1 ? (6 * (size_t)num_seqs + 2) * sizeof(int32_t) : 0)
                    : 0;
   return p;
 }
@@ -1506,18 +1606,18 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   const int sp = plan.share_sp;
-  int32_t* lcp = nullptr;
+  int32_t* grp = nullptr;
   if (plan.balanced) {
     if (sp > 1) {
-      lcp = (int32_t*)(ws_ml + (size_t)num_seqs * num_heads * np * 2);
-      decode_lcp_kernel<<<(num_seqs + sp - 1) / sp, kLcpThreads, 0, s>>>(
-          block_tables, max_blocks_per_seq, context_lens, num_seqs, sp, max_context_len, lcp);
+      grp = (int32_t*)(ws_ml + (size_t)num_seqs * num_heads * np * 2);
+      decode_group_kernel<<<num_seqs, kGroupThreads, 0, s>>>(
+          block_tables, max_blocks_per_seq, context_lens, num_seqs, sp, max_context_len, grp);
     }
 #define PA_LAUNCH_BALANCED(DD)                                                                \
   decode_balanced_kernel<DD><<<kBalanceWaves, 64, 0, s>>>(                                    \
       (const uint16_t*)q, (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_tables,   \
       max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads, G, num_blocks,     \
-      scale_log2, np, ws_o, ws_ml, q_row, lcp, sp, max_context_len)
+      scale_log2, np, ws_o, ws_ml, q_row, grp, max_context_len)
     if (head_dim == 64)
       PA_LAUNCH_BALANCED(64);
     else if (head_dim == 128)
@@ -1605,7 +1705,7 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
 #define PA_LAUNCH_REDUCE(TT, DL)                                                              \
   decode_reduce_kernel<TT, DL><<<rgrid, 256, 0, s>>>(                                         \
       (TT*)out, ws_o, ws_ml, context_lens, num_heads, head_dim, np, max_blocks_per_seq,       \
-      part_len, bal, num_seqs, num_kv_heads, lcp, sp, max_context_len)
+      part_len, bal, num_seqs, num_kv_heads, grp, max_context_len)
   const bool wide = head_dim > 128;
   if (dtype == PA_DTYPE_BF16 || fp8) {
     if (wide)
