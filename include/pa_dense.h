@@ -1,8 +1,8 @@
 /*
  * pa_dense.h -- the dense side around the paged-attention path, for an
  * end-to-end decoder step: RMSNorm or LayerNorm (with the residual add fused
- * in), the SwiGLU activation, and skinny-M linear projections for decode
- * steps (larger batches use hipBLASLt).  Conventions as pa.h (device
+ * in), the SwiGLU activation, and the linear projections (skinny-M for
+ * decode steps, a tiled GEMM for prompt chunks).  Conventions as pa.h (device
  * pointers, stream-ordered, PA_OK or a negative pa_status); dtype
  * PA_DTYPE_F32 or PA_DTYPE_BF16, math in f32.
  */
@@ -59,8 +59,8 @@ enum { PA_LINEAR_RMS_IN = 1, PA_LINEAR_ADD_OUT = 2 };
  *                         outputs of column n rounded to bf16 (pa_silu_mul on
  *                         the unfused projection's output); bias must be NULL.
  * x [rows, K], weight [N or 2 N, K], out [rows, N], all contiguous bf16 and
- * 16-byte aligned, bias [N] or NULL; K (in_features) a multiple of 32, N
- * (out_features) a multiple of 16.  f32 accumulation.
+ * 16-byte aligned, bias [N] or NULL; K (in_features) and N (out_features)
+ * as the kernel below needs.  f32 accumulation.
  * packed = 1: weight is in the layout of pa_linear_pack (rows N or 2 N).
  * flags (0 or a combination):
  *   PA_LINEAR_RMS_IN   the rows of x are RMS-normalised on the fly: the result
@@ -80,8 +80,16 @@ enum { PA_LINEAR_RMS_IN = 1, PA_LINEAR_ADD_OUT = 2 };
  * tile, the last to finish summing the partial tiles in a fixed order (the
  * result does not depend on their timing).  Calls that may run at the same
  * time need distinct workspaces.  Without it one workgroup takes each tile.
- * Built for rows <= 64, where the weights dominate the traffic; the weights
- * are re-read once per 32 rows.  bf16 only (PA_ERR_UNSUPPORTED otherwise). */
+ * Two kernels behind the one entry point:
+ *  - rows <= 64 (decode steps), packed or row-major weights: the skinny
+ *    kernel, where the weights dominate the traffic (they are re-read once
+ *    per 32 rows); K a multiple of 32, N of 16;
+ *  - rows > 64 (prompt chunks), or an N the skinny tiles do not divide, with
+ *    row-major weights, no PA_LINEAR_RMS_IN and K a multiple of 64: a tiled
+ *    GEMM on the matrix cores (128 x 128 output tiles, K staged through LDS
+ *    in steps of 64; any N, with SwiGLU a multiple of 64; the workspace is
+ *    not used).
+ * Other shapes return PA_ERR_UNSUPPORTED, as does any dtype but bf16. */
 int32_t pa_linear(void* out, const void* x, const void* weight, const void* bias, int32_t rows,
                   int32_t out_features, int32_t in_features, int32_t act, int32_t packed,
                   int32_t flags, float eps, void* workspace, size_t workspace_bytes,

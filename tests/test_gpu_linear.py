@@ -284,3 +284,44 @@ def test_linear_split_k_workspace_any_call_order(pa):
         fresh = pa.linear(x, wp, workspace=pa.ops.linear_workspace(rows, n, k, device=DEV))
         assert torch.equal(got, fresh), rows
         torch.testing.assert_close(got.float(), x.float() @ w.float().T, atol=2e-2, rtol=1e-2)
+
+
+# Prefill-sized batches (rows > 64) take the tiled GEMM (gemm_tiled_kernel):
+# the config-5 projections at prompt-chunk row counts, ragged row tails
+# around the 128-row tile, bias, SwiGLU and the residual add.
+@pytest.mark.parametrize("m,n,k", [(65, 896, 896), (130, 256, 896), (1000, 896, 896),
+                                   (777, 896, 4864), (128, 128, 64), (4100, 1152, 896)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_tiled_gemm_matches_fp32(pa, m, n, k, with_bias):
+    x, w, b = operands(m, n, k, m * 3 + n + k)
+    out = pa.linear(x, w, bias=b if with_bias else None)
+    ref = x.float() @ w.float().T
+    if with_bias:
+        ref = ref + b.float()
+    assert out.shape == (m, n)
+    close(out, ref)
+
+
+@pytest.mark.parametrize("m,inter,k", [(300, 4864, 896), (65, 64, 128)])
+def test_tiled_gemm_swiglu(pa, m, inter, k):
+    x, w, _ = operands(m, 2 * inter, k, m + inter, wscale=0.05)
+    out = pa.linear(x, w, act=pa.ops.ACT_SILU_MUL)
+    gu = (x.float() @ w.float().T).to(torch.bfloat16).float()
+    close(out, F.silu(gu[:, :inter]) * gu[:, inter:])
+
+
+def test_tiled_gemm_add_out(pa):
+    x, w, _ = operands(257, 896, 4864, 11)
+    res = torch.randn(257, 896, device=DEV).to(torch.bfloat16)
+    out = res.clone()
+    pa.linear(x, w, out=out, add_to_out=True)
+    y = (x.float() @ w.float().T).to(torch.bfloat16).float()
+    close(out, res.float() + y)
+
+
+def test_tiled_gemm_large_prefill_chunk(pa):
+    # the config-5 gate|up projection over a whole prompt batch (9000 rows)
+    x, w, _ = operands(9000, 2 * 4864, 896, 3, wscale=0.05)
+    out = pa.linear(x, w, act=pa.ops.ACT_SILU_MUL)
+    gu = (x.float() @ w.float().T).to(torch.bfloat16).float()
+    close(out, F.silu(gu[:, :4864]) * gu[:, 4864:])

@@ -591,6 +591,140 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int64_t* __restr
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Prefill-sized linear layer: Y[M, N] = X[M, K] · W[N, K]ᵀ (bf16, f32
+// accumulation) for batches of many rows (prompt chunks), where the
+// arithmetic, not the weight stream, bounds the work.
+//
+// Workgroup = 4 wavefronts (2 x 2), tile 128 rows x 128 weight rows, K in
+// steps of 64.  Each step's X and W tiles (16 KB each) are copied HBM -> LDS
+// with global_load_lds (no register staging) into one of two buffers, one
+// step ahead of use; wavefront (wm, wn) computes 64 rows x 64 weight rows
+// as 2 x 2 tiles of v_mfma_f32_32x32x16_bf16.  Operand reads: lane l = 32 g
+// + n takes row n of a 32-row tile, k 8 g .. 8 g + 7 of the MFMA's 16 (one
+// 16-byte LDS read); the tiles' 128-byte rows hold their 16-byte k chunks
+// XOR-swizzled by bits 1-3 of the row (chunk position ch ^ ((r >> 1) & 7)),
+// so the 16 rows a read serves at once hit 16 distinct bank slots.
+// Output tile (32 x 32): lane (n, g) holds column n of rows
+// 8 (r / 4) + 4 g + r % 4 in register r.
+// Epilogues (EPI): 0 none; 1 + bias[n]; 2 SwiGLU over a fused gate|up
+// weight [2 N, K]: the workgroup's 128 weight rows are gate rows a0 .. a0+63
+// and up rows N + a0 .. N + a0 + 63 (a0 = 64 x the column tile), wavefront
+// wn takes gate and up rows 32 wn .. 32 wn + 31 of them, and
+// out[m][a] = silu(bf16(g)) * bf16(u); with add_out the result is added into
+// out (out = bf16(out + bf16(y))).  Rows past M read row M - 1, weight rows
+// past N (EPI 0 / 1: N need not fill the last tile) read row N - 1, and
+// neither is stored.
+constexpr int kSkinnyMaxRows = 64;  // pa_linear's skinny kernel up to here
+constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 64;
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_tiled_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ bias, int M, int N, int K, int add_out) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][2][kGemmBM * kGemmBK * 2];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n = lane & 31, g = lane >> 5;
+  const int m0 = blockIdx.y * kGemmBM;
+  // output columns of the workgroup: 128 (64 with SwiGLU)
+  const int c0 = blockIdx.x * (EPI == 2 ? 64 : kGemmBN);
+  auto swz = [](int r) -> int { return (r >> 1) & 7; };
+  // this wavefront's copies: 1 KB chunks 4 wave .. 4 wave + 3 of each tile,
+  // 8 rows of 128 bytes a chunk; lane l fills chunk position l % 8 of row
+  // l / 8, i.e. source chunk (l % 8) ^ swz(row)
+  const uint16_t* xsrc[4];
+  const uint16_t* wsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (4 * wave + i) * 8 + lane / 8;
+    const int ch = (lane % 8) ^ swz(r);
+    xsrc[i] = x + (int64_t)min(m0 + r, M - 1) * K + ch * 8;
+    const int wr = EPI == 2 ? (r < 64 ? c0 + r : N + c0 + r - 64) : min(c0 + r, N - 1);
+    wsrc[i] = w + (int64_t)wr * K + ch * 8;
+  }
+  auto issue = [&](int kt, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(xsrc[i] + kt * kGemmBK),
+          (__attribute__((address_space(3))) void*)&lds[buf][0][(4 * wave + i) * 1024], 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(wsrc[i] + kt * kGemmBK),
+          (__attribute__((address_space(3))) void*)&lds[buf][1][(4 * wave + i) * 1024], 16, 0, 0);
+    }
+  };
+  // LDS rows of this wavefront's operand tiles
+  int arow[2], brow[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    arow[t] = wm * 64 + 32 * t + n;
+    brow[t] = EPI == 2 ? 64 * t + 32 * wn + n : wn * 64 + 32 * t + n;
+  }
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.f;
+  const int nk = K / kGemmBK;
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) issue(kt + 1, buf ^ 1);
+    const uint8_t* at = &lds[buf][0][0];
+    const uint8_t* bt = &lds[buf][1][0];
+#pragma unroll
+    for (int s = 0; s < kGemmBK / 16; ++s) {
+      bf16x8 af[2], bfr[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        af[t] = *reinterpret_cast<const bf16x8*>(at + arow[t] * 128 +
+                                                 (((2 * s + g) ^ swz(arow[t])) * 16));
+        bfr[t] = *reinterpret_cast<const bf16x8*>(bt + brow[t] * 128 +
+                                                  (((2 * s + g) ^ swz(brow[t])) * 16));
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt + 1 landed
+    __syncthreads();
+  }
+  // epilogue
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * 64 + 32 * a + 8 * (r / 4) + 4 * g + r % 4;
+      if (row >= M) continue;
+      if constexpr (EPI == 2) {
+        const int col = c0 + 32 * wn + n;
+        const float gg = bf16_bits_to_f32(f32_to_bf16_bits(acc[a][0][r]));
+        const float uu = bf16_bits_to_f32(f32_to_bf16_bits(acc[a][1][r]));
+        out[(int64_t)row * N + col] = f32_to_bf16_bits(gg / (1.0f + expf(-gg)) * uu);
+      } else {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int col = c0 + wn * 64 + 32 * b + n;
+          if (col >= N) continue;
+          float y = acc[a][b][r];
+          if constexpr (EPI == 1) y += bf16_bits_to_f32(bias[col]);
+          uint16_t* o = out + (int64_t)row * N + col;
+          if (add_out) y = bf16_bits_to_f32(*o) + bf16_bits_to_f32(f32_to_bf16_bits(y));
+          *o = f32_to_bf16_bits(y);
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 }  // namespace pa
 
@@ -725,10 +859,6 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
              "pa_linear: unknown activation %d", act);
   PA_REQUIRE(rows >= 0 && out_features > 0 && in_features > 0, PA_ERR_INVALID_ARG,
              "pa_linear: bad sizes");
-  PA_REQUIRE(in_features % 32 == 0, PA_ERR_UNSUPPORTED,
-             "pa_linear: in_features %d not a multiple of 32", in_features);
-  PA_REQUIRE(out_features % 16 == 0, PA_ERR_UNSUPPORTED,
-             "pa_linear: out_features %d not a multiple of 16", out_features);
   PA_REQUIRE(act == PA_ACT_NONE || !bias, PA_ERR_INVALID_ARG,
              "pa_linear: bias with the SwiGLU epilogue");
   PA_REQUIRE((flags & ~(PA_LINEAR_RMS_IN | PA_LINEAR_ADD_OUT)) == 0, PA_ERR_INVALID_ARG,
@@ -741,6 +871,37 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   PA_REQUIRE(out && x && weight, PA_ERR_INVALID_ARG, "pa_linear: null pointer");
   PA_REQUIRE(((uintptr_t)x | (uintptr_t)weight | (uintptr_t)out) % 16 == 0, PA_ERR_INVALID_ARG,
              "pa_linear: x, weight and out must be 16-byte aligned");
+  // Batches of many rows (prompt chunks), and output widths the skinny
+  // kernel's 16-row tiles do not divide: the tiled GEMM over row-major
+  // weights, when K fits its steps (and the SwiGLU width its 64 columns).
+  const bool tiled = !packed && !(flags & PA_LINEAR_RMS_IN) && in_features % kGemmBK == 0 &&
+                     (act != PA_ACT_SILU_MUL || out_features % 64 == 0) &&
+                     (rows > kSkinnyMaxRows || out_features % 16 != 0);
+  PA_REQUIRE(tiled || in_features % 32 == 0, PA_ERR_UNSUPPORTED,
+             "pa_linear: in_features %d not a multiple of 32", in_features);
+  PA_REQUIRE(tiled || out_features % 16 == 0, PA_ERR_UNSUPPORTED,
+             "pa_linear: out_features %d not a multiple of 16", out_features);
+  if (tiled) {
+    const dim3 grid(act == PA_ACT_SILU_MUL ? out_features / 64
+                                           : (out_features + kGemmBN - 1) / kGemmBN,
+                    (rows + kGemmBM - 1) / kGemmBM);
+    PA_REQUIRE(grid.y <= 65535, PA_ERR_UNSUPPORTED, "pa_linear: %d rows", rows);
+    hipStream_t s = (hipStream_t)stream;
+    const int add = (flags & PA_LINEAR_ADD_OUT) ? 1 : 0;
+    auto* o = (uint16_t*)out;
+    auto* xx = (const uint16_t*)x;
+    auto* ww = (const uint16_t*)weight;
+    if (act == PA_ACT_SILU_MUL)
+      gemm_tiled_kernel<2><<<grid, 256, 0, s>>>(o, xx, ww, nullptr, rows, out_features,
+                                                in_features, 0);
+    else if (bias)
+      gemm_tiled_kernel<1><<<grid, 256, 0, s>>>(o, xx, ww, (const uint16_t*)bias, rows,
+                                                out_features, in_features, add);
+    else
+      gemm_tiled_kernel<0><<<grid, 256, 0, s>>>(o, xx, ww, nullptr, rows, out_features,
+                                                in_features, add);
+    return check_launch("pa_linear");
+  }
   PA_REQUIRE((rows + 31) / 32 <= 65535, PA_ERR_UNSUPPORTED, "pa_linear: %d rows", rows);
   // The split plan when the workspace holds it, else one workgroup per tile.
   LinearPlan plan = linear_plan(rows, out_features, in_features, act, true);

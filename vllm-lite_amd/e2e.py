@@ -18,8 +18,8 @@ StepBatch per engine step, and per layer
 Projections of batches of at most SKINNY_ROWS rows (decode steps, the LM head
 over the last tokens) run in pa_linear over weights repacked once at load
 time (pa_linear_pack: every MFMA operand fragment one contiguous kilobyte);
-larger batches (prefill chunks) run in hipBLASLt (torch.nn.functional.linear),
-and so does the long-K down projection of the unfused path.  With RMSNorm and
+larger batches (prefill chunks) run in pa_linear's tiled GEMM over the
+row-major weights (gate|up with its SwiGLU epilogue).  With RMSNorm and
 weights packed with the norm weights folded in (Weights.pack()), a decode step
 runs the fused layer of Engine._forward_fused: five launches per layer (the
 QKV projection with RoPE and the KV write in its epilogue, attention, O, gate|up
@@ -44,7 +44,6 @@ from .kv_cache import PagedKvCache, StepBatch
 
 
 SKINNY_ROWS = 64
-SKINNY_MAX_K = 1024  # in_features above this stay on hipBLASLt
 
 
 @dataclasses.dataclass
@@ -177,9 +176,9 @@ class Engine:
         skinny = t <= SKINNY_ROWS
 
         def linear(inp, weight, bias=None, packed=None):
-            if skinny and ops.linear_supports(inp, weight) and inp.shape[1] <= SKINNY_MAX_K:
-                return ops.linear(inp, packed if packed is not None else weight, bias)
-            return F.linear(inp, weight, bias)
+            if skinny and packed is not None:
+                return ops.linear(inp, packed, bias)
+            return ops.linear(inp.contiguous(), weight, bias)
 
         pk = w.packed or {}
 
@@ -205,17 +204,13 @@ class Engine:
             attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq, self.scale)
             o = linear(attn.view(t, nq), w.wo[layer], packed=packed("o", layer))
             self._norm(x, w.ln2[layer], c.eps, add=o, out=h)
-            if skinny and ops.linear_supports(h, w.wgu[layer]) and c.hidden <= SKINNY_MAX_K:
-                gu = packed("gu", layer)
-                act = ops.linear(h, gu if gu is not None else w.wgu[layer], act=ops.ACT_SILU_MUL)
-            else:
-                act = ops.silu_mul(F.linear(h, w.wgu[layer]))
+            gu = packed("gu", layer) if skinny else None
+            act = ops.linear(h, gu if gu is not None else w.wgu[layer], act=ops.ACT_SILU_MUL)
             add = linear(act, w.wd[layer])
         self._norm(x, w.norm, c.eps, add=add, out=h)
         rows = h if logit_rows is None else h[logit_rows]
-        if rows.shape[0] <= SKINNY_ROWS and ops.linear_supports(rows, w.embed):
-            return ops.linear(rows, pk.get("lm_head", w.embed))
-        return F.linear(rows, w.embed)
+        lm = pk.get("lm_head") if rows.shape[0] <= SKINNY_ROWS else None
+        return ops.linear(rows.contiguous(), lm if lm is not None else w.embed)
 
     def _forward_fused(self, tokens, logit_rows):
         """Decode-step forward with the RMSNorms folded into the projections:
@@ -255,7 +250,7 @@ class Engine:
                 ops.linear(act, pk["down"][layer], out=x, add_to_out=True,
                            workspace=self.linear_ws)
             else:
-                x.addmm_(act, w.wd[layer].t())
+                ops.linear(act, w.wd[layer], out=x, add_to_out=True)
         rows = x if logit_rows is None else x[logit_rows].contiguous()
         return ops.linear(rows, pk["lm_head"], rms_eps=c.eps)
 
