@@ -74,8 +74,9 @@ def test_linear_rejects_unsupported(pa):
     x, w, b = operands(4, 64, 96, 1)
     with pytest.raises(pa.PaError):
         pa.linear(x[:, :80].contiguous(), w[:, :80].contiguous())  # K not a multiple of 32
-    with pytest.raises(pa.PaError):
-        pa.linear(x, w[:40].contiguous())  # N not a multiple of 16
+    # N not a multiple of 16: the tiled GEMM takes it (K a multiple of 64)
+    x2, w2, _ = operands(4, 40, 128, 2)
+    close(pa.linear(x2, w2), x2.float() @ w2.float().T)
     with pytest.raises(pa.PaError):
         pa.linear(x.float(), w.float())  # f32
     with pytest.raises(pa.PaError):
@@ -286,11 +287,13 @@ def test_linear_split_k_workspace_any_call_order(pa):
         torch.testing.assert_close(got.float(), x.float() @ w.float().T, atol=2e-2, rtol=1e-2)
 
 
-# Prefill-sized batches (rows > 64) take the tiled GEMM (gemm_tiled_kernel):
-# the config-5 projections at prompt-chunk row counts, ragged row tails
-# around the 128-row tile, bias, SwiGLU and the residual add.
+# Prefill-sized batches (rows > 64) take the tiled GEMM (gemm_tiled_kernel,
+# 128 x 128 workgroup tiles, or 256 x 256 for outputs of 256 such tiles or
+# more): the config-5 projections at prompt-chunk row counts, ragged row and
+# column tails around both tiles, bias, SwiGLU and the residual add.
 @pytest.mark.parametrize("m,n,k", [(65, 896, 896), (130, 256, 896), (1000, 896, 896),
-                                   (777, 896, 4864), (128, 128, 64), (4100, 1152, 896)])
+                                   (777, 896, 4864), (128, 128, 64), (4100, 1152, 896),
+                                   (2100, 8000, 128), (9000, 896, 896)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_tiled_gemm_matches_fp32(pa, m, n, k, with_bias):
     x, w, b = operands(m, n, k, m * 3 + n + k)

@@ -3,6 +3,7 @@
 // the greedy argmax over logit rows.  All are HBM-bound.
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 
 #include "pa_common.hpp"
 #include "../../include/pa_dense.h"
@@ -597,130 +598,211 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int64_t* __restr
 // accumulation) for batches of many rows (prompt chunks), where the
 // arithmetic, not the weight stream, bounds the work.
 //
-// Workgroup = 4 wavefronts (2 x 2), tile 128 rows x 128 weight rows, K in
-// steps of 64.  Each step's X and W tiles (16 KB each) are copied HBM -> LDS
-// with global_load_lds (no register staging) into one of two buffers, one
-// step ahead of use; wavefront (wm, wn) computes 64 rows x 64 weight rows
-// as 2 x 2 tiles of v_mfma_f32_32x32x16_bf16.  Operand reads: lane l = 32 g
-// + n takes row n of a 32-row tile, k 8 g .. 8 g + 7 of the MFMA's 16 (one
-// 16-byte LDS read); the tiles' 128-byte rows hold their 16-byte k chunks
-// XOR-swizzled by bits 1-3 of the row (chunk position ch ^ ((r >> 1) & 7)),
-// so the 16 rows a read serves at once hit 16 distinct bank slots.
-// Output tile (32 x 32): lane (n, g) holds column n of rows
-// 8 (r / 4) + 4 g + r % 4 in register r.
+// Workgroup = WM x WN wavefronts; wavefront (wm, wn) computes TM x TN tiles
+// of 32 x 32 (v_mfma_f32_32x32x16_bf16), so the workgroup tile is
+// BM = 32 WM TM rows x BN = 32 WN TN weight rows, K in steps of BK.  Each
+// step's X and W tiles are copied HBM -> LDS with global_load_lds (no
+// register staging) into one of S buffers, S - 1 steps ahead of use.
+// Operand reads: lane l = 32 g + n takes row n of a 32-row tile, k 8 g ..
+// 8 g + 7 of the MFMA's 16 (one 16-byte LDS read, which feeds TN or TM
+// MFMAs); the tiles' rows (2 BK bytes) hold their 16-byte k chunks
+// XOR-swizzled by the row's position above the rows that share 256 bytes
+// (chunk position ch ^ ((r / (256 / 2 BK)) % (BK / 8))), so the 16 rows a
+// read serves at once hit 16 distinct bank slots.
+// The MFMAs compute the transposed tile (W rows x X rows: A = W, B = X), so
+// lane (n, g) holds X row n and, in register r, output column
+// 8 (r / 4) + 4 g + r % 4: four consecutive columns per 8-byte store.
 // Epilogues (EPI): 0 none; 1 + bias[n]; 2 SwiGLU over a fused gate|up
-// weight [2 N, K]: the workgroup's 128 weight rows are gate rows a0 .. a0+63
-// and up rows N + a0 .. N + a0 + 63 (a0 = 64 x the column tile), wavefront
-// wn takes gate and up rows 32 wn .. 32 wn + 31 of them, and
-// out[m][a] = silu(bf16(g)) * bf16(u); with add_out the result is added into
+// weight [2 N, K]: the workgroup's BN weight rows are gate rows a0 ..
+// a0 + BN/2 - 1 then the up rows N + a0 .. (a0 = BN/2 x the column tile),
+// wavefront wn takes its TN/2 gate tiles and the matching up tiles, and
+// out[m][a] = silu(bf16(g)) * bf16(u) (the exponential
+// is __expf); with add_out the result is added into
 // out (out = bf16(out + bf16(y))).  Rows past M read row M - 1, weight rows
 // past N (EPI 0 / 1: N need not fill the last tile) read row N - 1, and
 // neither is stored.
 constexpr int kSkinnyMaxRows = 64;  // pa_linear's skinny kernel up to here
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 64;
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_tiled_kernel(
+constexpr int kGemmKMultiple = 64;  // K the tiled kernel takes: a multiple of this
+constexpr int kGemmGroupM = 4;  // row tiles per group of the tile order
+template <int EPI, int WM, int WN, int TM, int TN, int BK, int S>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const uint16_t* __restrict__ bias, int M, int N, int K, int add_out) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2][2][kGemmBM * kGemmBK * 2];
+    const uint16_t* __restrict__ bias, int M, int N, int K, int add_out, int ntm, int ntn) {
+  constexpr int NW = WM * WN;
+  constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
+  static_assert(kGemmKMultiple % BK == 0, "K steps");
+  constexpr int RB = BK * 2;           // bytes per tile row
+  constexpr int RPC = 1024 / RB;       // rows per 1 KB copy chunk
+  constexpr int LPR = RB / 16;         // lanes (16-byte chunks) per row
+  constexpr int CA = BM / RPC / NW, CB = BN / RPC / NW;  // copy chunks per wavefront
+  static_assert(CA * NW * RPC == BM && CB * NW * RPC == BN && (EPI != 2 || TN % 2 == 0),
+                "tiles");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a[S][BM * RB];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b[S][BN * RB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int n = lane & 31, g = lane >> 5;
-  const int m0 = blockIdx.y * kGemmBM;
-  // output columns of the workgroup: 128 (64 with SwiGLU)
-  const int c0 = blockIdx.x * (EPI == 2 ? 64 : kGemmBN);
-  auto swz = [](int r) -> int { return (r >> 1) & 7; };
-  // this wavefront's copies: 1 KB chunks 4 wave .. 4 wave + 3 of each tile,
-  // 8 rows of 128 bytes a chunk; lane l fills chunk position l % 8 of row
-  // l / 8, i.e. source chunk (l % 8) ^ swz(row)
-  const uint16_t* xsrc[4];
-  const uint16_t* wsrc[4];
+  // Tile order: workgroups are dealt round-robin to the 8 XCDs, so
+  // workgroup id maps to logical tile (id % 8) * per_xcd + id / 8 and each
+  // XCD takes a contiguous range of the order; the order goes through
+  // groups of kGemmGroupM row tiles, column tiles outer within a group, so
+  // the workgroups running together on an XCD share X rows and W rows in
+  // its L2.
+  const int total = ntm * ntn, per_xcd = (total + 7) / 8;
+  const int L = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (L >= total) return;
+  const int grp = L / (kGemmGroupM * ntn), first_m = grp * kGemmGroupM;
+  const int gsz = min(kGemmGroupM, ntm - first_m);
+  const int tile_m = first_m + (L % (kGemmGroupM * ntn)) % gsz;
+  const int tile_n = (L % (kGemmGroupM * ntn)) / gsz;
+  const int m0 = tile_m * BM;
+  const int c0 = tile_n * (EPI == 2 ? BN / 2 : BN);  // first output column
+  auto swz = [](int r) -> int { return (r / (256 / RB)) % LPR; };
+  // this wavefront's copies: RPC rows per 1 KB chunk; lane l fills chunk
+  // position l % LPR of row l / LPR, i.e. source chunk (l % LPR) ^ swz(row)
+  const uint16_t* xsrc[CA];
+  const uint16_t* wsrc[CB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (4 * wave + i) * 8 + lane / 8;
-    const int ch = (lane % 8) ^ swz(r);
-    xsrc[i] = x + (int64_t)min(m0 + r, M - 1) * K + ch * 8;
-    const int wr = EPI == 2 ? (r < 64 ? c0 + r : N + c0 + r - 64) : min(c0 + r, N - 1);
-    wsrc[i] = w + (int64_t)wr * K + ch * 8;
+  for (int i = 0; i < CA; ++i) {
+    const int r = (CA * wave + i) * RPC + lane / LPR;
+    xsrc[i] = x + (int64_t)min(m0 + r, M - 1) * K + ((lane % LPR) ^ swz(r)) * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < CB; ++i) {
+    const int r = (CB * wave + i) * RPC + lane / LPR;
+    const int wr = EPI == 2 ? (r < BN / 2 ? c0 + r : N + c0 + r - BN / 2) : min(c0 + r, N - 1);
+    wsrc[i] = w + (int64_t)wr * K + ((lane % LPR) ^ swz(r)) * 8;
   }
   auto issue = [&](int kt, int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < CA; ++i)
       __builtin_amdgcn_global_load_lds(
-          (const void*)(xsrc[i] + kt * kGemmBK),
-          (__attribute__((address_space(3))) void*)&lds[buf][0][(4 * wave + i) * 1024], 16, 0, 0);
+          (const void*)(xsrc[i] + kt * BK),
+          (__attribute__((address_space(3))) void*)&lds_a[buf][(CA * wave + i) * 1024], 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < CB; ++i)
       __builtin_amdgcn_global_load_lds(
-          (const void*)(wsrc[i] + kt * kGemmBK),
-          (__attribute__((address_space(3))) void*)&lds[buf][1][(4 * wave + i) * 1024], 16, 0, 0);
-    }
+          (const void*)(wsrc[i] + kt * BK),
+          (__attribute__((address_space(3))) void*)&lds_b[buf][(CB * wave + i) * 1024], 16, 0, 0);
   };
-  // LDS rows of this wavefront's operand tiles
-  int arow[2], brow[2];
+  // LDS rows of this wavefront's operand tiles (SwiGLU: gate tiles, then
+  // the matching up tiles)
+  int arow[TM], brow[TN];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    arow[t] = wm * 64 + 32 * t + n;
-    brow[t] = EPI == 2 ? 64 * t + 32 * wn + n : wn * 64 + 32 * t + n;
-  }
-  f32x16 acc[2][2];
+  for (int t = 0; t < TM; ++t) arow[t] = (wm * TM + t) * 32 + n;
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int t = 0; t < TN; ++t)
+    brow[t] = EPI == 2 ? (t < TN / 2 ? (wn * TN / 2 + t) * 32 + n
+                                     : BN / 2 + (wn * TN / 2 + t - TN / 2) * 32 + n)
+                       : (wn * TN + t) * 32 + n;
+  f32x16 acc[TM][TN];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.f;
-  const int nk = K / kGemmBK;
-  issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();
+  const int nk = K / BK;
+  // copies S - 1 steps ahead: before step kt, the copies of steps kt + 1 ..
+  // kt + S - 2 may still be in flight (CA + CB loads each)
+  constexpr int PER = CA + CB;
+  static_assert(PER * (S - 2) <= 63, "vmcnt range");
+  for (int t = 0; t < S - 1 && t < nk; ++t) issue(t, t);
   for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) issue(kt + 1, buf ^ 1);
-    const uint8_t* at = &lds[buf][0][0];
-    const uint8_t* bt = &lds[buf][1][0];
-#pragma unroll
-    for (int s = 0; s < kGemmBK / 16; ++s) {
-      bf16x8 af[2], bfr[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        af[t] = *reinterpret_cast<const bf16x8*>(at + arow[t] * 128 +
-                                                 (((2 * s + g) ^ swz(arow[t])) * 16));
-        bfr[t] = *reinterpret_cast<const bf16x8*>(bt + brow[t] * 128 +
-                                                  (((2 * s + g) ^ swz(brow[t])) * 16));
-      }
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step kt + 1 landed
+    const int buf = kt % S;
+    const int ahead = min(S - 2, nk - 1 - kt);  // later steps issued
+    if (ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * PER) & 0xF) | (((2 * PER) >> 4) << 14));
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (PER & 0xF) | ((PER >> 4) << 14));
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+    // step kt has landed for every wavefront, and every wavefront is done
+    // with step kt - 1's buffer, which the copy of step kt + S - 1 reuses
     __syncthreads();
+    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    const uint8_t* at = &lds_a[buf][0];
+    const uint8_t* bt = &lds_b[buf][0];
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      bf16x8 af[TM], bfr[TN];
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        af[t] = *reinterpret_cast<const bf16x8*>(at + arow[t] * RB +
+                                                 (((2 * s + g) ^ swz(arow[t])) * 16));
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        bfr[t] = *reinterpret_cast<const bf16x8*>(bt + brow[t] * RB +
+                                                  (((2 * s + g) ^ swz(brow[t])) * 16));
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[b], af[a], acc[a][b], 0, 0, 0);
+    }
   }
-  // epilogue
+  // epilogue: acc[a][b] is the transposed tile (W rows x X rows), so lane
+  // (n, g) holds X row n and, in registers 4 q .. 4 q + 3, the four
+  // consecutive output columns 8 q + 4 g .. 8 q + 4 g + 3 (one 8-byte store)
+  const bool vec = N % 4 == 0;
 #pragma unroll
-  for (int a = 0; a < 2; ++a) {
+  for (int a = 0; a < TM; ++a) {
+    const int row = m0 + (wm * TM + a) * 32 + n;
+    if (row >= M) continue;
+    uint16_t* orow = out + (int64_t)row * N;
+    if constexpr (EPI == 2) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + wm * 64 + 32 * a + 8 * (r / 4) + 4 * g + r % 4;
-      if (row >= M) continue;
-      if constexpr (EPI == 2) {
-        const int col = c0 + 32 * wn + n;
-        const float gg = bf16_bits_to_f32(f32_to_bf16_bits(acc[a][0][r]));
-        const float uu = bf16_bits_to_f32(f32_to_bf16_bits(acc[a][1][r]));
-        out[(int64_t)row * N + col] = f32_to_bf16_bits(gg / (1.0f + expf(-gg)) * uu);
-      } else {
+      for (int b = 0; b < TN / 2; ++b)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          const int col = c0 + wn * 64 + 32 * b + n;
-          if (col >= N) continue;
-          float y = acc[a][b][r];
-          if constexpr (EPI == 1) y += bf16_bits_to_f32(bias[col]);
-          uint16_t* o = out + (int64_t)row * N + col;
-          if (add_out) y = bf16_bits_to_f32(*o) + bf16_bits_to_f32(f32_to_bf16_bits(y));
-          *o = f32_to_bf16_bits(y);
+        for (int qd = 0; qd < 4; ++qd) {
+          const int col = c0 + (wn * TN / 2 + b) * 32 + 8 * qd + 4 * g;
+          uint16_t v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float gg = bf16_bits_to_f32(f32_to_bf16_bits(acc[a][b][4 * qd + e]));
+            const float uu = bf16_bits_to_f32(f32_to_bf16_bits(acc[a][b + TN / 2][4 * qd + e]));
+            v[e] = f32_to_bf16_bits(gg / (1.0f + __expf(-gg)) * uu);
+          }
+          *reinterpret_cast<uint64_t*>(orow + col) = *reinterpret_cast<const uint64_t*>(v);
         }
-      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < TN; ++b)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int col = c0 + (wn * TN + b) * 32 + 8 * qd + 4 * g;
+          if (col >= N) continue;
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = acc[a][b][4 * qd + e];
+          if (vec) {
+            if constexpr (EPI == 1) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) y[e] += bf16_bits_to_f32(bias[col + e]);
+            }
+            uint64_t ow = add_out ? *reinterpret_cast<const uint64_t*>(orow + col) : 0;
+            uint16_t v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float t = y[e];
+              if (add_out)
+                t = bf16_bits_to_f32((uint16_t)(ow >> (16 * e))) +
+                    bf16_bits_to_f32(f32_to_bf16_bits(t));
+              v[e] = f32_to_bf16_bits(t);
+            }
+            *reinterpret_cast<uint64_t*>(orow + col) = *reinterpret_cast<const uint64_t*>(v);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (col + e >= N) continue;
+              float t = y[e];
+              if constexpr (EPI == 1) t += bf16_bits_to_f32(bias[col + e]);
+              if (add_out) t = bf16_bits_to_f32(orow[col + e]) + bf16_bits_to_f32(f32_to_bf16_bits(t));
+              orow[col + e] = f32_to_bf16_bits(t);
+            }
+          }
+        }
     }
   }
 }
@@ -874,7 +956,7 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   // Batches of many rows (prompt chunks), and output widths the skinny
   // kernel's 16-row tiles do not divide: the tiled GEMM over row-major
   // weights, when K fits its steps (and the SwiGLU width its 64 columns).
-  const bool tiled = !packed && !(flags & PA_LINEAR_RMS_IN) && in_features % kGemmBK == 0 &&
+  const bool tiled = !packed && !(flags & PA_LINEAR_RMS_IN) && in_features % kGemmKMultiple == 0 &&
                      (act != PA_ACT_SILU_MUL || out_features % 64 == 0) &&
                      (rows > kSkinnyMaxRows || out_features % 16 != 0);
   PA_REQUIRE(tiled || in_features % 32 == 0, PA_ERR_UNSUPPORTED,
@@ -882,24 +964,49 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
   PA_REQUIRE(tiled || out_features % 16 == 0, PA_ERR_UNSUPPORTED,
              "pa_linear: out_features %d not a multiple of 16", out_features);
   if (tiled) {
-    const dim3 grid(act == PA_ACT_SILU_MUL ? out_features / 64
-                                           : (out_features + kGemmBN - 1) / kGemmBN,
-                    (rows + kGemmBM - 1) / kGemmBM);
-    PA_REQUIRE(grid.y <= 65535, PA_ERR_UNSUPPORTED, "pa_linear: %d rows", rows);
+    // Large outputs: 256 x 256 workgroup tiles (8 wavefronts of 64 x 128:
+    // each operand read feeds 4 or 2 MFMAs); otherwise 128 x 128 (4
+    // wavefronts of 64 x 64), which keeps small projections spread over
+    // more workgroups.
     hipStream_t s = (hipStream_t)stream;
     const int add = (flags & PA_LINEAR_ADD_OUT) ? 1 : 0;
     auto* o = (uint16_t*)out;
     auto* xx = (const uint16_t*)x;
     auto* ww = (const uint16_t*)weight;
-    if (act == PA_ACT_SILU_MUL)
-      gemm_tiled_kernel<2><<<grid, 256, 0, s>>>(o, xx, ww, nullptr, rows, out_features,
-                                                in_features, 0);
-    else if (bias)
-      gemm_tiled_kernel<1><<<grid, 256, 0, s>>>(o, xx, ww, (const uint16_t*)bias, rows,
-                                                out_features, in_features, add);
-    else
-      gemm_tiled_kernel<0><<<grid, 256, 0, s>>>(o, xx, ww, nullptr, rows, out_features,
-                                                in_features, add);
+    auto* bb = (const uint16_t*)bias;
+    const int wcols = act == PA_ACT_SILU_MUL ? 2 * out_features : out_features;
+    const bool big = (long long)((rows + 255) / 256) * ((wcols + 255) / 256) >= 256 &&
+                     (act != PA_ACT_SILU_MUL || out_features % 128 == 0);
+    auto launch = [&](auto wmc, auto wnc, auto tmc, auto tnc) -> int32_t {
+      constexpr int WM_ = decltype(wmc)::value, WN_ = decltype(wnc)::value;
+      constexpr int TM_ = decltype(tmc)::value, TN_ = decltype(tnc)::value;
+      // K steps of 64 through two LDS buffers (measured at the config-5
+      // shapes against steps of 32 through 2, 3 or 4 buffers: equal for the
+      // 256 x 256 tiles, 28.6 vs 33.6-36.4 us for the 128 x 128 ones)
+      constexpr int BK_ = 64, S_ = 2;
+      constexpr int BM_ = 32 * WM_ * TM_, BN_ = 32 * WN_ * TN_;
+      const int ntn = act == PA_ACT_SILU_MUL ? out_features / (BN_ / 2)
+                                             : (out_features + BN_ - 1) / BN_;
+      const int ntm = (rows + BM_ - 1) / BM_;
+      PA_REQUIRE((long long)ntm * ntn < (1ll << 30), PA_ERR_UNSUPPORTED, "pa_linear: %d rows",
+                 rows);
+      const dim3 grid(8 * ((ntm * ntn + 7) / 8));
+      if (act == PA_ACT_SILU_MUL)
+        gemm_tiled_kernel<2, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+            o, xx, ww, nullptr, rows, out_features, in_features, 0, ntm, ntn);
+      else if (bias)
+        gemm_tiled_kernel<1, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+            o, xx, ww, bb, rows, out_features, in_features, add, ntm, ntn);
+      else
+        gemm_tiled_kernel<0, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+            o, xx, ww, nullptr, rows, out_features, in_features, add, ntm, ntn);
+      return PA_OK;
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    const int32_t rc = big ? launch(I4{}, I2{}, I2{}, I4{}) : launch(I2{}, I2{}, I2{}, I2{});
+    if (rc != PA_OK) return rc;
     return check_launch("pa_linear");
   }
   PA_REQUIRE((rows + 31) / 32 <= 65535, PA_ERR_UNSUPPORTED, "pa_linear: %d rows", rows);
