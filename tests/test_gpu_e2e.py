@@ -185,8 +185,8 @@ def qwen_weights(pa):
 @pytest.mark.parametrize("n_req,lo,hi,steps", [(6, 64, 512, 6), (40, 8, 48, 4)])
 def test_engine_config5_architecture(pa, oracle, qwen_weights, n_req, lo, hi, steps):
     # The engine at its benchmark architecture against the fp32 forward:
-    # prompts U[lo, hi] of random ids, prefill (hipBLASLt projections for the
-    # long batch) then decode steps on the fused path (QKV + RoPE + KV write
+    # prompts U[lo, hi] of random ids, prefill (the tiled GEMM projections for
+    # the long batch) then decode steps on the fused path (QKV + RoPE + KV write
     # epilogue, decode_mfma_kernel at D 64 with a 7:1 group, the K-split down
     # projection on the shared workspace).  40 requests put the decode
     # projections on both 32-row tiles, after the 6-request case used one.
@@ -195,6 +195,127 @@ def test_engine_config5_architecture(pa, oracle, qwen_weights, n_req, lo, hi, st
     prompts = [list(rng.integers(0, cfg.vocab, int(n)))
                for n in rng.integers(lo, hi + 1, n_req)]
     check_engine(oracle, cfg, w, prompts, steps, 1024, 0.995, 0.05)
+
+
+class RefCache:
+    """fp32 torch restatement of the model with a per-sequence K / V cache,
+    for long teacher-forced runs: prefill each prompt once (ref_logits'
+    arithmetic, keeping each layer's rotated k and v), then decode steps
+    for the whole batch at once (one new token per sequence, attention over
+    its cached keys with the lengths masked)."""
+
+    def __init__(self, cfg, w, inv_freq, prompts):
+        self.cfg, self.w, self.inv = cfg, w, inv_freq
+        f = lambda t: t.float()
+        hq, hkv, d = cfg.heads, cfg.kv_heads, cfg.head_dim
+        b, lmax = len(prompts), max(len(p) for p in prompts) + 64
+        self.k = torch.zeros(cfg.layers, b, lmax, hkv, d, device=DEV)
+        self.v = torch.zeros_like(self.k)
+        self.len = [len(p) for p in prompts]
+        last = []
+        for i, p in enumerate(prompts):
+            t = len(p)
+            x = f(w.embed)[torch.tensor(p, device=DEV)]
+            cos, sin = self._angles(torch.arange(t, device=DEV))
+            mask = torch.full((t, t), float("-inf"), device=DEV).triu(1)
+            for l in range(cfg.layers):
+                q, k, v = self._qkv(x, l, cos, sin)
+                self.k[l, i, :t], self.v[l, i, :t] = k, v
+                kk, vv = k.repeat_interleave(hq // hkv, 1), v.repeat_interleave(hq // hkv, 1)
+                sc = torch.einsum("qhd,khd->hqk", q, kk) / math.sqrt(d) + mask
+                a = torch.einsum("hqk,khd->qhd", sc.softmax(-1), vv).reshape(t, hq * d)
+                x = self._mlp(x + a @ f(w.wo[l]).T, l)
+            last.append(x[-1:])
+        self.logits = self._head(torch.cat(last))
+
+    def _angles(self, pos):
+        ang = pos.float()[:, None] * self.inv[None, :]
+        return torch.cos(ang), torch.sin(ang)
+
+    def _norm(self, z, wt):
+        if self.cfg.norm == "layer":
+            return F.layer_norm(z, (z.shape[-1],), wt.float(), None, self.cfg.eps)
+        return z / torch.sqrt(z.pow(2).mean(-1, keepdim=True) + self.cfg.eps) * wt.float()
+
+    def _qkv(self, x, l, cos, sin):
+        c, w = self.cfg, self.w
+        hq, hkv, d = c.heads, c.kv_heads, c.head_dim
+        qkv = self._norm(x, w.ln1[l]) @ w.wqkv[l].float().T + w.bqkv[l].float()
+        t = x.shape[0]
+
+        def rope(z):
+            z1, z2 = z[..., :d // 2], z[..., d // 2:]
+            return torch.cat([z1 * cos[:, None] - z2 * sin[:, None],
+                              z2 * cos[:, None] + z1 * sin[:, None]], -1)
+        q = rope(qkv[:, :hq * d].view(t, hq, d))
+        k = rope(qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d))
+        return q, k, qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+
+    def _mlp(self, x, l):
+        c, w = self.cfg, self.w
+        gu = self._norm(x, w.ln2[l]) @ w.wgu[l].float().T
+        return x + (F.silu(gu[:, :c.inter]) * gu[:, c.inter:]) @ w.wd[l].float().T
+
+    def _head(self, x):
+        return self._norm(x, self.w.norm) @ self.w.embed.float().T
+
+    def step(self, tokens):
+        """Appends one token per sequence; returns the next logits [B, vocab]."""
+        c, w = self.cfg, self.w
+        hq, hkv, d = c.heads, c.kv_heads, c.head_dim
+        b = len(tokens)
+        pos = torch.tensor(self.len, device=DEV)
+        x = w.embed.float()[torch.tensor(tokens, device=DEV)]
+        cos, sin = self._angles(pos)
+        idx = torch.arange(b, device=DEV)
+        keep = torch.arange(self.k.shape[2], device=DEV)[None, :] <= pos[:, None]  # [B, L]
+        for l in range(c.layers):
+            q, k, v = self._qkv(x, l, cos, sin)
+            self.k[l, idx, pos], self.v[l, idx, pos] = k, v
+            kk = self.k[l].repeat_interleave(hq // hkv, 2)  # [B, L, hq, d]
+            vv = self.v[l].repeat_interleave(hq // hkv, 2)
+            sc = torch.einsum("bhd,blhd->bhl", q, kk) / math.sqrt(d)
+            sc = sc.masked_fill(~keep[:, None, :], float("-inf"))
+            a = torch.einsum("bhl,blhd->bhd", sc.softmax(-1), vv).reshape(b, hq * d)
+            x = self._mlp(x + a @ w.wo[l].float().T, l)
+        self.len = [n + 1 for n in self.len]
+        return self._head(x)
+
+
+def test_engine_config5_benchmark_workload(pa, qwen_weights):
+    # The benchmark's own workload at the config-5 architecture: 32 requests
+    # with prompts U[64, 512] of random ids, one prefill step (the tiled GEMM
+    # projections) then 32 decode steps on the fused, graph-free path,
+    # teacher-forced with the fp32 reference's greedy tokens; every step's
+    # logits against the reference (contexts up to ~545 tokens).
+    from vllm_lite_amd import e2e
+    cfg, w = qwen_weights
+    rng = np.random.default_rng(32)
+    prompts = [list(map(int, rng.integers(0, cfg.vocab, int(n))))
+               for n in rng.integers(64, 513, 32)]
+    steps = 32
+    eng = e2e.Engine(cfg, w, num_blocks=1400, device=DEV)
+    b = len(prompts)
+    blocks = [[eng.free.pop() for _ in range((len(p) + steps + 15) // 16)] for p in prompts]
+    lens = [len(p) for p in prompts]
+    eng.batch.prepare(eng.cache, lens, [0] * b, blocks)
+    toks = torch.tensor([x for p in prompts for x in p], dtype=torch.int64, device=DEV)
+    got = eng.forward(toks, torch.tensor(np.cumsum(lens) - 1, device=DEV))
+    ref = RefCache(cfg, w, eng.inv_freq, prompts)
+    refs = ref.logits
+    errs, cmin = [], []
+    for step in range(steps + 1):
+        errs.append(((got - refs).abs().max() / refs.abs().max()).item())
+        cmin.append(F.cosine_similarity(got, refs, dim=-1).min().item())
+        if step == steps:
+            break
+        nxt = refs.argmax(-1).tolist()
+        eng.batch.prepare(eng.cache, [1] * b, [n + step for n in lens], blocks)
+        got = eng.forward(torch.tensor(nxt, dtype=torch.int64, device=DEV), None)
+        refs = ref.step(nxt)
+    print("max rel logit error per step:", [round(e, 4) for e in errs], flush=True)
+    print("min cosine per step:", [round(c, 5) for c in cmin], flush=True)
+    assert min(cmin) > 0.995 and max(errs) < 0.05, (min(cmin), max(errs))
 
 
 def test_engine_config5_graph_matches_eager(pa, qwen_weights):

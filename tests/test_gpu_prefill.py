@@ -149,10 +149,12 @@ def test_config3_full_size(pa, oracle):
     # BASELINE config 3 at full size: 4 x 2048 new tokens on past
     # 0 / 512 / 1024 / 2048, 32 / 8 x 128, bf16; the persistent grid's
     # rounds and snake order run exactly as in the benchmark.
-    #  (1) Sampled query rows against the oracle: row i of sequence s is a
-    #      one-row sequence with past P_s + i over the same table.  Rows on
-    #      every 64-row tile diagonal edge (i % 64 in {0, 63}), both 32-row
-    #      wavefront halves, the first and the last row, and random rows.
+    #  (1) Whole 64-row query tiles (a workgroup's tile) against the oracle:
+    #      per sequence the first and the last tile and every eighth tile
+    #      (offset by the sequence), 6 of its 32 tiles, so every diagonal
+    #      position within the 64-key LDS tiles and both 32-row wavefront
+    #      halves are covered; 1536 rows in all.  Each tile is a 64-row
+    #      sequence with past P_s + 64 t over the same block table.
     #  (2) Every row against pa_decode over context P_s + i + 1 (the decode
     #      kernel is itself checked against the oracle): all 8192 x 32 rows.
     rng = np.random.default_rng(2)
@@ -163,19 +165,18 @@ def test_config3_full_size(pa, oracle):
     out = pa.prefill(to_dev(q), dk, dv, dbt, to_dev(cu), to_dev(past), chunk)
     got = oracle.bf16_to_f32(to_np(out))
 
-    rows = []  # (sequence, row)
+    tiles = []  # (sequence, tile)
     for s in range(4):
-        pick = {0, 1, 31, 32, 33, 2047, 2046}
-        pick |= {i for i in range(chunk) if i % 64 in (0, 63) and i % 256 < 64}
-        pick |= set(rng.integers(0, chunk, 12).tolist())
-        rows += [(s, i) for i in sorted(pick)]
-    sel = np.array([cu[s] + i for s, i in rows])
-    q1 = q[sel]
-    bt1 = bt[[s for s, _ in rows]]
-    past1 = np.array([pasts[s] + i for s, i in rows], np.int32)
-    ref = oracle.paged_attention(oracle.as_f32(q1), oracle.as_f32(kc), oracle.as_f32(vc), bt1,
-                                 np.arange(len(rows) + 1), past1, scale=1 / math.sqrt(128))
-    assert_close(got[sel], ref, BF16_ATOL, BF16_RTOL, "config 3 full, sampled rows vs oracle")
+        pick = {0, chunk // 64 - 1} | {t for t in range(chunk // 64) if t % 8 == s + 1}
+        tiles += [(s, t) for t in sorted(pick)]
+    sel = np.concatenate([cu[s] + 64 * t + np.arange(64) for s, t in tiles])
+    bt1 = bt[[s for s, _ in tiles]]
+    past1 = np.array([pasts[s] + 64 * t for s, t in tiles], np.int32)
+    ref = oracle.paged_attention(oracle.as_f32(q[sel]), oracle.as_f32(kc), oracle.as_f32(vc),
+                                 bt1, np.arange(0, 64 * len(tiles) + 1, 64), past1,
+                                 scale=1 / math.sqrt(128))
+    assert len(sel) == 1536
+    assert_close(got[sel], ref, BF16_ATOL, BF16_RTOL, "config 3 full, 64-row tiles vs oracle")
 
     seq = np.repeat(np.arange(4), chunk)
     ctx = (np.asarray(pasts)[seq] + np.tile(np.arange(chunk), 4) + 1).astype(np.int32)
