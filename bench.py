@@ -686,6 +686,19 @@ def main():
                 "avg_launch_us": round(t_attn * 1e6, 2)}
         flushed_legs(roof, w, max(args.steps, 20),
                      lambda x: w.alg_bytes / x / 1e9 / HBM_PEAK_GBS, args.no_flush)
+        if args.config == "decode-fp8":
+            # the same launch through pa_decode_fp8_flagged (the bench's
+            # finite values leave every block flag 0)
+            flags = torch.zeros(w.kc.shape[0], dtype=torch.uint8, device=DEV)
+
+            class WF:
+                def attend(self):
+                    w.pa.decode(w.q, w.kc, w.vc, w.bt, w.ctx_dev, w.max_ctx, scale=w.scale,
+                                out=w.out, workspace=w.ws, block_flags=flags)
+            WF().attend()
+            tf = time_attend(WF(), max(args.steps, 20))
+            roof["flagged_launch_us"] = round(tf * 1e6, 2)
+            roof["flagged_frac"] = round(w.alg_bytes / tf / 1e9 / HBM_PEAK_GBS, 4)
         if args.config == "splitk":
             roof["unique_block_gbs"] = round((w.unique_kv_bytes) / t_attn / 1e9, 1)
             # batch-order independence of the shared-prefix grouping

@@ -100,6 +100,23 @@ int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, uint8_t* k_
                                  int64_t key_stride, int64_t value_stride, int32_t src_dtype,
                                  pa_stream_t stream);
 
+/* pa_reshape_and_cache_fp8 that also keeps per-block flags for
+ * pa_decode_fp8_flagged: block_flags [num_blocks] (device, one byte per
+ * block) gets 1 at every block that receives a code the hardware E4M3
+ * conversion reads differently from the reference's decode (the NaN and
+ * +-inf codes the encoder gives non-finite input,
+ * crates/model/src/components/kv_cache_fp8.rs:143-212).  Flags are only
+ * ever set; the caller zeroes them (e.g. when it hands a block to a new
+ * sequence).  No reference counterpart: the reference decodes every code
+ * on the host. */
+int32_t pa_reshape_and_cache_fp8_flagged(const void* key, const void* value, uint8_t* k_cache,
+                                         uint8_t* v_cache, const int64_t* slot_mapping,
+                                         int32_t num_tokens, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t num_blocks,
+                                         int64_t key_stride, int64_t value_stride,
+                                         int32_t src_dtype, uint8_t* block_flags,
+                                         pa_stream_t stream);
+
 /* Build slot_mapping on the device from per-sequence block tables:
  *   slot_mapping[t] = block_tables[s, positions[t] / 16] * 16 + positions[t] % 16
  * for t in [cu_seq_tokens[s], cu_seq_tokens[s+1]).  A position whose block
@@ -221,6 +238,24 @@ int32_t pa_decode(void* out, const void* q, const void* k_cache, const void* v_c
                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                   float scale, void* workspace, size_t workspace_bytes, int32_t dtype,
                   pa_stream_t stream);
+
+/* pa_decode on FP8-E4M3 caches (dtype implied) whose blocks carry the flags
+ * of pa_reshape_and_cache_fp8_flagged: blocks whose flag is 0 are converted
+ * by the hardware (exact for every code but the flagged ones) without the
+ * per-code test pa_decode makes on every byte it streams; a partition that
+ * reads a flagged block is attended again with the reference's exact
+ * decode.  Same results as pa_decode as long as every code the flags
+ * describe was written through the flagged writer (a block written any
+ * other way with a NaN / inf code and flag 0 would read as the hardware
+ * conversion does).  block_flags [num_blocks], device.  Replaces the same
+ * reference functions as pa_decode. */
+int32_t pa_decode_fp8_flagged(void* out, const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* block_tables, int32_t max_blocks_per_seq,
+                              const int32_t* context_lens, int32_t max_context_len,
+                              int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t num_blocks, float scale, void* workspace,
+                              size_t workspace_bytes, const uint8_t* block_flags,
+                              pa_stream_t stream);
 
 /* pa_decode without a workspace argument and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate

@@ -333,3 +333,79 @@ def test_decode_fp8_config2_full_size(pa, oracle):
     case, kc, vc = fp8_decode_case(oracle, rng, 64, 32, 8, 128, [4096] * 64)
     got, ref = run_fp8_decode(pa, oracle, case, kc, vc)
     assert_close(got, ref, BF16_ATOL, BF16_RTOL, "fp8 config 2 full")
+
+
+def exotic_codes(c):
+    """Codes the hardware E4M3 conversion reads differently from the
+    reference's decode: exponent field 15, or exponent field 0 and a
+    nonzero byte."""
+    e = (c >> 3) & 0xF
+    return (e == 15) | ((e == 0) & (c != 0))
+
+
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+@pytest.mark.parametrize("h,d", [(8, 128), (3, 40)])
+def test_reshape_and_cache_fp8_flagged(pa, oracle, src, h, d):
+    # The flagged writer stores the same bytes as pa_reshape_and_cache_fp8
+    # and sets exactly the flags of the blocks that received a NaN / inf
+    # code (the values wide_values plants), leaving flags already set.
+    # (8, 128): the block-coalesced kernel, with one whole-block run of
+    # slots; (3, 40): the per-token kernel.
+    rng = np.random.default_rng(h + d)
+    t, nb = 77, 12
+    k = wide_values(rng, (t, h, d))
+    v = wide_values(rng, (t, h, d))
+    if src == "bf16":
+        dk, dv = to_dev(oracle.f32_to_bf16(k)), to_dev(oracle.f32_to_bf16(v))
+        k, v = oracle.bf16_to_f32(oracle.f32_to_bf16(k)), oracle.bf16_to_f32(oracle.f32_to_bf16(v))
+    else:
+        dk, dv = to_dev(k), to_dev(v)
+    slots = rng.permutation(nb * 16)[:t].astype(np.int64)
+    slots[16:32] = 5 * 16 + np.arange(16)      # tokens 16-31 fill block 5 in order
+    slots[3] = -1
+    run = (np.arange(t) >= 16) & (np.arange(t) < 32)
+    slots = np.where(np.isin(slots, slots[16:32]) & ~run, -1, slots)
+    kc, vc = pa.ops.new_cache(nb, h, d, torch.uint8, DEV)
+    kc2, vc2 = pa.ops.new_cache(nb, h, d, torch.uint8, DEV)
+    flags = torch.zeros(nb, dtype=torch.uint8, device=DEV)
+    flags[11] = 1                               # set before: stays set
+    pa.reshape_and_cache_fp8(dk, dv, kc, vc, to_dev(slots), block_flags=flags)
+    pa.reshape_and_cache_fp8(dk, dv, kc2, vc2, to_dev(slots))
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    codes_k, codes_v = oracle.fp8_encode(k), oracle.fp8_encode(v)
+    want = np.zeros(nb, np.uint8)
+    want[11] = 1
+    for i, s in enumerate(slots):
+        if 0 <= s < nb * 16 and (exotic_codes(codes_k[i]).any() or exotic_codes(codes_v[i]).any()):
+            want[s // 16] = 1
+    assert want.sum() >= 3
+    assert np.array_equal(to_np(flags), want)
+
+
+@pytest.mark.parametrize("B,ctx_hi", [(7, 3000), (64, 2048), (24, 6000)])
+def test_decode_fp8_flagged(pa, oracle, B, ctx_hi):
+    # pa_decode_fp8_flagged over the special-code caches of
+    # test_decode_fp8_special_codes with the flags of the blocks that hold
+    # them: bit-identical to pa_decode (whose per-code test finds the same
+    # partitions), hence the reference's NaN / inf pattern; with one more,
+    # needless flag the output is still the same.
+    rng = np.random.default_rng(B)
+    hq, hkv, d = 32, 8, 128
+    ctx = rng.integers(ctx_hi // 2, ctx_hi + 1, B).astype(np.int32)
+    ctx[6] = ctx_hi - 5
+    case, kc, vc = fp8_decode_case(oracle, rng, B, hq, hkv, d, ctx)
+    plant_codes(rng, kc, vc, case["block_tables"], ctx, hkv, d)
+    nb = kc.shape[0]
+    flags = (exotic_codes(kc).reshape(nb, -1).any(1) |
+             exotic_codes(vc).reshape(nb, -1).any(1)).astype(np.uint8)
+    assert flags.sum() > 0
+    q, bt = to_dev(case["q"]), to_dev(case["block_tables"])
+    dk, dv, dctx = to_dev(kc), to_dev(oracle.v_from_ref(vc)), to_dev(ctx)
+    plain = pa.decode(q, dk, dv, bt, dctx, int(ctx.max()))
+    flagged = pa.decode(q, dk, dv, bt, dctx, int(ctx.max()), block_flags=to_dev(flags))
+    assert torch.equal(plain.view(torch.int16), flagged.view(torch.int16))
+    _, ref = run_fp8_decode(pa, oracle, case, kc, vc)
+    assert_same_specials(oracle.bf16_to_f32(to_np(flagged)), ref, f"fp8 flagged B {B}")
+    flags[case["block_tables"][1, 0]] = 1
+    again = pa.decode(q, dk, dv, bt, dctx, int(ctx.max()), block_flags=to_dev(flags))
+    assert torch.equal(plain.view(torch.int16), again.view(torch.int16))

@@ -19,6 +19,10 @@ SIGNATURES = {
     "pa_read_kv": (_i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p, _i32, _p]),
     "pa_block_hash": (_i32, [_p, _p, _i32, _i32, _i32, _i32, _p, _p]),
     "pa_decode_workspace_size": (_sz, [_i32, _i32, _i32, _i32]),
+    "pa_reshape_and_cache_fp8_flagged": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32,
+                                                 _i64, _i64, _i32, _p, _p]),
+    "pa_decode_fp8_flagged": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32,
+                                      _i32, _f32, _p, _sz, _p, _p]),
     "pa_decode": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
                          _p, _sz, _i32, _p]),
     "pa_decode_noalloc": (_i32, [_p, _p, _p, _p, _p, _i32, _p, _i32, _i32, _i32, _i32, _i32,

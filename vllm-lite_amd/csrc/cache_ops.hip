@@ -70,7 +70,7 @@ template <typename T, int VEC>
 __global__ __launch_bounds__(256) void reshape_and_cache_fp8_kernel(
     const T* __restrict__ key, const T* __restrict__ value, uint8_t* __restrict__ k_cache,
     uint8_t* __restrict__ v_cache, const int64_t* __restrict__ slots, int H, int D,
-    int64_t num_slots, int64_t key_stride, int64_t value_stride) {
+    int64_t num_slots, int64_t key_stride, int64_t value_stride, uint8_t* __restrict__ flags) {
   const int t = blockIdx.x;
   const int64_t slot = slots[t];
   if (slot < 0 || slot >= num_slots) return;
@@ -85,11 +85,15 @@ __global__ __launch_bounds__(256) void reshape_and_cache_fp8_kernel(
     uint8_t* kd = k_cache + ((blk * H + h) * kBlock + off) * (int64_t)D + d0;
     uint8_t* vd = v_cache + ((blk * H + h) * (int64_t)D + d0) * kBlock + off;
     uint8_t kb[VEC];
+    uint32_t ex = 0;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
       kb[e] = fp8_encode(Elem<T>::load(ks + e));
-      vd[e * kBlock] = fp8_encode(Elem<T>::load(vs + e));
+      const uint8_t vb = fp8_encode(Elem<T>::load(vs + e));
+      vd[e * kBlock] = vb;
+      ex |= fp8_exotic_bits((uint32_t)kb[e] | ((uint32_t)vb << 8));
     }
+    if (flags && (ex & 0x8080u)) flags[blk] = 1;
     if constexpr (VEC == 8) {
       *reinterpret_cast<uint2*>(kd) = *reinterpret_cast<const uint2*>(kb);
     } else {
@@ -151,11 +155,27 @@ __device__ inline void store_unit(TC* __restrict__ p, const Unit8<TS, TC>& u) {
   }
 }
 
+// FP8 units: whether the K or V unit holds a code the hardware conversion
+// reads differently from the reference (encoded from NaN / inf input); the
+// flagged write records its block for pa_decode_fp8_flagged.
+template <typename TS, typename TC>
+__device__ inline bool unit_exotic(const Unit8<TS, TC>& k, const Unit8<TS, TC>& v) {
+  if constexpr (sizeof(TC) == 1) {
+    uint32_t w[4];
+    __builtin_memcpy(w, k.v, 8);
+    __builtin_memcpy(w + 2, v.v, 8);
+    return ((fp8_exotic_bits(w[0]) | fp8_exotic_bits(w[1]) | fp8_exotic_bits(w[2]) |
+             fp8_exotic_bits(w[3])) & 0x80808080u) != 0;
+  } else {
+    return false;
+  }
+}
+
 template <typename TS, typename TC>
 __global__ __launch_bounds__(256) void cache_write_kernel(
     const TS* __restrict__ key, const TS* __restrict__ value, TC* __restrict__ k_cache,
     TC* __restrict__ v_cache, const int64_t* __restrict__ slots, int T, int H, int D,
-    int64_t num_slots, int64_t key_stride, int64_t value_stride) {
+    int64_t num_slots, int64_t key_stride, int64_t value_stride, uint8_t* __restrict__ flags) {
   __shared__ int range_start[2];  // full-block range of this workgroup / of g + 1, or -1
   __shared__ __align__(16) TC vt[kBlock * 512];
   const int tid = threadIdx.x;
@@ -190,9 +210,12 @@ __global__ __launch_bounds__(256) void cache_write_kernel(
     for (int i = tid; i < kBlock * units; i += blockDim.x) {
       const int u = i % units, j = i / units;
       const int64_t src = (int64_t)(r0 + j) * key_stride + (int64_t)h * D + 8 * u;
-      store_unit<TS, TC>(kd + j * D + 8 * u, load_unit<TS, TC>(key + src));
+      const Unit8<TS, TC> ku = load_unit<TS, TC>(key + src);
+      store_unit<TS, TC>(kd + j * D + 8 * u, ku);
       const int64_t vsrc = (int64_t)(r0 + j) * value_stride + (int64_t)h * D + 8 * u;
-      store_unit<TS, TC>(vt + j * D + 8 * u, load_unit<TS, TC>(value + vsrc));
+      const Unit8<TS, TC> vu = load_unit<TS, TC>(value + vsrc);
+      store_unit<TS, TC>(vt + j * D + 8 * u, vu);
+      if (flags && unit_exotic(ku, vu)) flags[blk] = 1;
     }
     __syncthreads();
     TC* vd = v_cache + (blk * H + h) * (int64_t)D * kBlock;
@@ -217,10 +240,12 @@ __global__ __launch_bounds__(256) void cache_write_kernel(
     if (slot < 0 || slot >= num_slots) continue;
     const int64_t blk = slot / kBlock;
     const int off = (int)(slot % kBlock);
-    store_unit<TS, TC>(k_cache + ((blk * H + h) * kBlock + off) * (int64_t)D + 8 * u,
-                       load_unit<TS, TC>(key + (int64_t)t * key_stride + (int64_t)h * D + 8 * u));
+    const Unit8<TS, TC> ku =
+        load_unit<TS, TC>(key + (int64_t)t * key_stride + (int64_t)h * D + 8 * u);
+    store_unit<TS, TC>(k_cache + ((blk * H + h) * kBlock + off) * (int64_t)D + 8 * u, ku);
     const Unit8<TS, TC> vv =
         load_unit<TS, TC>(value + (int64_t)t * value_stride + (int64_t)h * D + 8 * u);
+    if (flags && unit_exotic(ku, vv)) flags[blk] = 1;
     TC* vd = v_cache + ((blk * H + h) * (int64_t)D + 8 * u) * kBlock + off;
 #pragma unroll
     for (int e = 0; e < 8; ++e) vd[e * kBlock] = vv.v[e];
@@ -419,11 +444,12 @@ extern "C" int32_t pa_reshape_and_cache(const void* key, const void* value, void
     if (dtype == PA_DTYPE_BF16)
       cache_write_kernel<uint16_t, uint16_t><<<wgrid, block, 0, s>>>(
           (const uint16_t*)key, (const uint16_t*)value, (uint16_t*)k_cache, (uint16_t*)v_cache,
-          slot_mapping, num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride);
+          slot_mapping, num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride,
+          nullptr);
     else
       cache_write_kernel<float, float><<<wgrid, block, 0, s>>>(
           (const float*)key, (const float*)value, (float*)k_cache, (float*)v_cache, slot_mapping,
-          num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride);
+          num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride, nullptr);
     return check_launch("pa_reshape_and_cache");
   }
   if (dtype == PA_DTYPE_BF16) {
@@ -452,12 +478,12 @@ extern "C" int32_t pa_reshape_and_cache(const void* key, const void* value, void
   return check_launch("pa_reshape_and_cache");
 }
 
-extern "C" int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, uint8_t* k_cache,
-                                            uint8_t* v_cache, const int64_t* slot_mapping,
-                                            int32_t num_tokens, int32_t num_kv_heads,
-                                            int32_t head_dim, int32_t num_blocks,
-                                            int64_t key_stride, int64_t value_stride,
-                                            int32_t src_dtype, pa_stream_t stream) {
+namespace {
+int32_t reshape_and_cache_fp8_impl(const void* key, const void* value, uint8_t* k_cache,
+                                   uint8_t* v_cache, const int64_t* slot_mapping,
+                                   int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                                   int32_t num_blocks, int64_t key_stride, int64_t value_stride,
+                                   int32_t src_dtype, uint8_t* flags, pa_stream_t stream) {
   clear_error();
   PA_REQUIRE(dtype_ok(src_dtype), PA_ERR_INVALID_ARG,
              "pa_reshape_and_cache_fp8: source dtype %d is not f32 or bf16", src_dtype);
@@ -484,17 +510,17 @@ extern "C" int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, 
     if (src_dtype == PA_DTYPE_BF16)
       cache_write_kernel<uint16_t, uint8_t><<<wgrid, block, 0, s>>>(
           (const uint16_t*)key, (const uint16_t*)value, k_cache, v_cache, slot_mapping,
-          num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride);
+          num_tokens, num_kv_heads, head_dim, num_slots, key_stride, value_stride, flags);
     else
       cache_write_kernel<float, uint8_t><<<wgrid, block, 0, s>>>(
           (const float*)key, (const float*)value, k_cache, v_cache, slot_mapping, num_tokens,
-          num_kv_heads, head_dim, num_slots, key_stride, value_stride);
+          num_kv_heads, head_dim, num_slots, key_stride, value_stride, flags);
     return check_launch("pa_reshape_and_cache_fp8");
   }
 #define PA_LAUNCH_Q(T, V)                                                                    \
   reshape_and_cache_fp8_kernel<T, V><<<grid, block, 0, s>>>(                                 \
       (const T*)key, (const T*)value, k_cache, v_cache, slot_mapping, num_kv_heads, head_dim, \
-      num_slots, key_stride, value_stride)
+      num_slots, key_stride, value_stride, flags)
   if (src_dtype == PA_DTYPE_BF16) {
     if (vec)
       PA_LAUNCH_Q(uint16_t, 8);
@@ -508,6 +534,33 @@ extern "C" int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, 
   }
 #undef PA_LAUNCH_Q
   return check_launch("pa_reshape_and_cache_fp8");
+}
+}  // namespace
+
+extern "C" int32_t pa_reshape_and_cache_fp8(const void* key, const void* value, uint8_t* k_cache,
+                                            uint8_t* v_cache, const int64_t* slot_mapping,
+                                            int32_t num_tokens, int32_t num_kv_heads,
+                                            int32_t head_dim, int32_t num_blocks,
+                                            int64_t key_stride, int64_t value_stride,
+                                            int32_t src_dtype, pa_stream_t stream) {
+  return reshape_and_cache_fp8_impl(key, value, k_cache, v_cache, slot_mapping, num_tokens,
+                                    num_kv_heads, head_dim, num_blocks, key_stride, value_stride,
+                                    src_dtype, nullptr, stream);
+}
+
+extern "C" int32_t pa_reshape_and_cache_fp8_flagged(
+    const void* key, const void* value, uint8_t* k_cache, uint8_t* v_cache,
+    const int64_t* slot_mapping, int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+    int32_t num_blocks, int64_t key_stride, int64_t value_stride, int32_t src_dtype,
+    uint8_t* block_flags, pa_stream_t stream) {
+  if (!block_flags) {
+    clear_error();
+    set_error("pa_reshape_and_cache_fp8_flagged: null block_flags");
+    return PA_ERR_INVALID_ARG;
+  }
+  return reshape_and_cache_fp8_impl(key, value, k_cache, v_cache, slot_mapping, num_tokens,
+                                    num_kv_heads, head_dim, num_blocks, key_stride, value_stride,
+                                    src_dtype, block_flags, stream);
 }
 
 extern "C" int32_t pa_slot_mapping(const int32_t* block_tables, int32_t max_blocks_per_seq,

@@ -138,7 +138,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
     float scale_log2, int num_parts, int part_len, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, int64_t q_row) {
+    float* __restrict__ ws_ml, int64_t q_row, const uint8_t* /* FP8 flags, unused */) {
   constexpr int KS = D / 32;  // QK reduction steps
   constexpr int DT = D / 16;  // PV output tiles
   // NW > 1: the workgroup's wavefronts take partitions blockIdx.x * NW + w
@@ -365,6 +365,7 @@ struct Fp8Partition {
   const int32_t* btab;  // the partition's first block-table entry
   int Hkv, kvh, num_blocks, tok0, tok_end, nblk, c, j;
   float scale_log2;
+  const uint8_t* flags;  // per-block exotic-code flags (pa_decode_fp8_flagged), or null
 
   // The online-softmax state of a lane.
   struct State {
@@ -376,6 +377,7 @@ struct Fp8Partition {
     u32x4 k0[KS / 2], k1[KS / 2];  // 16 bytes = two reduction steps, token tk0 / tk0 + 4
     uint64_t v[DT];
     int lim0, lim1;
+    uint32_t f;  // the two blocks' flags (flagged launches)
   };
 
   __device__ void init(State& s) const {
@@ -401,6 +403,7 @@ struct Fp8Partition {
                  : "s"(tab), "s"(__builtin_amdgcn_readfirstlane(idx * 4)));
     return v;
   }
+  template <bool FLAGGED = false>
   __device__ void load_step(int ib, Step& st) const {
     const int64_t head_stride = (int64_t)kBlock * D;  // bytes per (block, head)
     const bool k_second = (c >> 3) != 0;              // this lane's K rows are in block 1
@@ -430,6 +433,10 @@ struct Fp8Partition {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
       st.v[dt] = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(vr + dt * 16 * kBlock));
+    // the blocks' flag bytes arrive with the step's K / V (no round trip of
+    // their own); an id outside the pool reads block 0's flag (at worst a
+    // needless exact pass)
+    if constexpr (FLAGGED) st.f = (uint32_t)flags[b0] | (uint32_t)flags[b1];
   }
   template <bool EXACT>
   __device__ void compute_step(Step& st, const bf16x8 (&qv)[KS], State& S) const {
@@ -520,13 +527,20 @@ __device__ __attribute__((noinline)) typename Fp8Partition<D>::State fp8_exact_p
   return S;
 }
 
-template <int D, int NW>
+// FLAGGED: the caller keeps per-block flags of the blocks that hold such
+// codes (block_flags, written by pa_reshape_and_cache_fp8_flagged); the
+// streaming loop then tests no codes, it ORs the step's two flag bytes, and
+// a wavefront that read a flagged block takes the exact pass.  (Measured on
+// the config-2 shape: 85.5 us against 88.9 us with the per-code test; with
+// the test gone, two to four steps in flight at two or three wavefronts per
+// SIMD, 512- or 1024-token partitions: 89.7-94.6 us.)
+template <int D, int NW, bool FLAGGED>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1))) void decode_fp8_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
     const uint8_t* __restrict__ vc, const int32_t* __restrict__ block_tables, int mbs,
     const int32_t* __restrict__ context_lens, int Hq, int Hkv, int G, int num_blocks,
     float scale_log2, int num_parts, int part_len, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, int64_t q_row) {
+    float* __restrict__ ws_ml, int64_t q_row, const uint8_t* __restrict__ block_flags) {
   using Part = Fp8Partition<D>;
   constexpr int KS = Part::KS;
   constexpr int DT = Part::DT;
@@ -551,7 +565,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 12
   const int tok_end = empty ? tok0 : min(ctx, tok0 + part_len);
   const Part P{kc, vc, block_tables + (int64_t)seq * mbs + tok0 / kBlock, Hkv, kvh, num_blocks,
                tok0, tok_end, (tok_end - tok0 + kBlock - 1) / kBlock /* 0 when empty */, c, j,
-               scale_log2};
+               scale_log2, block_flags};
 
   const int head = kvh * G + c;
   const uint16_t* qrow = c < G ? q + (int64_t)seq * q_row + (int64_t)head * D : nullptr;
@@ -579,15 +593,19 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 12
   // per SIMD measured slower, their extra VALU work less hidden.
   typename Part::Step st;
   for (int ib = 0; ib < P.nblk; ib += 2) {
-    P.load_step(ib, st);
+    P.template load_step<FLAGGED>(ib, st);
+    if constexpr (FLAGGED) {
+      exotic |= st.f << 7;
+    } else {
 #pragma unroll
-    for (int s = 0; s < KS / 2; ++s)
+      for (int s = 0; s < KS / 2; ++s)
 #pragma unroll
-      for (int h = 0; h < 4; ++h)
-        exotic |= fp8_exotic_bits(st.k0[s][h]) | fp8_exotic_bits(st.k1[s][h]);
+        for (int h = 0; h < 4; ++h)
+          exotic |= fp8_exotic_bits(st.k0[s][h]) | fp8_exotic_bits(st.k1[s][h]);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      exotic |= fp8_exotic_bits((uint32_t)st.v[dt]) | fp8_exotic_bits((uint32_t)(st.v[dt] >> 32));
+      for (int dt = 0; dt < DT; ++dt)
+        exotic |= fp8_exotic_bits((uint32_t)st.v[dt]) | fp8_exotic_bits((uint32_t)(st.v[dt] >> 32));
+    }
     P.template compute_step<false>(st, qv, S);
   }
   if (__builtin_amdgcn_ballot_w64((exotic & 0x80808080u) != 0)) S = fp8_exact_pass<D>(P, qrow);
@@ -1567,7 +1585,8 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
                     int32_t max_blocks_per_seq, const int32_t* context_lens,
                     int32_t max_context_len, int32_t num_seqs, int32_t num_heads,
                     int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks, float scale,
-                    void* workspace, size_t workspace_bytes, int32_t dtype, pa_stream_t stream, int64_t q_row = 0) {
+                    void* workspace, size_t workspace_bytes, int32_t dtype, pa_stream_t stream, int64_t q_row = 0,
+                    const uint8_t* block_flags = nullptr) {
   clear_error();
   PA_REQUIRE(dtype_ok(dtype) || dtype == PA_DTYPE_FP8_E4M3, PA_ERR_INVALID_ARG,
              "pa_decode: unknown dtype %d", dtype);
@@ -1629,36 +1648,43 @@ int32_t decode_impl(void* out, const void* q, const void* k_cache, const void* v
     const dim3 grid(merge_waves > 1 ? 1 : np, num_kv_heads, num_seqs);
     auto* o = (uint16_t*)out;
     auto* qq = (const uint16_t*)q;
-#define PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, NW)                                                 \
-  KERNEL<DD, NW><<<grid, 64 * NW, 0, s>>>(                                                    \
+#define PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, NW, ...)                                            \
+  KERNEL<DD, NW __VA_ARGS__><<<grid, 64 * NW, 0, s>>>(                                                    \
       o, qq, (const TC*)k_cache, (const TC*)v_cache, block_tables, max_blocks_per_seq,        \
       context_lens, num_heads, num_kv_heads, G, num_blocks, scale_log2, np, part_len, ws_o,   \
-      ws_ml, q_row)
-#define PA_LAUNCH_MFMA(KERNEL, TC, DD)                                                        \
+      ws_ml, q_row, block_flags)
+#define PA_LAUNCH_MFMA(KERNEL, TC, DD, ...)                                                   \
   do {                                                                                        \
     if (merge_waves == 2)                                                                     \
-      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 2);                                                   \
+      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 2, __VA_ARGS__);                                      \
     else if (merge_waves == 4)                                                                \
-      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 4);                                                   \
+      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 4, __VA_ARGS__);                                      \
     else if (merge_waves == 8)                                                                \
-      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, (DD <= 128 ? 8 : 4));                                 \
+      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, (DD <= 128 ? 8 : 4), __VA_ARGS__);                    \
     else                                                                                      \
-      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 1);                                                   \
+      PA_LAUNCH_MFMA_NW(KERNEL, TC, DD, 1, __VA_ARGS__);                                      \
   } while (0)
-    if (fp8) {
+    if (fp8 && block_flags) {
       if (head_dim == 64)
-        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 64);
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 64, , true);
       else if (head_dim == 128)
-        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 128);
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 128, , true);
       else
-        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 256);
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 256, , true);
+    } else if (fp8) {
+      if (head_dim == 64)
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 64, , false);
+      else if (head_dim == 128)
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 128, , false);
+      else
+        PA_LAUNCH_MFMA(decode_fp8_kernel, uint8_t, 256, , false);
     } else {
       if (head_dim == 64)
-        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 64);
+        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 64, );
       else if (head_dim == 128)
-        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 128);
+        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 128, );
       else
-        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 256);
+        PA_LAUNCH_MFMA(decode_mfma_kernel, uint16_t, 256, );
     }
 #undef PA_LAUNCH_MFMA
 #undef PA_LAUNCH_MFMA_NW
@@ -1732,6 +1758,25 @@ extern "C" int32_t pa_decode(void* out, const void* q, const void* k_cache, cons
   return decode_impl(out, q, k_cache, v_cache, nullptr, block_tables, max_blocks_per_seq,
                      context_lens, max_context_len, num_seqs, num_heads, num_kv_heads, head_dim,
                      num_blocks, scale, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" int32_t pa_decode_fp8_flagged(void* out, const void* q, const void* k_cache,
+                                         const void* v_cache, const int32_t* block_tables,
+                                         int32_t max_blocks_per_seq, const int32_t* context_lens,
+                                         int32_t max_context_len, int32_t num_seqs,
+                                         int32_t num_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t num_blocks, float scale,
+                                         void* workspace, size_t workspace_bytes,
+                                         const uint8_t* block_flags, pa_stream_t stream) {
+  if (!block_flags) {
+    clear_error();
+    set_error("pa_decode_fp8_flagged: null block_flags");
+    return PA_ERR_INVALID_ARG;
+  }
+  return decode_impl(out, q, k_cache, v_cache, nullptr, block_tables, max_blocks_per_seq,
+                     context_lens, max_context_len, num_seqs, num_heads, num_kv_heads, head_dim,
+                     num_blocks, scale, workspace, workspace_bytes, PA_DTYPE_FP8_E4M3, stream, 0,
+                     block_flags);
 }
 
 extern "C" int32_t pa_decode_quantized(void* out, const void* q, const float* k_cache,

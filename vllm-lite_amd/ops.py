@@ -104,9 +104,11 @@ def _cache_code(k_cache, q=None):
     return _dtype_code(k_cache)
 
 
-def reshape_and_cache_fp8(key, value, k_cache, v_cache, slot_mapping):
+def reshape_and_cache_fp8(key, value, k_cache, v_cache, slot_mapping, block_flags=None):
     """Quantise key/value [T, H, D] (f32 or bf16) into uint8 FP8 caches at
-    slot_mapping [T] (int64), with the reference's E4M3 encoder."""
+    slot_mapping [T] (int64), with the reference's E4M3 encoder.
+    block_flags (uint8 [NB]): pa_reshape_and_cache_fp8_flagged, which also
+    sets the flag of every block that receives a NaN / inf code."""
     _dev(k_cache, v_cache, slot_mapping)
     nb, h, d = _cache_dims(k_cache, v_cache)
     if k_cache.dtype != torch.uint8:
@@ -119,9 +121,22 @@ def reshape_and_cache_fp8(key, value, k_cache, v_cache, slot_mapping):
     if not (_rows_ok(key, h, d) and _rows_ok(value, h, d)):
         raise ValueError("key/value rows must be contiguous [H, D], not overlapping")
     lib = _lib.load()
+    if block_flags is not None:
+        _flags(block_flags, nb)
+        _check("pa_reshape_and_cache_fp8_flagged", lib.pa_reshape_and_cache_fp8_flagged(
+            _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), t, h, d,
+            nb, key.stride(0), value.stride(0), _dtype_code(key), _ptr(block_flags),
+            _stream(k_cache)))
+        return
     _check("pa_reshape_and_cache_fp8", lib.pa_reshape_and_cache_fp8(
         _ptr(key), _ptr(value), _ptr(k_cache), _ptr(v_cache), _ptr(slot_mapping), t, h, d, nb,
         key.stride(0), value.stride(0), _dtype_code(key), _stream(k_cache)))
+
+
+def _flags(block_flags, nb):
+    _dev(block_flags)
+    if block_flags.dtype != torch.uint8 or block_flags.shape != (nb,):
+        raise ValueError("block_flags must be uint8 [num_blocks]")
 
 
 def slot_mapping(block_tables, positions, cu_seq_tokens):
@@ -173,9 +188,11 @@ def decode_workspace_size(num_seqs, num_heads, head_dim, max_context_len):
 
 
 def decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len, scale=None,
-           out=None, workspace=None, block_scales=None):
+           out=None, workspace=None, block_scales=None, block_flags=None):
     """Decode attention: q [B, Hq, D] -> out [B, Hq, D].  block_scales
-    (f32 [NB]) marks the f32 caches as quantised (pa_decode_quantized)."""
+    (f32 [NB]) marks the f32 caches as quantised (pa_decode_quantized);
+    block_flags (uint8 [NB]) FP8 caches written with flags
+    (pa_decode_fp8_flagged)."""
     _dev(q, k_cache, v_cache, block_tables, context_lens)
     nb, hkv, d = _cache_dims(k_cache, v_cache)
     b, hq, dq = q.shape
@@ -199,6 +216,15 @@ def decode(q, k_cache, v_cache, block_tables, context_lens, max_context_len, sca
             _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_scales),
             _ptr(block_tables), block_tables.shape[1], _ptr(context_lens), max_context_len, b, hq,
             hkv, d, nb, float(scale), _ptr(workspace), ws_bytes, _stream(q)))
+        return out
+    if block_flags is not None:
+        if k_cache.dtype != torch.uint8:
+            raise ValueError("block_flags are for FP8 caches")
+        _flags(block_flags, nb)
+        _check("pa_decode_fp8_flagged", lib.pa_decode_fp8_flagged(
+            _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
+            block_tables.shape[1], _ptr(context_lens), max_context_len, b, hq, hkv, d, nb,
+            float(scale), _ptr(workspace), ws_bytes, _ptr(block_flags), _stream(q)))
         return out
     _check("pa_decode", lib.pa_decode(
         _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
