@@ -602,7 +602,10 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int64_t* __restr
 // of 32 x 32 (v_mfma_f32_32x32x16_bf16), so the workgroup tile is
 // BM = 32 WM TM rows x BN = 32 WN TN weight rows, K in steps of BK.  Each
 // step's X and W tiles are copied HBM -> LDS with global_load_lds (no
-// register staging) into one of S buffers, S - 1 steps ahead of use.
+// register staging) into one of two buffers, one step ahead of use; the
+// grid is persistent (the LDS-resident workgroups of the GPU), and a
+// workgroup's steps run as one sequence over its tiles, so the next tile's
+// first copy is in flight during a tile's epilogue.
 // Operand reads: lane l = 32 g + n takes row n of a 32-row tile, k 8 g ..
 // 8 g + 7 of the MFMA's 16 (one 16-byte LDS read, which feeds TN or TM
 // MFMAs); the tiles' rows (2 BK bytes) hold their 16-byte k chunks
@@ -617,14 +620,28 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int64_t* __restr
 // a0 + BN/2 - 1 then the up rows N + a0 .. (a0 = BN/2 x the column tile),
 // wavefront wn takes its TN/2 gate tiles and the matching up tiles, and
 // out[m][a] = silu(bf16(g)) * bf16(u) (the exponential
-// is __expf); with add_out the result is added into
+// __expf, the reciprocal v_rcp_f32); with add_out the result is added into
 // out (out = bf16(out + bf16(y))).  Rows past M read row M - 1, weight rows
 // past N (EPI 0 / 1: N need not fill the last tile) read row N - 1, and
 // neither is stored.
-constexpr int kSkinnyMaxRows = 64;  // pa_linear's skinny kernel up to here
+constexpr int kSkinnyMaxRows = 64;
+// Compute units of the current device (cached per device).
+int gemm_compute_units() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}  // pa_linear's skinny kernel up to here
 constexpr int kGemmKMultiple = 64;  // K the tiled kernel takes: a multiple of this
 constexpr int kGemmGroupM = 4;  // row tiles per group of the tile order
-template <int EPI, int WM, int WN, int TM, int TN, int BK, int S>
+template <int EPI, int WM, int WN, int TM, int TN, int BK>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ bias, int M, int N, int K, int add_out, int ntm, int ntn) {
@@ -637,54 +654,64 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   constexpr int CA = BM / RPC / NW, CB = BN / RPC / NW;  // copy chunks per wavefront
   static_assert(CA * NW * RPC == BM && CB * NW * RPC == BN && (EPI != 2 || TN % 2 == 0),
                 "tiles");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_a[S][BM * RB];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_b[S][BN * RB];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a[2][BM * RB];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b[2][BN * RB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int n = lane & 31, g = lane >> 5;
-  // Tile order: workgroups are dealt round-robin to the 8 XCDs, so
-  // workgroup id maps to logical tile (id % 8) * per_xcd + id / 8 and each
-  // XCD takes a contiguous range of the order; the order goes through
-  // groups of kGemmGroupM row tiles, column tiles outer within a group, so
-  // the workgroups running together on an XCD share X rows and W rows in
-  // its L2.
+  // Persistent grid, tile order: workgroups are dealt round-robin to the 8
+  // XCDs; XCD x takes the contiguous range [x per_xcd, (x + 1) per_xcd) of
+  // the logical order, its workgroups (slots) taking every nslot-th tile of
+  // it, so the tiles in flight on an XCD are neighbours in the order.  The
+  // order goes through groups of kGemmGroupM row tiles, column tiles outer
+  // within a group, so those workgroups share X rows and W rows in the
+  // XCD's L2.
   const int total = ntm * ntn, per_xcd = (total + 7) / 8;
-  const int L = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-  if (L >= total) return;
-  const int grp = L / (kGemmGroupM * ntn), first_m = grp * kGemmGroupM;
-  const int gsz = min(kGemmGroupM, ntm - first_m);
-  const int tile_m = first_m + (L % (kGemmGroupM * ntn)) % gsz;
-  const int tile_n = (L % (kGemmGroupM * ntn)) / gsz;
-  const int m0 = tile_m * BM;
-  const int c0 = tile_n * (EPI == 2 ? BN / 2 : BN);  // first output column
+  const int xcd = (int)(blockIdx.x % 8), slot = (int)(blockIdx.x / 8);
+  const int nslot = (int)(gridDim.x / 8);
+  const int lo = xcd * per_xcd, hi = min(total, lo + per_xcd);
+  if (lo + slot >= hi) return;
+  const int my_tiles = (hi - 1 - lo - slot) / nslot + 1;
+  auto tile_origin = [&](int i, int& m0, int& c0) {
+    const int L = lo + slot + i * nslot;
+    const int grp = L / (kGemmGroupM * ntn), first_m = grp * kGemmGroupM;
+    const int gsz = min(kGemmGroupM, ntm - first_m);
+    const int r = L % (kGemmGroupM * ntn);
+    m0 = (first_m + r % gsz) * BM;
+    c0 = (r / gsz) * (EPI == 2 ? BN / 2 : BN);  // first output column
+  };
   auto swz = [](int r) -> int { return (r / (256 / RB)) % LPR; };
   // this wavefront's copies: RPC rows per 1 KB chunk; lane l fills chunk
   // position l % LPR of row l / LPR, i.e. source chunk (l % LPR) ^ swz(row)
-  const uint16_t* xsrc[CA];
-  const uint16_t* wsrc[CB];
+  int xr[CA], wr[CB], xch[CA], wch[CB];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
-    const int r = (CA * wave + i) * RPC + lane / LPR;
-    xsrc[i] = x + (int64_t)min(m0 + r, M - 1) * K + ((lane % LPR) ^ swz(r)) * 8;
+    xr[i] = (CA * wave + i) * RPC + lane / LPR;
+    xch[i] = ((lane % LPR) ^ swz(xr[i])) * 8;
   }
 #pragma unroll
   for (int i = 0; i < CB; ++i) {
-    const int r = (CB * wave + i) * RPC + lane / LPR;
-    const int wr = EPI == 2 ? (r < BN / 2 ? c0 + r : N + c0 + r - BN / 2) : min(c0 + r, N - 1);
-    wsrc[i] = w + (int64_t)wr * K + ((lane % LPR) ^ swz(r)) * 8;
+    wr[i] = (CB * wave + i) * RPC + lane / LPR;
+    wch[i] = ((lane % LPR) ^ swz(wr[i])) * 8;
   }
-  auto issue = [&](int kt, int buf) {
+  // copies of step kt of the wavefront's tile i into buffer buf
+  auto issue = [&](int i, int kt, int buf) {
+    int m0, c0;
+    tile_origin(i, m0, c0);
 #pragma unroll
-    for (int i = 0; i < CA; ++i)
+    for (int u = 0; u < CA; ++u)
       __builtin_amdgcn_global_load_lds(
-          (const void*)(xsrc[i] + kt * BK),
-          (__attribute__((address_space(3))) void*)&lds_a[buf][(CA * wave + i) * 1024], 16, 0, 0);
+          (const void*)(x + (int64_t)min(m0 + xr[u], M - 1) * K + xch[u] + kt * BK),
+          (__attribute__((address_space(3))) void*)&lds_a[buf][(CA * wave + u) * 1024], 16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < CB; ++i)
+    for (int u = 0; u < CB; ++u) {
+      const int r = wr[u];
+      const int row = EPI == 2 ? (r < BN / 2 ? c0 + r : N + c0 + r - BN / 2) : min(c0 + r, N - 1);
       __builtin_amdgcn_global_load_lds(
-          (const void*)(wsrc[i] + kt * BK),
-          (__attribute__((address_space(3))) void*)&lds_b[buf][(CB * wave + i) * 1024], 16, 0, 0);
+          (const void*)(w + (int64_t)row * K + wch[u] + kt * BK),
+          (__attribute__((address_space(3))) void*)&lds_b[buf][(CB * wave + u) * 1024], 16, 0, 0);
+    }
   };
   // LDS rows of this wavefront's operand tiles (SwiGLU: gate tiles, then
   // the matching up tiles)
@@ -703,45 +730,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     for (int b = 0; b < TN; ++b)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.f;
-  const int nk = K / BK;
-  // copies S - 1 steps ahead: before step kt, the copies of steps kt + 1 ..
-  // kt + S - 2 may still be in flight (CA + CB loads each)
-  constexpr int PER = CA + CB;
-  static_assert(PER * (S - 2) <= 63, "vmcnt range");
-  for (int t = 0; t < S - 1 && t < nk; ++t) issue(t, t);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt % S;
-    const int ahead = min(S - 2, nk - 1 - kt);  // later steps issued
-    if (ahead >= 2)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * PER) & 0xF) | (((2 * PER) >> 4) << 14));
-    else if (ahead == 1)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (PER & 0xF) | ((PER >> 4) << 14));
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-    // step kt has landed for every wavefront, and every wavefront is done
-    // with step kt - 1's buffer, which the copy of step kt + S - 1 reuses
-    __syncthreads();
-    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
-    const uint8_t* at = &lds_a[buf][0];
-    const uint8_t* bt = &lds_b[buf][0];
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      bf16x8 af[TM], bfr[TN];
-#pragma unroll
-      for (int t = 0; t < TM; ++t)
-        af[t] = *reinterpret_cast<const bf16x8*>(at + arow[t] * RB +
-                                                 (((2 * s + g) ^ swz(arow[t])) * 16));
-#pragma unroll
-      for (int t = 0; t < TN; ++t)
-        bfr[t] = *reinterpret_cast<const bf16x8*>(bt + brow[t] * RB +
-                                                  (((2 * s + g) ^ swz(brow[t])) * 16));
-#pragma unroll
-      for (int a = 0; a < TM; ++a)
-#pragma unroll
-        for (int b = 0; b < TN; ++b)
-          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[b], af[a], acc[a][b], 0, 0, 0);
-    }
-  }
+  // epilogue of the tile at (m0, c0)
+  auto store_tile = [&](int m0, int c0) {
   // epilogue: acc[a][b] is the transposed tile (W rows x X rows), so lane
   // (n, g) holds X row n and, in registers 4 q .. 4 q + 3, the four
   // consecutive output columns 8 q + 4 g .. 8 q + 4 g + 3 (one 8-byte store)
@@ -760,9 +750,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
           uint16_t v[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float gg = bf16_bits_to_f32(f32_to_bf16_bits(acc[a][b][4 * qd + e]));
-            const float uu = bf16_bits_to_f32(f32_to_bf16_bits(acc[a][b + TN / 2][4 * qd + e]));
-            v[e] = f32_to_bf16_bits(gg / (1.0f + __expf(-gg)) * uu);
+            const float gg = (float)(__bf16)acc[a][b][4 * qd + e];
+            const float uu = (float)(__bf16)acc[a][b + TN / 2][4 * qd + e];
+            v[e] = __builtin_bit_cast(
+                uint16_t, (__bf16)(gg * __builtin_amdgcn_rcpf(1.0f + __expf(-gg)) * uu));
           }
           *reinterpret_cast<uint64_t*>(orow + col) = *reinterpret_cast<const uint64_t*>(v);
         }
@@ -803,6 +794,51 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
             }
           }
         }
+    }
+  }
+  };
+  // The workgroup's steps run as one sequence over its tiles (step gs =
+  // step gs % nk of tile gs / nk, in buffer gs % 2), the copy of step gs + 1
+  // issued before step gs is computed -- across tile boundaries too, so the
+  // next tile's first copy is in flight during the epilogue.
+  const int nk = K / BK, nsteps = my_tiles * nk;
+  issue(0, 0, 0);
+  for (int gs = 0; gs < nsteps; ++gs) {
+    const int i = gs / nk, kt = gs - i * nk, buf = gs & 1;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step gs landed
+    // every wavefront's copies of step gs are visible, and every wavefront
+    // is done with step gs - 1's buffer, which step gs + 1's copy reuses
+    __syncthreads();
+    if (gs + 1 < nsteps) issue((gs + 1) / nk, (gs + 1) % nk, buf ^ 1);
+    const uint8_t* at = &lds_a[buf][0];
+    const uint8_t* bt = &lds_b[buf][0];
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      bf16x8 af[TM], bfr[TN];
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        af[t] = *reinterpret_cast<const bf16x8*>(at + arow[t] * RB +
+                                                 (((2 * s + g) ^ swz(arow[t])) * 16));
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        bfr[t] = *reinterpret_cast<const bf16x8*>(bt + brow[t] * RB +
+                                                  (((2 * s + g) ^ swz(brow[t])) * 16));
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[b], af[a], acc[a][b], 0, 0, 0);
+    }
+    if (kt == nk - 1) {
+      int m0, c0;
+      tile_origin(i, m0, c0);
+      store_tile(m0, c0);
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+          for (int q = 0; q < 16; ++q) acc[a][b][q] = 0.f;
     }
   }
 }
@@ -983,22 +1019,29 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
       // K steps of 64 through two LDS buffers (measured at the config-5
       // shapes against steps of 32 through 2, 3 or 4 buffers: equal for the
       // 256 x 256 tiles, 28.6 vs 33.6-36.4 us for the 128 x 128 ones)
-      constexpr int BK_ = 64, S_ = 2;
+      constexpr int BK_ = 64;
+      constexpr int WPC = WM_ * WN_ == 8 ? 1 : 2;  // workgroups per CU (LDS)
+      static_assert(WPC == 1 || WPC == 2, "");
       constexpr int BM_ = 32 * WM_ * TM_, BN_ = 32 * WN_ * TN_;
       const int ntn = act == PA_ACT_SILU_MUL ? out_features / (BN_ / 2)
                                              : (out_features + BN_ - 1) / BN_;
       const int ntm = (rows + BM_ - 1) / BM_;
       PA_REQUIRE((long long)ntm * ntn < (1ll << 30), PA_ERR_UNSUPPORTED, "pa_linear: %d rows",
                  rows);
-      const dim3 grid(8 * ((ntm * ntn + 7) / 8));
+      const int per_xcd = (ntm * ntn + 7) / 8;
+      // persistent for the large tiles (one workgroup per CU: its next
+      // tile's first copy overlaps the epilogue); a workgroup per tile for
+      // the small ones (two per CU: one's epilogue overlaps the other's loop)
+      const dim3 grid(8 * (WPC == 1 ? std::max(1, std::min(per_xcd, gemm_compute_units() / 8))
+                                    : per_xcd));
       if (act == PA_ACT_SILU_MUL)
-        gemm_tiled_kernel<2, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+        gemm_tiled_kernel<2, WM_, WN_, TM_, TN_, BK_><<<grid, 64 * WM_ * WN_, 0, s>>>(
             o, xx, ww, nullptr, rows, out_features, in_features, 0, ntm, ntn);
       else if (bias)
-        gemm_tiled_kernel<1, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+        gemm_tiled_kernel<1, WM_, WN_, TM_, TN_, BK_><<<grid, 64 * WM_ * WN_, 0, s>>>(
             o, xx, ww, bb, rows, out_features, in_features, add, ntm, ntn);
       else
-        gemm_tiled_kernel<0, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+        gemm_tiled_kernel<0, WM_, WN_, TM_, TN_, BK_><<<grid, 64 * WM_ * WN_, 0, s>>>(
             o, xx, ww, nullptr, rows, out_features, in_features, add, ntm, ntn);
       return PA_OK;
     };
