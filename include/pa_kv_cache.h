@@ -13,9 +13,14 @@
  * place of its `Err` results.  H here is the number of KV heads.
  *
  * Unlike the stateless entry points of pa.h, the cache allocates: the
- * caches themselves at creation and a small device staging buffer for block
- * ids / slots, grown on demand.  Index arguments marked "host" are read on
- * the host and validated before anything is enqueued.
+ * caches themselves at creation, a small device staging buffer for block
+ * ids / slots, grown on demand, and one host-mapped word for a single
+ * token's block hash.  Index arguments marked "host" are read on the host
+ * and validated before anything is enqueued.  Writes return after the
+ * stream has run them (their block hashes come back to the host); a
+ * read_kv over more than 16 blocks (or from a quantised cache) also waits
+ * for its index upload, a shorter one passes the ids in the kernel
+ * arguments and returns once the read is enqueued on `stream`.
  */
 #ifndef VLLM_LITE_AMD_PA_KV_CACHE_H
 #define VLLM_LITE_AMD_PA_KV_CACHE_H

@@ -5,6 +5,8 @@
 // elements in both source and cache; its V row is scattered into the
 // token-minor V block ([D, 16] per head), one element per 32 B (bf16) or
 // 64 B (f32) row of the block.
+#include <type_traits>
+
 #include "pa_common.hpp"
 #include "pa_internal.hpp"
 
@@ -297,15 +299,24 @@ __global__ void slot_mapping_kernel(const int32_t* __restrict__ block_tables, in
   }
 }
 
-// Gather: one workgroup per token.
-template <typename T>
+// Gather: one workgroup per token.  Ids: a device array, or (SmallIds, by
+// value in the kernel arguments) the few block ids of a short read, which
+// then needs no upload.
+struct SmallIds {
+  int32_t id[kSmallIds];
+};
+template <typename T, typename Ids>
 __global__ __launch_bounds__(256) void read_kv_kernel(const T* __restrict__ k_cache,
-                                                      const T* __restrict__ v_cache,
-                                                      const int32_t* __restrict__ block_ids, int H,
-                                                      int D, int num_blocks, T* __restrict__ out_k,
+                                                      const T* __restrict__ v_cache, Ids block_ids,
+                                                      int H, int D, int num_blocks,
+                                                      T* __restrict__ out_k,
                                                       T* __restrict__ out_v) {
   const int t = blockIdx.x;
-  const int32_t blk = block_ids[t / kBlock];
+  int32_t blk;
+  if constexpr (std::is_pointer_v<Ids>)
+    blk = block_ids[t / kBlock];
+  else
+    blk = block_ids.id[t / kBlock];
   const bool ok = blk >= 0 && blk < num_blocks;
   const int off = t % kBlock;
   for (int i = threadIdx.x; i < H * D; i += blockDim.x) {
@@ -317,6 +328,37 @@ __global__ __launch_bounds__(256) void read_kv_kernel(const T* __restrict__ k_ca
     }
     out_k[(int64_t)t * H * D + i] = kx;
     out_v[(int64_t)t * H * D + i] = vx;
+  }
+}
+
+// write_kv of one token (buffer.rs:103-267) in one launch: the hash of the K
+// block as it stands after the token (buffer.rs:263-264; the token's rows
+// from the input, the others from the cache), then the token's K row and V
+// entries stored; the hash goes to *hash_out (host-mapped memory, read after
+// the caller's synchronisation).
+template <typename T>
+__global__ __launch_bounds__(256) void write_token_kernel(T* __restrict__ k_cache,
+                                                          T* __restrict__ v_cache,
+                                                          const T* __restrict__ key,
+                                                          const T* __restrict__ value, int H,
+                                                          int D, int64_t blk, int off,
+                                                          uint64_t* __restrict__ hash_out) {
+  __shared__ uint64_t red[256];
+  const int n = H * kBlock * D;
+  const T* base = k_cache + blk * n;
+  const uint64_t h = workgroup_block_hash(
+      n,
+      [&](int e) -> float {
+        const int hd = e / (kBlock * D), r = e % (kBlock * D);
+        return r / D == off ? Elem<T>::load(key + (int64_t)hd * D + r % D)
+                            : Elem<T>::load(base + e);
+      },
+      red);  // ends with a barrier: every read of the block precedes the stores
+  if (threadIdx.x == 0) *hash_out = h;
+  for (int i = threadIdx.x; i < H * D; i += blockDim.x) {
+    const int hd = i / D, d = i % D;
+    k_cache[((blk * H + hd) * kBlock + off) * D + d] = key[i];
+    v_cache[((blk * H + hd) * D + d) * kBlock + off] = value[i];
   }
 }
 
@@ -390,6 +432,36 @@ __global__ __launch_bounds__(256) void block_hash_kernel(const float* __restrict
 }
 
 }  // namespace
+
+int32_t launch_write_token(void* k_cache, void* v_cache, const void* key, const void* value,
+                           int32_t dtype, int H, int D, int64_t blk, int off,
+                           uint64_t* hash_out, hipStream_t stream) {
+  if (dtype == PA_DTYPE_BF16)
+    write_token_kernel<uint16_t><<<1, 256, 0, stream>>>(
+        (uint16_t*)k_cache, (uint16_t*)v_cache, (const uint16_t*)key, (const uint16_t*)value, H,
+        D, blk, off, hash_out);
+  else
+    write_token_kernel<float><<<1, 256, 0, stream>>>((float*)k_cache, (float*)v_cache,
+                                                     (const float*)key, (const float*)value, H,
+                                                     D, blk, off, hash_out);
+  return check_launch("write_kv");
+}
+
+int32_t launch_read_kv_small(const void* k_cache, const void* v_cache, int32_t dtype,
+                             const int32_t* ids, int n_ids, int seq_len, int H, int D,
+                             int num_blocks, void* out_k, void* out_v, hipStream_t stream) {
+  SmallIds v{};
+  for (int i = 0; i < n_ids && i < kSmallIds; ++i) v.id[i] = ids[i];
+  if (dtype == PA_DTYPE_BF16)
+    read_kv_kernel<uint16_t, SmallIds><<<seq_len, 256, 0, stream>>>(
+        (const uint16_t*)k_cache, (const uint16_t*)v_cache, v, H, D, num_blocks,
+        (uint16_t*)out_k, (uint16_t*)out_v);
+  else
+    read_kv_kernel<float, SmallIds><<<seq_len, 256, 0, stream>>>(
+        (const float*)k_cache, (const float*)v_cache, v, H, D, num_blocks, (float*)out_k,
+        (float*)out_v);
+  return check_launch("read_kv");
+}
 
 int32_t launch_block_hash_replay(const void* k_cache, const void* key, int32_t dtype, int H,
                                  int D, int num_tasks, const int32_t* task_block,
@@ -598,13 +670,13 @@ extern "C" int32_t pa_read_kv(const void* k_cache, const void* v_cache, const in
         (const uint8_t*)k_cache, (const uint8_t*)v_cache, block_ids, num_kv_heads, head_dim,
         num_blocks, (float*)out_k, (float*)out_v);
   else if (dtype == PA_DTYPE_BF16)
-    read_kv_kernel<uint16_t><<<seq_len, 256, 0, s>>>(
+    read_kv_kernel<uint16_t, const int32_t*><<<seq_len, 256, 0, s>>>(
         (const uint16_t*)k_cache, (const uint16_t*)v_cache, block_ids, num_kv_heads, head_dim,
         num_blocks, (uint16_t*)out_k, (uint16_t*)out_v);
   else
-    read_kv_kernel<float><<<seq_len, 256, 0, s>>>((const float*)k_cache, (const float*)v_cache,
-                                                 block_ids, num_kv_heads, head_dim, num_blocks,
-                                                 (float*)out_k, (float*)out_v);
+    read_kv_kernel<float, const int32_t*><<<seq_len, 256, 0, s>>>(
+        (const float*)k_cache, (const float*)v_cache, block_ids, num_kv_heads, head_dim,
+        num_blocks, (float*)out_k, (float*)out_v);
   return check_launch("pa_read_kv");
 }
 

@@ -32,6 +32,25 @@ struct pa_kv_cache {
   void* host_stage = nullptr;
   void* dev_stage = nullptr;
   size_t stage_bytes = 0;
+  // One token's block hash, written by the device into host-mapped memory
+  // (write_kv of a single token: no index upload, no copy back).
+  uint64_t* hash_host = nullptr;
+  uint64_t* hash_dev = nullptr;
+
+  int32_t ensure_hash_slot() {
+    if (hash_host) return PA_OK;
+    void* h = nullptr;
+    void* d = nullptr;
+    if (hipHostMalloc(&h, 256, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+        hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+      if (h) (void)hipHostFree(h);
+      pa::set_error("pa_kv_cache: allocating the mapped hash slot failed");
+      return PA_ERR_HIP;
+    }
+    hash_host = (uint64_t*)h;
+    hash_dev = (uint64_t*)d;
+    return PA_OK;
+  }
 
   size_t layer_bytes() const {
     return (size_t)num_blocks * num_heads * pa::kBlock * head_dim * pa::dtype_size(dtype);
@@ -226,6 +245,7 @@ extern "C" void pa_kv_cache_destroy(pa_kv_cache* c) {
   for (void* p : c->value) (void)hipFree(p);
   for (float* p : c->scales) (void)hipFree(p);
   if (c->host_stage) (void)hipHostFree(c->host_stage);
+  if (c->hash_host) (void)hipHostFree(c->hash_host);
   if (c->dev_stage) (void)hipFree(c->dev_stage);
   delete c;
 }
@@ -263,7 +283,20 @@ extern "C" int32_t pa_kv_cache_write_kv(pa_kv_cache* c, int32_t layer, int64_t b
   PA_REQUIRE(token_offset >= 0 && token_offset < pa::kBlock, PA_ERR_OUT_OF_BOUNDS,
              "token_offset %lld out of bounds for block size %d", (long long)token_offset,
              pa::kBlock);
-  return scatter(c, layer, {block_id * pa::kBlock + token_offset}, k, v, (hipStream_t)stream);
+  hipStream_t s = (hipStream_t)stream;
+  if (!c->quantized) {
+    // one launch: the block's hash after the token, then the token's rows
+    int32_t rc = c->ensure_hash_slot();
+    if (rc != PA_OK) return rc;
+    rc = pa::launch_write_token(c->key[layer], c->value[layer], k, v, c->dtype, c->num_heads,
+                                c->head_dim, block_id, (int)token_offset, c->hash_dev, s);
+    rc = finish(s, rc);
+    if (rc != PA_OK) return rc;
+    const uint64_t h = *(volatile uint64_t*)c->hash_host;
+    c->block_hashes[layer][h] = block_id;
+    return PA_OK;
+  }
+  return scatter(c, layer, {block_id * pa::kBlock + token_offset}, k, v, s);
 }
 
 extern "C" int32_t pa_kv_cache_write_kv_batch(pa_kv_cache* c, int32_t layer, int64_t block_id,
@@ -347,6 +380,13 @@ extern "C" int32_t pa_kv_cache_read_kv(pa_kv_cache* c, int32_t layer, const int6
   }
   hipStream_t s = (hipStream_t)stream;
   int32_t rc = PA_OK;
+  if (!c->quantized && used <= pa::kSmallIds) {
+    // the ids go in the kernel arguments: no upload, so nothing to wait for
+    rc = pa::launch_read_kv_small(c->key[layer], c->value[layer], c->dtype, ids.data(), used, n,
+                                  c->num_heads, c->head_dim, c->num_blocks, out_k, out_v, s);
+    if (rc == PA_OK) *n_read = n;
+    return rc;
+  }
   void* d_ids = c->upload(ids.data(), ids.size() * sizeof(int32_t), s, &rc);
   if (rc != PA_OK) return rc;
   if (c->quantized)

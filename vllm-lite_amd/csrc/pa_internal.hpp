@@ -21,6 +21,17 @@ PA_HIDDEN int32_t launch_block_hash_replay(const void* k_cache, const void* key,
                                            const int32_t* task_block, const int32_t* task_beg,
                                            const int32_t* tok, const int32_t* off,
                                            uint64_t* hashes, hipStream_t stream);
+// write_kv of one token (non-quantised caches): block hash + store in one
+// launch, the hash into host-mapped *hash_out.
+PA_HIDDEN int32_t launch_write_token(void* k_cache, void* v_cache, const void* key,
+                                     const void* value, int32_t dtype, int H, int D, int64_t blk,
+                                     int off, uint64_t* hash_out, hipStream_t stream);
+// read_kv of at most kSmallIds blocks with the ids in the kernel arguments.
+constexpr int kSmallIds = 16;
+PA_HIDDEN int32_t launch_read_kv_small(const void* k_cache, const void* v_cache, int32_t dtype,
+                                       const int32_t* ids, int n_ids, int seq_len, int H, int D,
+                                       int num_blocks, void* out_k, void* out_v,
+                                       hipStream_t stream);
 PA_HIDDEN int32_t launch_quant_read(const float* k_cache, const float* v_cache,
                                     const float* scales, const int32_t* block_ids, int seq_len,
                                     int H, int D, float* out_k, float* out_v, hipStream_t stream);
