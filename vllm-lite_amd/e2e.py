@@ -90,7 +90,7 @@ class Weights:
     def pack(self, fold_rms=True):
         """Repacks the weights pa_linear reads (QKV as separate Q and K|V row
         blocks, O, gate|up, the tied embedding as LM head) into its fragment
-        layout; the row-major tensors stay for the hipBLASLt path.  fold_rms:
+        layout; the row-major tensors stay for the tiled GEMM of prompt chunks.  fold_rms:
         fold each RMSNorm weight into the columns of the projection after it
         (ln1 into Q and K|V, ln2 into gate|up, the final norm into the LM head),
         for the engine's fused decode step (pa_linear normalises its input

@@ -398,14 +398,6 @@ ACT_NONE, ACT_SILU_MUL = 0, 1
 LINEAR_RMS_IN, LINEAR_ADD_OUT = 1, 2
 
 
-def linear_supports(x, weight):
-    """Whether pa_linear takes these operands (bf16, K a multiple of 32, N a
-    multiple of 16; the fused gate|up weight has an even number of 16-row
-    halves whenever its N is a multiple of 32)."""
-    return (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and
-            x.shape[-1] % 32 == 0 and weight.shape[0] % 16 == 0)
-
-
 class PackedWeight:
     """A bf16 weight [N, K] repacked by pa_linear_pack (see pa_dense.h); pass
     it to linear() in place of the row-major tensor.  col_scale [K] (bf16):
