@@ -624,7 +624,27 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int64_t* __restr
 // out (out = bf16(out + bf16(y))).  Rows past M read row M - 1, weight rows
 // past N (EPI 0 / 1: N need not fill the last tile) read row N - 1, and
 // neither is stored.
+#ifndef PA_GEMM_BIG_BK
+#define PA_GEMM_BIG_BK 64
+#define PA_GEMM_BIG_S 2
+#define PA_GEMM_SMALL_BK 64
+#define PA_GEMM_SMALL_S 2
+#endif
 constexpr int kSkinnyMaxRows = 64;
+// HBM -> LDS copy of 16 bytes per lane (lane l's bytes land at lds + 16 l),
+// written out in assembly: with the builtin, the compiler cannot tell that
+// the operand reads which follow use the other LDS buffer, and makes them
+// wait for the copy (vmcnt(0) right after every copy, so no copy overlapped
+// any compute).  The kernel orders copies and reads itself (vmcnt(0) and a
+// barrier at the top of every step).
+__device__ inline void lds_copy16(const void* src, void* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(m0)
+               : "memory", "m0");
+}
 // Compute units of the current device (cached per device).
 int gemm_compute_units() {
   static int cached[64] = {0};
@@ -641,7 +661,7 @@ int gemm_compute_units() {
 }  // pa_linear's skinny kernel up to here
 constexpr int kGemmKMultiple = 64;  // K the tiled kernel takes: a multiple of this
 constexpr int kGemmGroupM = 4;  // row tiles per group of the tile order
-template <int EPI, int WM, int WN, int TM, int TN, int BK>
+template <int EPI, int WM, int WN, int TM, int TN, int BK, int S>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ bias, int M, int N, int K, int add_out, int ntm, int ntn) {
@@ -654,8 +674,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   constexpr int CA = BM / RPC / NW, CB = BN / RPC / NW;  // copy chunks per wavefront
   static_assert(CA * NW * RPC == BM && CB * NW * RPC == BN && (EPI != 2 || TN % 2 == 0),
                 "tiles");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_a[2][BM * RB];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds_b[2][BN * RB];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a[S][BM * RB];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b[S][BN * RB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -673,7 +693,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   const int lo = xcd * per_xcd, hi = min(total, lo + per_xcd);
   if (lo + slot >= hi) return;
   const int my_tiles = (hi - 1 - lo - slot) / nslot + 1;
-  auto tile_origin = [&](int i, int& m0, int& c0) {
+  auto tile_origin = [&](int i, int& m0, int& c0) __attribute__((always_inline)) {
     const int L = lo + slot + i * nslot;
     const int grp = L / (kGemmGroupM * ntn), first_m = grp * kGemmGroupM;
     const int gsz = min(kGemmGroupM, ntm - first_m);
@@ -695,23 +715,31 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     wr[i] = (CB * wave + i) * RPC + lane / LPR;
     wch[i] = ((lane % LPR) ^ swz(wr[i])) * 8;
   }
-  // copies of step kt of the wavefront's tile i into buffer buf
-  auto issue = [&](int i, int kt, int buf) {
+  // copies of step kt of the tile whose source rows are xs / ws into
+  // buffer BUF; the rows change only per tile (set_sources)
+  const uint16_t* xs[CA];
+  const uint16_t* ws[CB];
+  auto set_sources = [&](int i) __attribute__((always_inline)) {
     int m0, c0;
     tile_origin(i, m0, c0);
 #pragma unroll
-    for (int u = 0; u < CA; ++u)
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(x + (int64_t)min(m0 + xr[u], M - 1) * K + xch[u] + kt * BK),
-          (__attribute__((address_space(3))) void*)&lds_a[buf][(CA * wave + u) * 1024], 16, 0, 0);
+    for (int u = 0; u < CA; ++u) xs[u] = x + (int64_t)min(m0 + xr[u], M - 1) * K + xch[u];
 #pragma unroll
     for (int u = 0; u < CB; ++u) {
       const int r = wr[u];
       const int row = EPI == 2 ? (r < BN / 2 ? c0 + r : N + c0 + r - BN / 2) : min(c0 + r, N - 1);
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(w + (int64_t)row * K + wch[u] + kt * BK),
-          (__attribute__((address_space(3))) void*)&lds_b[buf][(CB * wave + u) * 1024], 16, 0, 0);
+      ws[u] = w + (int64_t)row * K + wch[u];
     }
+  };
+  auto issue = [&](int kt, int buf) __attribute__((always_inline)) {
+    uint8_t* la = lds_a[buf];
+    uint8_t* lb = lds_b[buf];
+#pragma unroll
+    for (int u = 0; u < CA; ++u)
+      lds_copy16(xs[u] + kt * BK, &la[(CA * wave + u) * 1024]);
+#pragma unroll
+    for (int u = 0; u < CB; ++u)
+      lds_copy16(ws[u] + kt * BK, &lb[(CB * wave + u) * 1024]);
   };
   // LDS rows of this wavefront's operand tiles (SwiGLU: gate tiles, then
   // the matching up tiles)
@@ -731,7 +759,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.f;
   // epilogue of the tile at (m0, c0)
-  auto store_tile = [&](int m0, int c0) {
+  auto store_tile = [&](int m0, int c0) __attribute__((always_inline)) {
   // epilogue: acc[a][b] is the transposed tile (W rows x X rows), so lane
   // (n, g) holds X row n and, in registers 4 q .. 4 q + 3, the four
   // consecutive output columns 8 q + 4 g .. 8 q + 4 g + 3 (one 8-byte store)
@@ -758,6 +786,29 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
           *reinterpret_cast<uint64_t*>(orow + col) = *reinterpret_cast<const uint64_t*>(v);
         }
     } else {
+      // every load of the epilogue is issued before any of its values is
+      // used (bias once for the tile, the residual row's values per row),
+      // so the round trips overlap instead of following one another
+      float bv[TN][4][4];
+#pragma unroll
+      for (int b = 0; b < TN; ++b)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int col = c0 + (wn * TN + b) * 32 + 8 * qd + 4 * g + e;
+            bv[b][qd][e] = EPI == 1 ? bf16_bits_to_f32(bias[min(col, N - 1)]) : 0.f;
+          }
+      uint64_t ow[TN][4];
+      if (add_out && vec) {
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            const int col = c0 + (wn * TN + b) * 32 + 8 * qd + 4 * g;
+            ow[b][qd] = col < N ? *reinterpret_cast<const uint64_t*>(orow + col) : 0;
+          }
+      }
 #pragma unroll
       for (int b = 0; b < TN; ++b)
 #pragma unroll
@@ -766,19 +817,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
           if (col >= N) continue;
           float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = acc[a][b][4 * qd + e];
+          for (int e = 0; e < 4; ++e) y[e] = acc[a][b][4 * qd + e] + bv[b][qd][e];
           if (vec) {
-            if constexpr (EPI == 1) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) y[e] += bf16_bits_to_f32(bias[col + e]);
-            }
-            uint64_t ow = add_out ? *reinterpret_cast<const uint64_t*>(orow + col) : 0;
             uint16_t v[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               float t = y[e];
               if (add_out)
-                t = bf16_bits_to_f32((uint16_t)(ow >> (16 * e))) +
+                t = bf16_bits_to_f32((uint16_t)(ow[b][qd] >> (16 * e))) +
                     bf16_bits_to_f32(f32_to_bf16_bits(t));
               v[e] = f32_to_bf16_bits(t);
             }
@@ -788,7 +834,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
             for (int e = 0; e < 4; ++e) {
               if (col + e >= N) continue;
               float t = y[e];
-              if constexpr (EPI == 1) t += bf16_bits_to_f32(bias[col + e]);
               if (add_out) t = bf16_bits_to_f32(orow[col + e]) + bf16_bits_to_f32(f32_to_bf16_bits(t));
               orow[col + e] = f32_to_bf16_bits(t);
             }
@@ -802,16 +847,40 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
   // issued before step gs is computed -- across tile boundaries too, so the
   // next tile's first copy is in flight during the epilogue.
   const int nk = K / BK, nsteps = my_tiles * nk;
-  issue(0, 0, 0);
+  // Copies run S - 1 steps ahead: before step gs computes, the copies of
+  // steps gs + 1 .. gs + S - 2 may still be in flight (CA + CB loads each).
+  constexpr int PER = CA + CB;
+  static_assert(PER * (S - 2) <= 63 && S >= 2 && S <= 4, "vmcnt range");
+  int cur = 0;      // tile of the step being computed
+  int iss = 0;      // next step to copy, and its tile / step within the tile
+  int iss_tile = 0, iss_kt = 0;
+  set_sources(0);
+  auto issue_next = [&]() __attribute__((always_inline)) {
+    if (iss_kt == nk) {  // the step starts the next tile
+      ++iss_tile;
+      iss_kt = 0;
+      set_sources(iss_tile);
+    }
+    issue(iss_kt, iss % S);
+    ++iss;
+    ++iss_kt;
+  };
+  for (int t = 0; t < S - 1 && t < nsteps; ++t) issue_next();
   for (int gs = 0; gs < nsteps; ++gs) {
-    const int i = gs / nk, kt = gs - i * nk, buf = gs & 1;
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): step gs landed
-    // every wavefront's copies of step gs are visible, and every wavefront
-    // is done with step gs - 1's buffer, which step gs + 1's copy reuses
+    const int kt = gs - cur * nk;
+    const int ahead = iss - 1 - gs;  // copies of later steps in flight
+    if (ahead >= 2)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * PER) & 0xF) | (((2 * PER) >> 4) << 14));
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (PER & 0xF) | ((PER >> 4) << 14));
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // step gs has landed for every wavefront, and every wavefront is done
+    // with step gs - 1's buffer, which the next copy reuses
     __syncthreads();
-    if (gs + 1 < nsteps) issue((gs + 1) / nk, (gs + 1) % nk, buf ^ 1);
-    const uint8_t* at = &lds_a[buf][0];
-    const uint8_t* bt = &lds_b[buf][0];
+    if (iss < nsteps) issue_next();
+    const uint8_t* at = lds_a[gs % S];
+    const uint8_t* bt = lds_b[gs % S];
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
       bf16x8 af[TM], bfr[TN];
@@ -831,7 +900,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
     }
     if (kt == nk - 1) {
       int m0, c0;
-      tile_origin(i, m0, c0);
+      tile_origin(cur, m0, c0);
       store_tile(m0, c0);
 #pragma unroll
       for (int a = 0; a < TM; ++a)
@@ -839,6 +908,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
         for (int b = 0; b < TN; ++b)
 #pragma unroll
           for (int q = 0; q < 16; ++q) acc[a][b][q] = 0.f;
+      ++cur;
     }
   }
 }
@@ -1019,7 +1089,8 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
       // K steps of 64 through two LDS buffers (measured at the config-5
       // shapes against steps of 32 through 2, 3 or 4 buffers: equal for the
       // 256 x 256 tiles, 28.6 vs 33.6-36.4 us for the 128 x 128 ones)
-      constexpr int BK_ = 64;
+      constexpr int BK_ = WM_ * WN_ == 8 ? PA_GEMM_BIG_BK : PA_GEMM_SMALL_BK;
+      constexpr int S_ = WM_ * WN_ == 8 ? PA_GEMM_BIG_S : PA_GEMM_SMALL_S;
       constexpr int WPC = WM_ * WN_ == 8 ? 1 : 2;  // workgroups per CU (LDS)
       static_assert(WPC == 1 || WPC == 2, "");
       constexpr int BM_ = 32 * WM_ * TM_, BN_ = 32 * WN_ * TN_;
@@ -1035,13 +1106,13 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
       const dim3 grid(8 * (WPC == 1 ? std::max(1, std::min(per_xcd, gemm_compute_units() / 8))
                                     : per_xcd));
       if (act == PA_ACT_SILU_MUL)
-        gemm_tiled_kernel<2, WM_, WN_, TM_, TN_, BK_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+        gemm_tiled_kernel<2, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
             o, xx, ww, nullptr, rows, out_features, in_features, 0, ntm, ntn);
       else if (bias)
-        gemm_tiled_kernel<1, WM_, WN_, TM_, TN_, BK_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+        gemm_tiled_kernel<1, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
             o, xx, ww, bb, rows, out_features, in_features, add, ntm, ntn);
       else
-        gemm_tiled_kernel<0, WM_, WN_, TM_, TN_, BK_><<<grid, 64 * WM_ * WN_, 0, s>>>(
+        gemm_tiled_kernel<0, WM_, WN_, TM_, TN_, BK_, S_><<<grid, 64 * WM_ * WN_, 0, s>>>(
             o, xx, ww, nullptr, rows, out_features, in_features, add, ntm, ntn);
       return PA_OK;
     };
