@@ -14,7 +14,7 @@ DEV = "cuda:0"
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("hidden", [896, 128, 100])
+@pytest.mark.parametrize("hidden", [896, 128, 100, 2048, 4096])
 def test_rms_norm(pa, dtype, hidden):
     g = torch.Generator(device=DEV).manual_seed(hidden)
     x = torch.randn(37, hidden, generator=g, device=DEV).to(dtype)

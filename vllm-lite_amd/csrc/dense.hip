@@ -44,6 +44,64 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(T* __restrict__ out, T* _
     Elem<T>::store(o + i, Elem<T>::load(x + i) * inv * Elem<T>::load(w + i));
 }
 
+// bf16 rows of hidden % 8 == 0, hidden <= 64 * 8 * kNormChunks: one wavefront
+// per row (4 rows per workgroup), the row held in registers as 16-byte
+// chunks (chunk i of lane l is chunk l + 64 i of the row), so x is read once
+// and written at most once; the sum of squares reduced by lane shuffles.
+// Same results as rms_norm_kernel up to the order of the f32 sum.
+constexpr int kNormChunks = 4;
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(uint16_t* __restrict__ out,
+                                                           uint16_t* __restrict__ res,
+                                                           const uint16_t* __restrict__ add,
+                                                           const uint16_t* __restrict__ w,
+                                                           int rows, int hidden, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = hidden / 8;
+  uint16_t* x = res + row * hidden;
+  const uint16_t* a = add ? add + row * hidden : nullptr;
+  bf16x8 v[kNormChunks], av[kNormChunks];
+#pragma unroll
+  for (int i = 0; i < kNormChunks; ++i) {
+    const int ch = lane + 64 * i;
+    if (ch < nch) {
+      v[i] = *reinterpret_cast<const bf16x8*>(x + 8 * ch);
+      if (a) av[i] = *reinterpret_cast<const bf16x8*>(a + 8 * ch);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormChunks; ++i) {
+    const int ch = lane + 64 * i;
+    if (ch < nch) {
+      if (a) {
+        // the residual is kept in the storage dtype, as the sum tensor would be
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = (__bf16)((float)v[i][e] + (float)av[i][e]);
+        *reinterpret_cast<bf16x8*>(x + 8 * ch) = v[i];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += (float)v[i][e] * (float)v[i][e];
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+  uint16_t* orow = out + row * hidden;
+#pragma unroll
+  for (int i = 0; i < kNormChunks; ++i) {
+    const int ch = lane + 64 * i;
+    if (ch < nch) {
+      const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + 8 * ch);
+      bf16x8 r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = (__bf16)((float)v[i][e] * inv * (float)wv[e]);
+      *reinterpret_cast<bf16x8*>(orow + 8 * ch) = r;
+    }
+  }
+}
+
 __device__ inline float block_sum(float v, float* red) {
   red[threadIdx.x] = v;
   __syncthreads();
@@ -918,6 +976,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_tiled_kernel(
 
 using namespace pa;
 
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 extern "C" int32_t pa_rms_norm(void* out, void* residual, const void* add, const void* weight,
                                int32_t rows, int32_t hidden, float eps, int32_t dtype,
                                pa_stream_t stream) {
@@ -927,7 +987,12 @@ extern "C" int32_t pa_rms_norm(void* out, void* residual, const void* add, const
   if (rows == 0) return PA_OK;
   PA_REQUIRE(out && residual && weight, PA_ERR_INVALID_ARG, "pa_rms_norm: null pointer");
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == PA_DTYPE_BF16)
+  if (dtype == PA_DTYPE_BF16 && hidden % 8 == 0 && hidden <= 64 * 8 * kNormChunks &&
+      aligned16(out) && aligned16(residual) && (!add || aligned16(add)) && aligned16(weight))
+    rms_norm_rows_kernel<<<(rows + 3) / 4, 256, 0, s>>>((uint16_t*)out, (uint16_t*)residual,
+                                                        (const uint16_t*)add,
+                                                        (const uint16_t*)weight, rows, hidden, eps);
+  else if (dtype == PA_DTYPE_BF16)
     rms_norm_kernel<uint16_t><<<rows, 256, 0, s>>>((uint16_t*)out, (uint16_t*)residual,
                                                    (const uint16_t*)add, (const uint16_t*)weight,
                                                    hidden, eps);

@@ -196,11 +196,18 @@ class Engine:
         for layer in range(c.layers):
             self._norm(x, w.ln1[layer], c.eps, add=add, out=h)
             wqkv, bqkv = w.wqkv[layer], w.bqkv[layer]
-            # the kernels take dense q rows
-            q = linear(h, wqkv[:nq], bqkv[:nq], packed("q", layer)).view(t, hq, d)
-            kv = linear(h, wqkv[nq:], bqkv[nq:], packed("kv", layer))
-            k = kv[:, :hkv * d].view(t, hkv, d)
-            v = kv[:, hkv * d:].view(t, hkv, d)
+            if skinny and packed("q", layer) is not None:
+                q = ops.linear(h, packed("q", layer), bqkv[:nq]).view(t, hq, d)
+                kv = ops.linear(h, packed("kv", layer), bqkv[nq:])
+                k = kv[:, :hkv * d].view(t, hkv, d)
+                v = kv[:, hkv * d:].view(t, hkv, d)
+            else:
+                # one projection for Q, K and V; attention takes strided
+                # views of its rows
+                qkv = ops.linear(h, wqkv, bqkv)
+                q = qkv[:, :nq].view(t, hq, d)
+                k = qkv[:, nq:nq + hkv * d].view(t, hkv, d)
+                v = qkv[:, nq + hkv * d:].view(t, hkv, d)
             attn = self.batch.attention(self.cache, layer, q, k, v, self.inv_freq, self.scale)
             o = linear(attn.view(t, nq), w.wo[layer], packed=packed("o", layer))
             self._norm(x, w.ln2[layer], c.eps, add=o, out=h)
