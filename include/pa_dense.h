@@ -80,10 +80,14 @@ enum { PA_LINEAR_RMS_IN = 1, PA_LINEAR_ADD_OUT = 2 };
  * tile, the last to finish summing the partial tiles in a fixed order (the
  * result does not depend on their timing).  Calls that may run at the same
  * time need distinct workspaces.  Without it one workgroup takes each tile.
- * Two kernels behind the one entry point:
+ * Three kernels behind the one entry point:
  *  - rows <= 64 (decode steps), packed or row-major weights: the skinny
  *    kernel, where the weights dominate the traffic (they are re-read once
  *    per 32 rows); K a multiple of 32, N of 16;
+ *  - rows <= 32, packed weights of at least 65,536 rows (the LM head), no
+ *    bias, activation or residual add, K <= 992: a persistent kernel that
+ *    holds X in LDS and streams the weight tiles over all CUs (the
+ *    workspace is not used);
  *  - rows > 64 (prompt chunks), or an N the skinny tiles do not divide, with
  *    row-major weights, no PA_LINEAR_RMS_IN and K a multiple of 64: a tiled
  *    GEMM on the matrix cores (128 x 128 output tiles, K staged through LDS

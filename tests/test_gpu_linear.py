@@ -70,6 +70,25 @@ def test_lm_head_shape(pa):
     close(out, x.float() @ w.float().T)
 
 
+@pytest.mark.parametrize("m,n,k", [(32, 151936, 896), (1, 65648, 896), (17, 65536, 128),
+                                   (32, 70000 // 16 * 16, 160), (9, 65600, 192),
+                                   (7, 66048, 992)])
+@pytest.mark.parametrize("rms", [False, True])
+def test_wide_projection_from_lds(pa, m, n, k, rms):
+    # packed weights of >= 4096 tiles with one batch tile: linear_wide_kernel
+    # (X in LDS, tiles dealt over a persistent grid; odd tile ranges, units of
+    # 7 / 4 / 1 K steps, the largest K it takes)
+    x, w, _ = operands(m, n, k, m + n + k)
+    gamma = None
+    if rms:
+        x = (x.float() * 3 + 0.5).to(torch.bfloat16)
+        g = torch.Generator(device=DEV).manual_seed(k + 1)
+        gamma = (1 + 0.2 * torch.randn(k, generator=g, device=DEV)).to(torch.bfloat16)
+    out = pa.linear(x, pa.ops.PackedWeight(w, col_scale=gamma), rms_eps=1e-6 if rms else None)
+    xr = rms_ref(x, gamma, 1e-6) if rms else x.float()
+    close(out, xr @ w.float().T)
+
+
 def test_linear_rejects_unsupported(pa):
     x, w, b = operands(4, 64, 96, 1)
     with pytest.raises(pa.PaError):

@@ -522,6 +522,184 @@ __global__ __launch_bounds__(NT == 1 && U == 4 ? 1024 : 512) void linear_skinny_
   }
 }
 
+// Wide projections of one batch tile (M <= 32 rows, N / 16 >= kWideMinTiles
+// weight tiles over packed weights: the LM head) with the batch rows held in
+// LDS.  A persistent grid of one WG-wavefront workgroup per CU: each
+// workgroup copies X [M, K] into LDS once (rows padded by 16 bytes so the 16
+// rows one operand read touches fall in distinct banks; rows past M zero),
+// with PA_LINEAR_RMS_IN forms 1 / rms of each row once, and then every
+// wavefront streams its own contiguous range of 16-row weight tiles from HBM
+// (two tiles at a time, each step's X fragments read from LDS once for both)
+// with the whole K per wavefront: no partial sums cross wavefronts.  The
+// weight stream runs in units of U K steps through NB register buffers,
+// across tile boundaries, so the next tile's first fragments are in flight
+// during a tile pair's epilogue.  Tiles are dealt evenly over the grid's
+// wavefronts, so every CU reads the same share of the weight.
+constexpr int kWideMinTiles = 4096;
+constexpr int kWideMaxK = 992;  // X in at most 64 KB of dynamic LDS
+template <int U, int NB, int WG>
+__global__ __launch_bounds__(64 * WG) void linear_wide_kernel(uint16_t* __restrict__ out,
+                                                         const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ w, int M,
+                                                         int N, int K, int flags, float eps) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs[];  // [32][2 K + 16] bytes, inv[32]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, j = lane >> 4;
+  const int nsteps = K / 32;
+  const int rowb = 2 * K + 16;
+  float* inv_s = reinterpret_cast<float*>(xs + 32 * rowb);
+
+  // this wavefront's tiles [t0, t1), in pairs (the last pair of an odd
+  // range repeats its tile and stores it once)
+  const int T = N / 16;
+  const int64_t gw = (int64_t)blockIdx.x * WG + wave, GW = (int64_t)gridDim.x * WG;
+  const int t0 = (int)(gw * T / GW), t1 = (int)((gw + 1) * T / GW);
+  const int npairs = (t1 - t0 + 1) / 2;
+  const int nu = nsteps / U;  // units per tile pair
+  const int total = npairs * nu;
+  const uint8_t* xr0 = xs + c * rowb + 16 * j;
+  const uint8_t* xr1 = xs + (16 + c) * rowb + 16 * j;
+
+  bf16x8 a0[U][2], a1[U][2];
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // U divides the K steps, so a unit's fragments of a tile are U
+  // consecutive KB of the packed weight.  Raw buffer loads over the tile
+  // (non-temporal: with the default policy the same launch after a write
+  // of 512 MB took 113 instead of 64 us, the weight's lines evicting dirty
+  // ones; only back-to-back launches whose weight stays partly in the MALL
+  // read faster with it): the lane's offset is one fixed register and the unit's
+  // a scalar, so no address registers are rewritten per unit (rewriting
+  // them made the compiler wait for loads in flight that had been given
+  // the same registers).
+  // X into LDS and 1 / rms of its rows, by the whole workgroup; called
+  // after the first weight units are in flight, so their latencies overlap
+  float inv[2];
+  auto stage_x = [&]() {
+    for (int e = threadIdx.x; e < 32 * (K / 8); e += 64 * WG) {
+      const int m = e / (K / 8), ch = e % (K / 8);
+      bf16x8 v = bf16x8{};
+      if (m < M) v = *reinterpret_cast<const bf16x8*>(x + (int64_t)m * K + 8 * ch);
+      *reinterpret_cast<bf16x8*>(xs + m * rowb + 16 * ch) = v;
+    }
+    __syncthreads();
+    if (threadIdx.x < 32 * 8) {
+      // eight lanes per row: sum of squares of the row's bf16 values
+      const int m = threadIdx.x >> 3, part = threadIdx.x & 7;
+      float ss = 0.f;
+      for (int ch = part; ch < K / 8; ch += 8) {
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(xs + m * rowb + 16 * ch);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += (float)v[e] * (float)v[e];
+      }
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      ss += __shfl_xor(ss, 4, 64);
+      if (part == 0)
+        inv_s[m] = (flags & PA_LINEAR_RMS_IN) ? 1.0f / sqrtf(ss / (float)K + eps) : 1.0f;
+    }
+    __syncthreads();
+    inv[0] = inv_s[c];
+    inv[1] = inv_s[16 + c];
+  };
+  const int voff = lane * 16;
+  const int tile_bytes = nsteps * 1024;
+  auto load = [&](int u, bf16x8 (&a)[U][2]) __attribute__((always_inline)) {
+    const int p = u / nu, st = u % nu;
+    const int ta = t0 + 2 * p, tb = min(ta + 1, t1 - 1);
+    const auto ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(w + (int64_t)ta * nsteps * 512), 0, tile_bytes, 0x00020000);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(w + (int64_t)tb * nsteps * 512), 0, tile_bytes, 0x00020000);
+#pragma unroll
+    for (int uu = 0; uu < U; ++uu) {
+      const int so = (st * U + uu) * 1024;
+      a[uu][0] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(ra, voff, so, 2));
+      a[uu][1] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rb, voff, so, 2));
+    }
+  };
+  auto mma = [&](int u, const bf16x8 (&a)[U][2]) __attribute__((always_inline)) {
+    const int p = u / nu, st = u % nu;
+    // the unit's X fragments first
+    bf16x8 b[U][2];
+#pragma unroll
+    for (int uu = 0; uu < U; ++uu) {
+      b[uu][0] = *reinterpret_cast<const bf16x8*>(xr0 + 64 * (st * U + uu));
+      b[uu][1] = *reinterpret_cast<const bf16x8*>(xr1 + 64 * (st * U + uu));
+    }
+#pragma unroll
+    for (int uu = 0; uu < U; ++uu)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[uu][t], b[uu][0], acc[t][0], 0, 0, 0);
+        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[uu][t], b[uu][1], acc[t][1], 0, 0, 0);
+      }
+    if (st == nu - 1) {
+      // the pair's epilogue: lane (c, j) holds weight rows 4 j .. 4 j + 3 of
+      // each tile for batch rows c and 16 + c
+      const int ta = t0 + 2 * p;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (ta + t < t1) {
+#pragma unroll
+          for (int bb = 0; bb < 2; ++bb) {
+            const int m = 16 * bb + c;
+            if (m < M) {
+              uint16_t o4[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) o4[r] = f32_to_bf16_bits(acc[t][bb][r] * inv[bb]);
+              *reinterpret_cast<uint64_t*>(out + (int64_t)m * N + (int64_t)(ta + t) * 16 + 4 * j) =
+                  *reinterpret_cast<const uint64_t*>(o4);
+            }
+          }
+        }
+        acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  // Loads are unconditional (past the last unit they repeat it and are not
+  // used), so the compiler's wait counts see one straight sequence: a load
+  // under a branch makes every later wait count for it as well.
+  // The scheduling barriers keep each unit's loads ahead of the previous
+  // unit's products (the scheduler would otherwise sink them between the
+  // products, after the waits for the previous unit's data).
+  if constexpr (NB == 2) {
+    if (total > 0) load(0, a0);
+    stage_x();
+    for (int u = 0; u < total; u += 2) {
+      load(min(u + 1, total - 1), a1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(u, a0);
+      if (u + 1 >= total) break;
+      load(min(u + 2, total - 1), a0);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(u + 1, a1);
+    }
+  } else {
+    bf16x8 a2[U][2];
+    if (total > 0) {
+      load(0, a0);
+      load(min(1, total - 1), a1);
+    }
+    stage_x();
+    for (int u = 0; u < total; u += 3) {
+      load(min(u + 2, total - 1), a2);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(u, a0);
+      if (u + 1 >= total) break;
+      load(min(u + 3, total - 1), a0);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(u + 1, a1);
+      if (u + 2 >= total) break;
+      load(min(u + 4, total - 1), a1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(u + 2, a2);
+    }
+  }
+}
+
 // Packs a row-major bf16 weight [N, K] (N a multiple of 16, K of 32) into the
 // MFMA-fragment order linear_skinny_kernel<., ., true> reads: fragment
 // (tile, step) = rows 16 tile .. +15, columns 32 step .. +31 is 1 KB at
@@ -1189,6 +1367,34 @@ extern "C" int32_t pa_linear(void* out, const void* x, const void* weight, const
     return check_launch("pa_linear");
   }
   PA_REQUIRE((rows + 31) / 32 <= 65535, PA_ERR_UNSUPPORTED, "pa_linear: %d rows", rows);
+  // A wide projection of one batch tile over packed weights (the LM head):
+  // the batch rows in LDS, a persistent grid of two workgroups per CU.
+  if (packed && rows <= 32 && act == PA_ACT_NONE && !bias && !(flags & PA_LINEAR_ADD_OUT) &&
+      out_features / 16 >= kWideMinTiles && in_features <= kWideMaxK) {
+    const size_t lds = 32 * (2 * (size_t)in_features + 16) + 32 * sizeof(float);
+    const int nsteps = in_features / 32;
+    // one 8-wavefront workgroup per CU (X staged once per CU); units of 7
+    // K steps (U divides the steps) through two register buffers, or of 4,
+    // 2 or 1 through three (the LM head back to back: 55-56 us; two
+    // 4-wavefront workgroups per CU 57-58 us; three buffers of 7 steps 58)
+    auto launch_wide = [&](auto uc, auto nbc) {
+      const int grid = std::min(gemm_compute_units(), (out_features / 16 + 7) / 8);
+      linear_wide_kernel<decltype(uc)::value, decltype(nbc)::value, 8>
+          <<<grid, 512, lds, (hipStream_t)stream>>>(
+          (uint16_t*)out, (const uint16_t*)x, (const uint16_t*)weight, rows, out_features,
+          in_features, flags, eps);
+    };
+    using std::integral_constant;
+    if (nsteps % 7 == 0)
+      launch_wide(integral_constant<int, 7>{}, integral_constant<int, 2>{});
+    else if (nsteps % 4 == 0)
+      launch_wide(integral_constant<int, 4>{}, integral_constant<int, 3>{});
+    else if (nsteps % 2 == 0)
+      launch_wide(integral_constant<int, 2>{}, integral_constant<int, 3>{});
+    else
+      launch_wide(integral_constant<int, 1>{}, integral_constant<int, 3>{});
+    return check_launch("pa_linear");
+  }
   // The split plan when the workspace holds it, else one workgroup per tile.
   LinearPlan plan = linear_plan(rows, out_features, in_features, act, true);
   const size_t ws_need = linear_ws_bytes(plan);
