@@ -460,3 +460,70 @@ def test_balanced_row_needing_plus_three_slots(pa, oracle):
         case[key] = np.concatenate([case[key], oracle.f32_to_bf16(pad)])
     got, _ = run_decode(pa, oracle, case, "bf16")
     assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, "plus-three slots")
+
+
+def _host_groups(ctx, tables, g_):
+    """The grouping decode_group_kernel forms, restated on the host: sequences
+    with at least one full 32-token unit, ordered by (first block id, batch
+    index), cut into runs of one first block and at most 16 / G members; a
+    group's shared units are the common table prefix in whole units, capped
+    by its shortest member."""
+    b = len(ctx)
+    none = 1 << 40
+    keys = sorted(((int(tables[s, 0]) if ctx[s] // 32 > 0 else none), s) for s in range(b))
+    groups, cur, prev = [], [], None
+    for hi, s in keys:
+        if cur and (hi == none or hi != prev or len(cur) == 16 // g_):
+            groups.append(cur)
+            cur = []
+        cur.append(s)
+        prev = hi
+    groups.append(cur)
+    out = {}
+    for grp in groups:
+        if len(grp) < 2:
+            continue
+        lim = min(int(ctx[s]) // 32 for s in grp)
+        rows = tables[grp][:, :2 * lim]
+        same = (rows == rows[0]).all(axis=0)
+        diff = int(np.argmin(same)) if not same.all() else 2 * lim
+        out[tuple(sorted(grp))] = min(lim, diff // 2)
+    return out
+
+
+@pytest.mark.parametrize("b", [1024, 1025])
+def test_balanced_group_capacity_edge(pa, oracle, b):
+    # The shared-prefix grouping handles up to 1024 sequences (one
+    # workgroup per possible group); 1025 run ungrouped.  Tables from 30
+    # prefix families (a random share of each family's 40 blocks, then
+    # blocks drawn with repetition from a pool whose first blocks also
+    # collide at random), contexts up to ~8300 so the balanced launch runs.
+    rng = np.random.default_rng(5000 + b)
+    hq, hkv, d = 2, 1, 64
+    ctx = rng.integers(1, 3000, b).astype(np.int32)
+    ctx[rng.choice(b, 6, replace=False)] = rng.integers(8200, 8400, 6)
+    mbs = int((ctx.max() + 15) // 16)
+    fam = rng.permutation(1200).astype(np.int32).reshape(30, 40)
+    bt = rng.integers(1200, 3200, (b, mbs)).astype(np.int32)
+    for s_ in range(b):
+        if rng.random() < 0.6:
+            n = int(rng.integers(1, 41))
+            bt[s_, :n] = fam[rng.integers(0, 30), :n]
+        bt[s_, (ctx[s_] + 15) // 16:] = -1
+    q = oracle.f32_to_bf16(rng.standard_normal((b, hq, d), dtype=np.float32))
+    kc = oracle.f32_to_bf16(rng.standard_normal((3200, hkv, 16, d), dtype=np.float32))
+    vr = oracle.f32_to_bf16(rng.standard_normal((3200, hkv, 16, d), dtype=np.float32))
+    case = {"q": q, "k_cache": kc, "v_cache_ref": vr, "block_tables": bt, "ctx": ctx,
+            "num_blocks": 3200}
+    max_ctx = int(ctx.max())
+    print(f"group capacity edge: B {b}, max ctx {max_ctx}", flush=True)
+    ws = torch.zeros(pa.decode_workspace_size(b, hq, d, max_ctx), dtype=torch.uint8, device=DEV)
+    out = pa.decode(to_dev(q), to_dev(kc), to_dev(oracle.v_from_ref(vr)), to_dev(bt),
+                    to_dev(ctx), max_ctx, workspace=ws)
+    got = oracle.bf16_to_f32(to_np(out))
+    assert_close(got, ref_f32(oracle, case), BF16_ATOL, BF16_RTOL, f"group capacity B {b}")
+    if b <= 1024:
+        groups, lcp = _balanced_groups(ws, b, hq, d, max_ctx)
+        dev = {tuple(g): int(l) for g, l in zip(groups, lcp) if len(g) > 1}
+        host = _host_groups(ctx, bt, hq // hkv)
+        assert len(host) > 30 and dev == host
