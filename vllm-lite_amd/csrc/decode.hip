@@ -43,9 +43,9 @@ __device__ inline float shfl_xor_f(float x, int mask) { return __shfl_xor(x, mas
 // K/V of a block that only this sequence reads are streamed once per decode
 // step: non-temporal loads (the `nt` cache policy) keep them from
 // displacing reusable lines and stream faster (measured ~6.8 TB/s vs
-// ~6.1 TB/s for plain 16-byte loads on MI355X).  A block that a neighbouring
-// sequence's table holds at the same index (a shared prefix) is read with
-// the default policy, so the other sequences find it in the cache.
+// ~6.1 TB/s for plain 16-byte loads on MI355X).  Blocks that a neighbouring
+// sequence's table holds at the same index (a shared prefix) are read with
+// the default policy, so the other sequences find them in the cache.
 // The loads are raw buffer loads over one (block, head) slice, whose cache
 // policy is an instruction operand (a select between a plain and a
 // non-temporal pointer load would be merged into a plain load).
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     uint64_t va[DT], vb[DT];
     int lim0, lim1;
   };
-  auto load_step = [&](int ib, Step& st) {
+  auto load_step = [&](auto policy, int ib, Step& st) {
     // Block ids for this step; ids outside the pool read block 0 and are masked.
     int32_t b0 = btab[ib];
     const bool has1 = ib + 1 < nblk;
@@ -205,9 +205,6 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     st.lim1 = has1 ? (rem - kBlock < kBlock ? rem - kBlock : kBlock) : 0;
     if (b0 < 0 || b0 >= num_blocks) { b0 = 0; st.lim0 = 0; }
     if (b1 < 0 || b1 >= num_blocks) { b1 = 0; st.lim1 = 0; }
-    const int bi0 = tok0 / kBlock + ib;
-    const bool nt0 = private_block(block_tables, mbs, seq, gridDim.z, bi0, b0);
-    const bool nt1 = private_block(block_tables, mbs, seq, gridDim.z, bi0 + 1, b1);
     const auto rk0 = slice_rsrc(kc + ((int64_t)b0 * Hkv + kvh) * head_stride, SLICE);
     const auto rk1 = slice_rsrc(kc + ((int64_t)b1 * Hkv + kvh) * head_stride, SLICE);
     const auto rv0 = slice_rsrc(vc + ((int64_t)b0 * Hkv + kvh) * head_stride, SLICE);
@@ -221,8 +218,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) vx[dt] = bload8<P>(rv, voff + dt * 16 * kBlock * 2);
     };
-    if (nt0) load_block(Stream{}, rk0, rv0, st.ka, st.va); else load_block(Plain{}, rk0, rv0, st.ka, st.va);
-    if (nt1) load_block(Stream{}, rk1, rv1, st.kb, st.vb); else load_block(Plain{}, rk1, rv1, st.kb, st.vb);
+    load_block(policy, rk0, rv0, st.ka, st.va);
+    load_block(policy, rk1, rv1, st.kb, st.vb);
   };
   auto compute_step = [&](Step& st) {
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -292,15 +289,43 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
   };
 
-  Step sa, sb;
-  if (nblk > 0) load_step(0, sa);
-  for (int ib = 0; ib < nblk; ib += 4) {
-    if (ib + 2 < nblk) load_step(ib + 2, sb);
-    compute_step(sa);
-    if (ib + 2 >= nblk) break;
-    if (ib + 4 < nblk) load_step(ib + 4, sa);
-    compute_step(sb);
-  }
+  // The steady-state loop issues its loads unconditionally (both steps it
+  // loads exist) and with one cache policy, so the compiler's wait before a
+  // step's products counts only that step's loads.  (With the next step's
+  // load under a branch, or a branch between the two policies per block,
+  // it waited for every load in flight, vmcnt(0), the step just issued
+  // included.)  The last one or two steps run after the loop.
+  auto run = [&](auto policy) {
+    Step sa, sb;
+    if (nblk > 0) load_step(policy, 0, sa);
+    int ib = 0;
+    for (; ib + 4 < nblk; ib += 4) {
+      load_step(policy, ib + 2, sb);
+      __builtin_amdgcn_sched_barrier(0);  // the loads go out before the products
+      compute_step(sa);
+      load_step(policy, ib + 4, sa);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_step(sb);
+    }
+    if (ib < nblk) {
+      if (ib + 2 < nblk) {
+        load_step(policy, ib + 2, sb);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_step(sa);
+        compute_step(sb);
+      } else {
+        compute_step(sa);
+      }
+    }
+  };
+  // One policy per partition: the default (cached) one when its first block
+  // is one a neighbouring sequence's table holds at the same index (a shared
+  // prefix, whose blocks the other sequences then find in the cache), else
+  // non-temporal.
+  if (nblk > 0 && !private_block(block_tables, mbs, seq, gridDim.z, tok0 / kBlock, btab[0]))
+    run(Plain{});
+  else
+    run(Stream{});
 
   lsum += shfl_xor_f(lsum, 16);
   lsum += shfl_xor_f(lsum, 32);
@@ -1333,14 +1358,28 @@ __global__ __launch_bounds__(64) void decode_balanced_kernel(
 #pragma unroll
     for (int st = 0; st < KS; ++st) asm volatile("" ::"v"(qv[st]));
     if constexpr (D <= 128) {
+      // unconditional loads in the steady state and a scheduling barrier
+      // after each step's loads, as in decode_mfma_kernel
       Step sa, sb;
       if (nblk > 0) load_step(0, sa);
-      for (int ib = 0; ib < nblk; ib += 4) {
-        if (ib + 2 < nblk) load_step(ib + 2, sb);
+      int ib = 0;
+      for (; ib + 4 < nblk; ib += 4) {
+        load_step(ib + 2, sb);
+        __builtin_amdgcn_sched_barrier(0);
         compute(sa);
-        if (ib + 2 >= nblk) break;
-        if (ib + 4 < nblk) load_step(ib + 4, sa);
+        load_step(ib + 4, sa);
+        __builtin_amdgcn_sched_barrier(0);
         compute(sb);
+      }
+      if (ib < nblk) {
+        if (ib + 2 < nblk) {
+          load_step(ib + 2, sb);
+          __builtin_amdgcn_sched_barrier(0);
+          compute(sa);
+          compute(sb);
+        } else {
+          compute(sa);
+        }
       }
     } else {
       // D = 256: two steps do not fit the register file; one at a time
