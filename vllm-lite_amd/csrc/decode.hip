@@ -558,7 +558,10 @@ __device__ __attribute__((noinline)) typename Fp8Partition<D>::State fp8_exact_p
 // a wavefront that read a flagged block takes the exact pass.  (Measured on
 // the config-2 shape: 85.5 us against 88.9 us with the per-code test; with
 // the test gone, two to four steps in flight at two or three wavefronts per
-// SIMD, 512- or 1024-token partitions: 89.7-94.6 us.)
+// SIMD, 512- or 1024-token partitions: 89.7-94.6 us; again with every load
+// of the steady state unconditional and a scheduling barrier after each
+// step's loads, so that each wait counted only its own step: 87.5-92.5
+// against 86.7-87.0 us, partitions of 512-2048 tokens.)
 template <int D, int NW, bool FLAGGED>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 4 : 1))) void decode_fp8_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ q, const uint8_t* __restrict__ kc,
