@@ -558,9 +558,92 @@ def run_e2e(pa, args):
                      "kernel": "one decode step (weights + KV)", "bytes_per_step": step_bytes,
                      "decode_step_ms": round(decode_step * 1e3, 3),
                      "prefill_ms": round(t["prefill_s"] * 1e3, 2)},
-        "cpu_baseline": None,
+        "cpu_baseline": None if args.no_cpu else cpu_baseline_e2e(cfg, w, lens, max_new),
     }
     print(json.dumps(line), flush=True)
+
+
+def cpu_baseline_e2e(cfg, w, lens, max_new, budget_s=12.0):
+    """Config 5's decode step on the host: the reference's CPU forward
+    restated (crates/model/src/causal_lm/model/mod.rs:143-164, decoder block
+    crates/model/src/components/decoder_block/mod.rs:157-198) in f32 over the
+    same weights, batched over the 32 requests (one matmul per projection
+    instead of the reference's per-sequence loop, which only makes the CPU
+    figure stronger): RMSNorm, QKV projection + bias, RoPE, the new token's
+    K / V into a paged f32 cache, attention through the C oracle (gather,
+    expand_kv, dense softmax, OpenMP), O projection, RMSNorm, SwiGLU MLP,
+    final norm and the tied LM head, greedy argmax.  Contexts are the
+    mid-generation ones (prompt + max_new / 2); every layer attends the same
+    seeded K / V pool (the timing does not depend on the values).  Reported
+    as output tokens/s of decode steps."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    f = lambda t: t.detach().float().cpu()
+    L, hq, hkv, d, hid = cfg.layers, cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.hidden
+    W = {"embed": f(w.embed), "norm": f(w.norm),
+         "ln1": [f(x) for x in w.ln1], "ln2": [f(x) for x in w.ln2],
+         "wqkv": [f(x) for x in w.wqkv], "bqkv": [f(x) for x in w.bqkv],
+         "wo": [f(x) for x in w.wo], "wgu": [f(x) for x in w.wgu], "wd": [f(x) for x in w.wd]}
+    b = len(lens)
+    ctx = np.array([n + max_new // 2 for n in lens], np.int32)
+    nblk = (ctx + 16) // 16 + 1
+    pool = int(nblk.sum())
+    rng = np.random.default_rng(6)
+    kc = rng.standard_normal((pool, hkv, 16, d), dtype=np.float32)
+    vc = rng.standard_normal((pool, hkv, 16, d), dtype=np.float32)
+    bt = np.zeros((b, int(nblk.max())), np.int32)
+    o = 0
+    for i in range(b):
+        bt[i, :nblk[i]] = np.arange(o, o + nblk[i])
+        o += nblk[i]
+    inv_freq = oracle.rope_inv_freq(d, cfg.rope_theta)
+    silu = torch.nn.functional.silu
+
+    def rms(x, g):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.eps) * g
+
+    def rope(x):  # [b, h, d] at each sequence's position (the oracle's RoPE)
+        return oracle.rope(x.contiguous().numpy(), ctx, inv_freq)
+
+    slot_blk = bt[np.arange(b), ctx // 16]
+    slot_off = ctx % 16
+
+    def step(tok):
+        x = W["embed"][tok]
+        for l in range(L):
+            h = rms(x, W["ln1"][l])
+            qkv = h @ W["wqkv"][l].T + W["bqkv"][l]
+            q = rope(qkv[:, :hq * d].view(b, hq, d))
+            k = rope(qkv[:, hq * d:(hq + hkv) * d].view(b, hkv, d))
+            v = qkv[:, (hq + hkv) * d:].view(b, hkv, d)
+            kc[slot_blk, :, slot_off, :] = k
+            vc[slot_blk, :, slot_off, :] = v.numpy()
+            a = oracle.paged_attention(q, kc, vc, bt, np.arange(b + 1), ctx, threads=threads)
+            x = x + torch.from_numpy(a).view(b, hq * d) @ W["wo"][l].T
+            h = rms(x, W["ln2"][l])
+            gu = h @ W["wgu"][l].T
+            act = silu(gu[:, :cfg.inter]) * gu[:, cfg.inter:]
+            x = x + act @ W["wd"][l].T
+        return (rms(x, W["norm"]) @ W["embed"].T).argmax(-1)
+
+    tok = torch.zeros(b, dtype=torch.int64)
+    tok = step(tok)  # warm
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        tok = step(tok)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 20:
+            break
+    return {"value": round(b * reps / el, 2), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{reps} decode steps of the 32 requests at mid-generation contexts "
+                      f"({el:.1f} s): f32 batched forward over the same weights, attention "
+                      "through the oracle (gather + expand_kv + dense softmax, OpenMP)"}
 
 
 def copy_calibration(args):
