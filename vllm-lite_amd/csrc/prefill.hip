@@ -29,6 +29,16 @@ constexpr float kNegBig = -1.0e30f;
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float shfl_xor_f(float x, int mask) { return __shfl_xor(x, mask, 64); }
+// Max of three as one v_max3_f32.  fmaxf on values the compiler cannot prove
+// canonical gets a quieting v_max_f32 x, x per operand first; MFMA results
+// need none (their NaNs are quiet), and the IEEE-mode instruction returns the
+// same value fmaxf does for them.  (Measured on the tiled prefill: the eight
+// quieting instructions a step cost 1.1%.)
+__device__ inline float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 
 // A sequence's query rows and past length as the kernels use them.  The
 // offsets are device data: they are clamped to the rows the call owns
@@ -691,9 +701,9 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       bool need = false;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const float t0 = fmaxf(fmaxf(S[nt][0][0], S[nt][0][1]), S[nt][0][2]);
-        const float t1 = fmaxf(fmaxf(S[nt][0][3], S[nt][1][0]), S[nt][1][1]);
-        lm[nt] = fmaxf(fmaxf(t0, t1), fmaxf(S[nt][1][2], S[nt][1][3]));
+        const float t0 = max3_raw(S[nt][0][0], S[nt][0][1], S[nt][0][2]);
+        const float t1 = max3_raw(S[nt][0][3], S[nt][1][0], S[nt][1][1]);
+        lm[nt] = max3_raw(t0, t1, max3_raw(S[nt][1][2], S[nt][1][3], S[nt][1][3]));
         need |= lm[nt] > 8.0f;
       }
       // Rows keep a stale max until one of their scores exceeds it by 2^8;
