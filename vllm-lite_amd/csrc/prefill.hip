@@ -370,7 +370,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
   bf16x8 qv[NT][KS];
   f32x4 o[NT][DT];
   f32x4 lacc[NT];  // softmax denominators, accumulated on the matrix core
-  float m[NT];
+  float nm[NT];  // minus the rows' running maxima (the Sᵀ accumulators start at it)
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int row = r0 + 16 * nt + c;
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
         qv[nt][s] = bf16x8{};
       }
     }
-    m[nt] = 0.f;
+    nm[nt] = 0.f;
     lacc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[nt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -719,7 +719,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
           bm = fmaxf(bm, shfl_xor_f(bm, 32));
           // a row with every key of the first step masked keeps m = 0
           const float delta = first ? (bm > -INFINITY ? bm : 0.f) : fmaxf(bm, 0.f);
-          m[nt] += delta;
+          nm[nt] -= delta;
 #pragma unroll
           for (int i = 0; i < 8; ++i) S[nt][i >> 2][i & 3] -= delta;
           if (!first) {
@@ -747,7 +747,7 @@ __global__ __launch_bounds__(64 * (16 / NT)) void prefill_tiled_kernel(
       for (int g = 0; g < NQK; ++g) {
         const int s_ = g / (2 * NT), q_ = g % (2 * NT), nt_ = q_ / 2, kk = q_ % 2;
         Snext[nt_][kk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            ka[kk][s_], qv[nt_][s_], s_ == 0 ? f32x4{-m[nt_], -m[nt_], -m[nt_], -m[nt_]}
+            ka[kk][s_], qv[nt_][s_], s_ == 0 ? f32x4{nm[nt_], nm[nt_], nm[nt_], nm[nt_]}
                                              : Snext[nt_][kk],
             0, 0, 0);
 #pragma unroll
