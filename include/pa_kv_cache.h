@@ -169,6 +169,19 @@ int32_t pa_batch_num_tokens(const pa_batch* batch);
 int32_t pa_batch_set_capacity(pa_batch* batch, int32_t max_context_len);
 /* 1 when every sequence is a single-token decode step. */
 int32_t pa_batch_is_decode(const pa_batch* batch);
+/* Advances a prepared decode batch by one token on the device: what
+ * pa_batch_prepare with the same block tables and every num_computed one
+ * higher would upload (positions, slots, context lengths), computed by one
+ * small kernel from the arrays already on the device, with no host upload.
+ * No counterpart in the reference (its decode step rebuilds the positions on
+ * the host, crates/model/src/components/attention/rope_gqa.rs:385-429): it
+ * is for callers that replay a captured decode step, which then advances
+ * itself.  Checked at the call against the host's copy of the batch (every
+ * sequence's table must hold the advanced context); a replay of a captured
+ * call is not checked again, so the caller sizes the tables for every step
+ * it replays (as the block tables of a whole generation are allocated up
+ * front).  Errors: not a decode batch, a table too short. */
+int32_t pa_batch_advance(pa_batch* batch, pa_stream_t stream);
 
 /* The prepared batch's fused QKV projection of one layer with RoPE and the
  * KV-cache write in its epilogue: pa_linear_rope_cache with the batch's

@@ -174,3 +174,102 @@ def test_decode_workspace_growth_refused_under_capture(pa):
         assert torch.equal(captured, eager)
     batch.close()
     cache.close()
+
+
+def _advance_case(pa, rng, seqs_ctx, d=64, nb=64):
+    hq, hkv = 8, 2
+    caches = []
+    k0 = torch.from_numpy(rng.standard_normal((nb, hkv, 16, d), dtype=np.float32))
+    for _ in range(2):
+        c = pa.PagedKvCache(1, hkv, d, nb, torch.bfloat16, DEV)
+        c.key_cache(0).copy_(k0.to(torch.bfloat16).to(DEV))
+        c.value_cache(0).copy_(k0.transpose(-1, -2).to(torch.bfloat16).to(DEV) * 0.5)
+        caches.append(c)
+    pool = list(rng.permutation(nb))
+    tables = [[int(pool.pop()) for _ in range((n + 8 + 15) // 16)] for n in seqs_ctx]
+    return caches, tables, hq, hkv
+
+
+def test_advance_equals_prepare(pa):
+    # pa_batch_advance from a prepared decode step gives the same positions,
+    # slots and context lengths as preparing the next step on the host:
+    # attention (with RoPE and the KV write) and the caches agree bit for bit
+    # over several steps, across block boundaries
+    rng = np.random.default_rng(21)
+    ctx = [15, 30, 47, 1]  # first decode tokens at positions 15, 30, 47, 1
+    (ca, cb), tables, hq, hkv = _advance_case(pa, rng, ctx)
+    d = 64
+    inv = torch.from_numpy(np.ascontiguousarray(
+        1e4 ** (-np.arange(0, d, 2, dtype=np.float32) / d))).to(DEV)
+    adv, ref = pa.StepBatch(), pa.StepBatch()
+    adv.prepare(ca, [1] * 4, ctx, tables)
+    for step in range(8):
+        if step:
+            adv.advance(ca)
+        ref.prepare(cb, [1] * 4, [n + step for n in ctx], tables)
+        assert adv.is_decode() and adv.num_tokens() == 4
+        q = torch.randn(4, hq, d, device=DEV).to(torch.bfloat16)
+        k = torch.randn(4, hkv, d, device=DEV).to(torch.bfloat16)
+        v = torch.randn(4, hkv, d, device=DEV).to(torch.bfloat16)
+        oa = adv.attention(ca, 0, q.clone(), k, v, inv)
+        ob = ref.attention(cb, 0, q.clone(), k, v, inv)
+        assert torch.equal(oa, ob), f"step {step}"
+    assert torch.equal(ca.key_cache(0), cb.key_cache(0))
+    assert torch.equal(ca.value_cache(0), cb.value_cache(0))
+    adv.close()
+    ref.close()
+
+
+def test_advance_rejects(pa):
+    rng = np.random.default_rng(3)
+    (c, _), tables, hq, hkv = _advance_case(pa, rng, [20, 5])
+    b = pa.StepBatch()
+    b.prepare(c, [5, 1], [0, 5], tables)  # a prefill chunk: not a decode step
+    with pytest.raises(pa.PaError, match="not a prepared decode step"):
+        b.advance(c)
+    # the first table holds 2 blocks (32 tokens), the second 1 (16)
+    b.prepare(c, [1, 1], [30, 5], [tables[0], tables[1]])
+    b.advance(c)  # 32 tokens: the last slot of the first table
+    with pytest.raises(pa.PaError, match="table holds"):
+        b.advance(c)
+    b.close()
+
+
+def test_captured_advance_replays_match_prepared_steps(pa):
+    # a captured [advance + attention] step, replayed with eager work and
+    # synchronisations between the replays, equals the host-prepared steps
+    rng = np.random.default_rng(8)
+    ctx = [14, 33, 3]
+    (ca, cb), tables, hq, hkv = _advance_case(pa, rng, ctx)
+    d = 64
+    adv, ref = pa.StepBatch(), pa.StepBatch()
+    cap = 16 * max(len(t) for t in tables)  # the widest table's tokens
+    adv.set_capacity(cap)
+    ref.set_capacity(cap)
+    qs = [torch.randn(3, hq, d, device=DEV).to(torch.bfloat16) for _ in range(6)]
+    ks = [torch.randn(3, hkv, d, device=DEV).to(torch.bfloat16) for _ in range(6)]
+    # step 0 eager on both (also sizes the decode workspace)
+    adv.prepare(ca, [1] * 3, ctx, tables)
+    ref.prepare(cb, [1] * 3, ctx, tables)
+    assert torch.equal(adv.attention(ca, 0, qs[0], ks[0], ks[0]),
+                       ref.attention(cb, 0, qs[0], ks[0], ks[0]))
+    torch.cuda.synchronize()
+    q_in = torch.empty_like(qs[0])
+    k_in = torch.empty_like(ks[0])
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        adv.advance(ca)
+        out = adv.attention(ca, 0, q_in, k_in, k_in)
+    for step in range(1, 6):
+        q_in.copy_(qs[step])
+        k_in.copy_(ks[step])
+        g.replay()
+        torch.cuda.synchronize()
+        ref.prepare(cb, [1] * 3, [n + step for n in ctx], tables)
+        want = ref.attention(cb, 0, qs[step], ks[step], ks[step])
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {step}"
+    assert torch.equal(ca.key_cache(0), cb.key_cache(0))
+    adv.close()
+    ref.close()

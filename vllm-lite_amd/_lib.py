@@ -74,6 +74,7 @@ SIGNATURES = {
     "pa_batch_num_tokens": (_i32, [_p]),
     "pa_batch_set_capacity": (_i32, [_p, _i32]),
     "pa_batch_is_decode": (_i32, [_p]),
+    "pa_batch_advance": (_i32, [_p, _p]),
     "pa_batch_qkv_rope_cache": (_i32, [_p, _p, _i32, _i32, _p, _p, _p, _p, _i32, _i32, _f32,
                                        _p, _p]),
     "pa_batch_attention": (_i32, [_p, _p, _i32, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _f32,

@@ -63,6 +63,9 @@ struct pa_batch {
   int num_seqs = 0, num_tokens = 0, max_blocks = 0, max_q = 0, max_ctx = 0, num_blocks = 0;
   int capacity = 0;  // fixed max context for decode launches (0 = per step)
   bool decode = false;
+  // host copies for pa_batch_advance's checks: per sequence the context
+  // length and the tokens its block table holds
+  std::vector<int32_t> host_ctx, host_cap;
   // device arrays: the index arrays are regions of one buffer (one upload
   // per prepare), at offsets that only change when a region must grow
   DevBuf index_buf, workspace;
@@ -238,6 +241,9 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
   }
   b->pending[sl] = true;
   b->slot = sl ^ 1;
+  b->host_ctx.assign(ctxl.begin(), ctxl.end());
+  b->host_cap.resize(num_seqs);
+  for (int s2 = 0; s2 < num_seqs; ++s2) b->host_cap[s2] = block_counts[s2] * pa::kBlock;
   b->num_seqs = num_seqs;
   b->num_tokens = T;
   b->max_blocks = max_blocks;
@@ -246,6 +252,43 @@ extern "C" int32_t pa_batch_prepare(pa_batch* b, int32_t num_seqs, const int32_t
   b->num_blocks = num_blocks;
   b->decode = decode;
   return PA_OK;
+}
+
+namespace {
+// One decode token per sequence: the next position, its slot in the
+// sequence's (already uploaded) block table, the context one longer.
+__global__ __launch_bounds__(256) void batch_advance_kernel(int64_t* __restrict__ pos,
+                                                            int64_t* __restrict__ slots,
+                                                            const int32_t* __restrict__ tables,
+                                                            int32_t* __restrict__ ctx_lens,
+                                                            int max_blocks, int num_seqs) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= num_seqs) return;
+  const int64_t p = pos[s] + 1;
+  const int64_t bi = p / pa::kBlock;
+  // a table too short (a replay the caller did not size for) writes nowhere
+  const int32_t blk = bi < max_blocks ? tables[(int64_t)s * max_blocks + bi] : -1;
+  pos[s] = p;
+  slots[s] = blk < 0 ? -1 : (int64_t)blk * pa::kBlock + p % pa::kBlock;
+  ctx_lens[s] = (int32_t)(p + 1);
+}
+}  // namespace
+
+extern "C" int32_t pa_batch_advance(pa_batch* b, pa_stream_t stream) {
+  pa::clear_error();
+  PA_REQUIRE(b, PA_ERR_INVALID_ARG, "pa_batch_advance: null batch");
+  PA_REQUIRE(b->decode && b->num_seqs > 0, PA_ERR_INVALID_ARG,
+             "pa_batch_advance: the batch is not a prepared decode step");
+  for (int s = 0; s < b->num_seqs; ++s)
+    PA_REQUIRE(b->host_ctx[s] + 1 <= b->host_cap[s], PA_ERR_OUT_OF_BOUNDS,
+               "pa_batch_advance: sequence %d needs %d tokens, its table holds %d", s,
+               b->host_ctx[s] + 1, b->host_cap[s]);
+  for (int s = 0; s < b->num_seqs; ++s) ++b->host_ctx[s];
+  ++b->max_ctx;
+  batch_advance_kernel<<<(b->num_seqs + 255) / 256, 256, 0, (hipStream_t)stream>>>(
+      (int64_t*)b->positions.ptr, (int64_t*)b->slots.ptr, (const int32_t*)b->tables.ptr,
+      (int32_t*)b->ctx_lens.ptr, b->max_blocks, b->num_seqs);
+  return pa::check_launch("pa_batch_advance");
 }
 
 extern "C" int32_t pa_batch_attention(pa_batch* b, pa_kv_cache* cache, int32_t layer,

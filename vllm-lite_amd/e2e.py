@@ -24,7 +24,9 @@ weights packed with the norm weights folded in (Weights.pack()), a decode step
 runs the fused layer of Engine._forward_fused: five launches per layer (the
 QKV projection with RoPE and the KV write in its epilogue, attention, O, gate|up
 + SwiGLU, and the down projection split over K by pa_linear's workspace), the
-residual adds in the O and down epilogues.
+residual adds in the O and down epilogues.  Decode steps after the first are
+one replay each of a captured step that advances the batch by a token on the
+device (pa_batch_advance; the block tables hold the whole generation).
 The norm is chosen explicitly by ModelConfig.norm: "rms" (RMSNorm, what the
 benchmark configuration states) or "layer" (the zero-bias LayerNorm the
 reference's CausalLm constructs for these models,
@@ -285,24 +287,35 @@ class Engine:
             t1 = time.perf_counter()
             rows = None  # decode steps: one token per sequence, every row's logits
             self.batch.set_capacity(max(lens) + max_new if self.graph else 0)
-            graph = static_tok = static_out = None
+            graph = None
+            hist = None  # graph path: generated ids [max_new, B], written by the replays
             for step in range(1, max_new):
-                self.batch.prepare(self.cache, [1] * b, [n + step - 1 for n in lens], blocks)
                 if not self.graph or step == 1:
                     # eager (also the warm-up of every launch the graph records)
+                    self.batch.prepare(self.cache, [1] * b, [n + step - 1 for n in lens],
+                                       blocks)
                     nxt = self.next_tokens(nxt, rows)
-                else:
-                    if graph is None:
-                        static_tok = nxt.clone()
-                        graph = torch.cuda.CUDAGraph()
-                        with torch.cuda.graph(graph):
-                            static_out = self.next_tokens(static_tok, rows)
-                    else:
-                        static_tok.copy_(nxt)
-                    graph.replay()
-                    nxt = static_out.clone()
-                out.append(nxt)
-            gen = torch.stack(out, 1).cpu()
+                    out.append(nxt)
+                    continue
+                if graph is None:
+                    # The captured step advances the batch by one token on
+                    # the device (the tables hold every block of the
+                    # generation), feeds its tokens to the next replay and
+                    # stores them in row `row` of hist: a replay is the whole
+                    # step, with no host work between replays.
+                    hist = torch.empty(max_new, b, dtype=torch.int64, device=self.device)
+                    hist[:step] = torch.stack(out, 0)
+                    row = torch.full((1,), step, dtype=torch.int64, device=self.device)
+                    static_tok = nxt.clone()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        self.batch.advance(self.cache)
+                        static_out = self.next_tokens(static_tok, rows)
+                        static_tok.copy_(static_out)
+                        hist.index_copy_(0, row, static_out[None])
+                        row.add_(1)
+                graph.replay()
+            gen = (hist.t() if hist is not None else torch.stack(out, 1)).cpu()
             t2 = time.perf_counter()
         finally:
             self.batch.set_capacity(0)

@@ -239,6 +239,12 @@ class StepBatch:
     def num_tokens(self):
         return self._lib.pa_batch_num_tokens(self._h)
 
+    def advance(self, cache):
+        """pa_batch_advance: the prepared decode step moved one token on,
+        on the device (no upload), on the cache's stream; capturable, so a
+        captured decode step can advance itself on every replay."""
+        _check("pa_batch_advance", self._lib.pa_batch_advance(self._h, cache._stream()))
+
     def set_capacity(self, max_context_len):
         """pa_batch_set_capacity: shape decode launches for a fixed maximum
         context so a captured step can be replayed (0 = per step)."""
