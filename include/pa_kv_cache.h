@@ -180,7 +180,10 @@ int32_t pa_batch_is_decode(const pa_batch* batch);
  * sequence's table must hold the advanced context); a replay of a captured
  * call is not checked again, so the caller sizes the tables for every step
  * it replays (as the block tables of a whole generation are allocated up
- * front).  Errors: not a decode batch, a table too short. */
+ * front), and sets a capacity (pa_batch_set_capacity) that covers the
+ * context of every replay: the captured decode launches keep the shape of
+ * the capture.  Errors: not a decode batch, a table too short, a capture
+ * without a capacity. */
 int32_t pa_batch_advance(pa_batch* batch, pa_stream_t stream);
 
 /* The prepared batch's fused QKV projection of one layer with RoPE and the

@@ -273,3 +273,18 @@ def test_captured_advance_replays_match_prepared_steps(pa):
     assert torch.equal(ca.key_cache(0), cb.key_cache(0))
     adv.close()
     ref.close()
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_captured_advance_needs_capacity(pa):
+    rng = np.random.default_rng(4)
+    (c, _), tables, hq, hkv = _advance_case(pa, rng, [10, 20])
+    b = pa.StepBatch()
+    b.prepare(c, [1, 1], [10, 20], tables)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(pa.PaError, match="capacity"):
+        with torch.cuda.graph(g, stream=torch.cuda.Stream()):
+            b.advance(c)
+    torch.cuda.synchronize()
+    b.close()

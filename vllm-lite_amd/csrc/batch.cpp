@@ -283,6 +283,14 @@ extern "C" int32_t pa_batch_advance(pa_batch* b, pa_stream_t stream) {
     PA_REQUIRE(b->host_ctx[s] + 1 <= b->host_cap[s], PA_ERR_OUT_OF_BOUNDS,
                "pa_batch_advance: sequence %d needs %d tokens, its table holds %d", s,
                b->host_ctx[s] + 1, b->host_cap[s]);
+  // A captured advance replays without this check, and the captured decode
+  // launches keep the shape of the capture: only a capacity (the shape of
+  // every replay) makes them cover the contexts of later replays.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  PA_REQUIRE(hipStreamIsCapturing((hipStream_t)stream, &cap) == hipSuccess &&
+                 (cap == hipStreamCaptureStatusNone || b->capacity > 0),
+             PA_ERR_INVALID_ARG,
+             "pa_batch_advance: capturing without a capacity (pa_batch_set_capacity)");
   for (int s = 0; s < b->num_seqs; ++s) ++b->host_ctx[s];
   ++b->max_ctx;
   batch_advance_kernel<<<(b->num_seqs + 255) / 256, 256, 0, (hipStream_t)stream>>>(
